@@ -1,0 +1,305 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-KV speculative verify step on one MI355X.
+
+Workload (Qwen2.5-1.5B-shaped single-layer verify, gamma = 5): batch 32, 12 q /
+2 kv heads, head_dim 128, block 16, bf16 KV; context lengths U[256, 4096]; block
+tables are a random permutation of a 65,536-block pool; the rest of the pool is
+the free list. One step =
+
+  1. append the 6 verify tokens of every sequence (device allocation + copy),
+  2. verify attention of the 6 rows x 12 heads over the paged context,
+  3. fused rejection sampling of the round over a 151,936-entry vocabulary
+     (target logits N(0, 2^2), draft = target + N(0, 1), T = 1, caller noise),
+  4. rewind of the pool to start + n_commit with the sampled lengths.
+
+All inputs are resident in HBM before timing; the step runs as one captured HIP
+graph. The headline ``value`` is the verify-attention HBM bandwidth (algorithmic
+bytes / measured time of the attention call); ``spec_step_us_per_seq`` is the
+whole step per sequence. ``cpu_baseline`` times the CPU oracle (the reference's
+gather + repeat_interleave + masked SDPA per sequence) on the host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "speculative-decoding-lab_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "verify-attn HBM GB/s (% of peak) + spec-step us/seq, gamma=5, 1 GPU"
+
+B, HQ, HKV, D, BS, GAMMA, CAP, VOCAB = 32, 12, 2, 128, 16, 5, 65536, 151936
+C = GAMMA + 1
+
+
+def attention_bytes(lens):
+    """Algorithmic HBM bytes of one verify-attention call (one layer)."""
+    total = 0
+    for L in lens:
+        n = L + C
+        total += n * 2 * HKV * D * 2          # K and V of every attended key (bf16)
+        total += 2 * C * HQ * D * 2           # q read + out write (bf16)
+        total += 4 * math.ceil(n / BS) + 8    # block-table entries + start / id
+    return total
+
+
+def sample_bytes(batch):
+    """Algorithmic bytes of one fused sampling call (T > 0)."""
+    return batch * ((C + GAMMA) * VOCAB * 4 + VOCAB * 4 + GAMMA * 8 + 12)
+
+
+def build_workload(dev, seed=0):
+    import torch
+
+    from engine.kv import PagedKVCache
+
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(256, 4097, (B,), generator=g).tolist()
+    perm = torch.randperm(CAP, generator=g).tolist()
+    tables, pos = [], 0
+    for L in lens:
+        n = -(-L // BS)
+        tables.append(perm[pos: pos + n])
+        pos += n
+    free = perm[pos:]
+    kv = PagedKVCache(1, HKV, D, CAP, BS, dev, torch.bfloat16, max_seqs=B,
+                      max_blocks_per_seq=-(-(4096 + C) // BS) + 1)
+    kv.load_state(tables, lens, free)
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    keys, values = [], []
+    for s, L in enumerate(lens):
+        k = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
+        kv.write_block(0, [s], [0], k, v)
+        keys.append(k[0])
+        values.append(v[0])
+    w = {
+        "lens": lens,
+        "kv": kv,
+        "keys": keys,
+        "values": values,
+        "q": torch.randn(B, C, HQ, D, generator=gd, device=dev).to(torch.bfloat16),
+        "k_new": torch.randn(B, C, HKV, D, generator=gd, device=dev).to(torch.bfloat16),
+        "v_new": torch.randn(B, C, HKV, D, generator=gd, device=dev).to(torch.bfloat16),
+        "sid": torch.arange(B, dtype=torch.int32, device=dev),
+        "start": torch.tensor(lens, dtype=torch.int32, device=dev),
+    }
+    target = torch.randn(B, C, VOCAB, generator=gd, device=dev) * 2.0
+    draft = target[:, :GAMMA] + torch.randn(B, GAMMA, VOCAB, generator=gd, device=dev)
+    probs_q = torch.softmax(draft, dim=-1)
+    w["target"] = target.contiguous()
+    w["draft"] = draft.contiguous()
+    w["proposals"] = torch.multinomial(probs_q.reshape(-1, VOCAB), 1, generator=gd).reshape(B, GAMMA).to(torch.int32)
+    w["u"] = torch.rand(B, GAMMA, generator=gd, device=dev)
+    w["noise"] = torch.empty(B, VOCAB, device=dev).exponential_(1, generator=gd)
+    w["attn_out"] = torch.empty_like(w["q"])
+    return w
+
+
+def make_step(w):
+    from engine.attention import verify_attention
+    from engine.spec_scheduler import _new_result, verify_sample
+
+    kv = w["kv"]
+    max_ctx = max(w["lens"]) + C
+    res = _new_result(B, GAMMA, kv.device)
+
+    def append():
+        kv.write_block_device(0, w["sid"], w["start"], w["k_new"], w["v_new"])
+
+    def attend():
+        verify_attention(w["q"], kv, 0, w["sid"], w["start"], max_ctx, out=w["attn_out"])
+
+    def sample():
+        verify_sample(w["target"], w["draft"], w["proposals"], w["u"], w["noise"], 1.0,
+                      start_pos=w["start"], result=res, validate=False)
+
+    def rewind():
+        kv.rewind_device(w["sid"], res.new_len, res.finished)
+
+    def step():
+        append()
+        attend()
+        sample()
+        rewind()
+
+    return step, {"append": append, "attend": attend, "sample": sample, "rewind": rewind}, res
+
+
+def graph_of(fn, reps, torch):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, iters, torch):
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters  # ms per replay
+
+
+def cpu_baseline(w, budget_s=12.0):
+    """The oracle's paged extend attention (gather per block, GQA expand, masked
+    SDPA per sequence) on the host, in GB/s of the same algorithmic bytes."""
+    import torch
+
+    from oracle import attention as ref_attn
+    from oracle import kv_pool as ref
+
+    n_seq = 8
+    lens = w["lens"][:n_seq]
+    cap = sum(-(-(L + C) // BS) for L in lens)
+    cpu = ref.PagedKVCache(1, HKV, D, cap, BS, dtype=torch.float32)
+    k_new = w["k_new"][:n_seq].float().cpu()
+    v_new = w["v_new"][:n_seq].float().cpu()
+    for s, L in enumerate(lens):
+        cpu.add_sequence(s)
+        cpu.write_block(0, [s], [0], w["keys"][s].float().cpu().unsqueeze(0),
+                        w["values"][s].float().cpu().unsqueeze(0))
+    cpu.write_block(0, list(range(n_seq)), lens, k_new, v_new)
+    q = w["q"][:n_seq].float().cpu()
+    nbytes = attention_bytes(lens)
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    ref_attn.paged_attention_extend(q, cpu, 0, list(range(n_seq)), lens, HQ)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end and len(times) < 20:
+        t0 = time.perf_counter()
+        ref_attn.paged_attention_extend(q, cpu, 0, list(range(n_seq)), lens, HQ)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": "oracle paged_attention_extend (per-block gather, repeat_interleave, masked SDPA "
+                  "per sequence, fp32) on the first {} of the 32 sequences, 1 layer, median of {} runs "
+                  "({:.1f} ms each)".format(n_seq, len(times), med * 1e3),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(--gpus {} requested)".format(args.gpus), file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    print("bench: building workload", file=sys.stderr, flush=True)
+    w = build_workload(dev, args.seed)
+    step, parts, res = make_step(w)
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    print("bench: warm-up done, capturing", file=sys.stderr, flush=True)
+
+    # Timed region: K whole steps, one graph replay each.
+    g_step = graph_of(step, 1, torch)
+    for _ in range(args.warmup):
+        g_step.replay()
+    torch.cuda.synchronize()
+    ms_per_step = time_graph(g_step, args.steps, torch)
+
+    # Per-part timings (graphs of 20 back-to-back calls, outside the timed region).
+    reps = 20
+    part_us = {}
+    for name in ("attend", "sample"):
+        gpart = graph_of(parts[name], reps, torch)
+        part_us[name] = time_graph(gpart, 5, torch) * 1000.0 / reps
+    g_ar = graph_of(lambda: (parts["append"](), parts["rewind"]()), reps, torch)
+    part_us["append_rewind"] = time_graph(g_ar, 5, torch) * 1000.0 / reps
+    torch.cuda.synchronize()
+    print("bench: timings done", file=sys.stderr, flush=True)
+
+    lens = w["lens"]
+    attn_bytes = attention_bytes(lens)
+    attn_gbs = attn_bytes / (part_us["attend"] * 1e-6) / 1e9
+    samp_gbs = sample_bytes(B) / (part_us["sample"] * 1e-6) / 1e9
+    accept = res.accept_len.float().mean().item()
+
+    line = {
+        "metric": METRIC,
+        "value": round(attn_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2.5-1.5B-shaped paged verify step: batch 32, gamma 5 (6 rows), "
+                        "12q/2kv heads, head_dim 128, block 16, ctx U[256,4096], 65536-block pool, "
+                        "1 layer; fused sampling over V=151936 fp32 at T=1",
+            "global_batch": B,
+            "seq_len": int(sum(lens) / len(lens)),
+            "parallelism": "single-gpu",
+        },
+        "pct_of_peak": round(100.0 * attn_gbs / HBM_PEAK_GBS, 2),
+        "spec_step_us_per_seq": round(ms_per_step * 1000.0 / B, 3),
+        "parts_us": {k: round(v, 2) for k, v in part_us.items()},
+        "sample_gbs": round(samp_gbs, 1),
+        "attn_bytes_per_call": attn_bytes,
+        "mean_accepted_drafts": round(accept, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(attn_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        print("bench: cpu baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,207 @@
+/*
+ * specverify.h -- C ABI of the gfx950 paged-KV speculative-verify library
+ * (libspecverify.so).
+ *
+ * Every pointer argument is a DEVICE pointer unless stated otherwise. The
+ * library allocates nothing: pools, tables, counters, outputs and workspaces
+ * belong to the caller. All work is enqueued on `stream` (a hipStream_t, NULL =
+ * the default stream) and the functions return without synchronising.
+ * Return value: SPV_OK (0) or a negative SPV_ERR_* code for invalid arguments
+ * or a failed launch; nothing is enqueued when an argument check fails.
+ * Thread-compatible: one caller per stream; calls on one pool must be ordered.
+ *
+ * Data layout in HBM (fixed by this library):
+ *   K pool  [num_layers][capacity][num_kv_heads][block_size][head_dim]
+ *   V pool  [num_layers][capacity][num_kv_heads][head_dim][block_size]
+ *   block_tables [max_seqs][max_blocks_per_seq] int32, num_blocks[max_seqs],
+ *   seq_lens[max_seqs], free_stack[capacity] (bottom..top), free_flag[capacity]
+ *   (1 = on the free list), ctr[SPV_CTR_WORDS] (ctr[0] = free count).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   engine/kv.py, engine/attention.py, engine/spec_scheduler.py,
+ *   specdec/sampler.py -- cited per entry point below.
+ */
+#ifndef SPECVERIFY_H
+#define SPECVERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPV_OK 0
+#define SPV_ERR_ARG (-1)
+#define SPV_ERR_LAUNCH (-2)
+#define SPV_ERR_WORKSPACE (-3)
+#define SPV_ERR_UNSUPPORTED (-4)
+
+#define SPV_CTR_WORDS 8
+
+/* element types */
+#define SPV_F32 0
+#define SPV_BF16 1
+#define SPV_F16 2
+#define SPV_FP8E4M3 3
+
+/* Library version string (host pointer). */
+const char* spv_version(void);
+
+/* ------------------------------------------------------------------ pool */
+
+/* BlockAllocator.__init__ free list [0..cap-1] (engine/kv.py:48-55) and
+ * PagedKVCache.reset of the free list (engine/kv.py:173-183). */
+int spv_pool_init(int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                  int32_t capacity, void* stream);
+
+/* BlockAllocator.alloc (engine/kv.py:61-70): pops the stack top. The id (or -1
+ * when the pool is exhausted) is written to *out_block (device int32). */
+int spv_pool_alloc_one(int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                       int32_t capacity, int32_t* out_block, void* stream);
+
+/* BlockAllocator.free (engine/kv.py:72-76): pushes `block` unless it is already
+ * free; *out_pushed (device int32) receives 1 if pushed, 0 if ignored. */
+int spv_pool_free_one(int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                      int32_t capacity, int32_t block, int32_t* out_pushed,
+                      void* stream);
+
+/* PagedKVCache.write (engine/kv.py:119-147) for a whole verify/extend block,
+ * i.e. the loop `for b in batch: for j < C: write(layer, sid_b, start_b + j)`
+ * of engine/model.py:184-187 in one launch. k_new/v_new are (B, C, Hkv, d) in
+ * kv_dtype (fp8 not accepted here). With may_alloc != 0 the missing blocks are
+ * first popped in batch order, each sequence's in logical order (one
+ * workgroup, exclusive scan). On exhaustion the sequences before the failing
+ * one get all their blocks, the failing one gets what is left, and ctr[1] is
+ * set to 1 + its batch index. `write_limit_b` (the failing batch index, or B)
+ * restricts the token writes exactly as the reference's raise would: sequences
+ * after it write nothing, and it writes only tokens whose block exists.
+ * write_limit_b = -1 (with may_alloc) takes that index from ctr[1] as set by
+ * this call's allocation, so a caller need not know it in advance.
+ * seq_lens[sid] = max(seq_lens[sid], last written position + 1). seq_ids must
+ * be distinct within one call. k_new = v_new = NULL allocates only
+ * (PagedKVCache._ensure_blocks_up_to, kv.py:119-122): no copy, no length change. */
+int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype,
+                  const void* k_new, const void* v_new,
+                  int32_t* block_tables, int32_t max_blocks_per_seq,
+                  int32_t* num_blocks, int32_t* seq_lens,
+                  int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                  const int32_t* seq_ids, const int32_t* start_pos,
+                  int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                  int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                  int32_t may_alloc, int32_t write_limit_b, void* stream);
+
+/* Rewind of a spec round (engine/spec_scheduler.py:302-307, 320-322) built
+ * from PagedKVCache.truncate (engine/kv.py:150-162) and .clear (kv.py:164-171),
+ * applied per entry in order: if new_len[i] >= 0 (and, with shrink_only, only
+ * when seq_lens > new_len) truncate -- free the table tail tail-first, set
+ * seq_len = max(0, new_len); then if finished[i] != 0 clear -- free the rest in
+ * forward order, seq_len = 0. new_len/finished may be NULL (= -1 / 0). One
+ * workgroup; pushes are placed by an exclusive scan in entry order; a block
+ * already free is detected and the whole call then replays sequentially with
+ * the reference's ignore-if-free rule. ctr[3] = blocks pushed. seq_ids must be
+ * distinct within one call. Also serves PagedKVCache.reset (kv.py:173-183):
+ * every sequence, new_len NULL, finished = 1. */
+int spv_kv_rewind(int32_t* block_tables, int32_t max_blocks_per_seq,
+                  int32_t* num_blocks, int32_t* seq_lens,
+                  int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                  const int32_t* seq_ids, const int32_t* new_len,
+                  const int32_t* finished, int32_t n, int32_t capacity,
+                  int32_t block_size, int32_t shrink_only, void* stream);
+
+/* gather_ctx (engine/attention.py:41-63): out = (2, length, Hkv, d) in kv_dtype
+ * (fp8 pools are dequantised to fp32 with kv_scales, see spv_verify_attn). */
+int spv_kv_gather(const void* k_pool, const void* v_pool, int kv_dtype,
+                  const float* kv_scales, const int32_t* block_tables,
+                  int32_t max_blocks_per_seq, int32_t seq_id, int32_t length,
+                  int32_t layer, int32_t capacity, int32_t block_size,
+                  int32_t num_kv_heads, int32_t head_dim, void* out, void* stream);
+
+/* PagedKVCache.key_map / value_map (engine/kv.py:208-213): out = (n, bs, Hkv, d)
+ * in kv_dtype for the physical ids phys[0..n) of `layer`. */
+int spv_kv_read_blocks(const void* pool, int is_value, int kv_dtype,
+                       const int32_t* phys, int32_t n, int32_t layer,
+                       int32_t capacity, int32_t block_size,
+                       int32_t num_kv_heads, int32_t head_dim, void* out,
+                       void* stream);
+
+/* ------------------------------------------------------------- attention */
+
+/* Workspace needed by spv_verify_attn for contexts up to max_ctx tokens. */
+size_t spv_verify_attn_workspace_bytes(int32_t B, int32_t C, int32_t num_q_heads,
+                                       int32_t num_kv_heads, int32_t head_dim,
+                                       int32_t block_size, int32_t max_ctx);
+
+/* paged_attention_extend (engine/attention.py:170-216): for sequence b, row j,
+ * q head h: out = softmax(scale * q . K[0..start_b+j]) V[0..start_b+j] using kv
+ * head h / (Hq/Hkv) (attention.py:32-38). q/out are (B, C, Hq, d) in q_dtype
+ * (f32/bf16/f16); the pool holds kv_dtype. For SPV_FP8E4M3 pools kv_scales is
+ * [layers][capacity][2] fp32 (K, V scale of each block). max_ctx must be >=
+ * start_b + C for every b. bf16 pools with head_dim 128 (or 64), block_size 16
+ * and (Hq/Hkv)*C >= 16 take the MFMA path; everything else the VALU path. */
+int spv_verify_attn(void* out, const void* q, int q_dtype,
+                    const void* k_pool, const void* v_pool, int kv_dtype,
+                    const float* kv_scales, const int32_t* block_tables,
+                    int32_t max_blocks_per_seq, const int32_t* seq_ids,
+                    const int32_t* start_pos, int32_t B, int32_t C,
+                    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                    int32_t block_size, int32_t layer, int32_t capacity,
+                    int32_t max_ctx, float scale, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* -------------------------------------------------------------- sampling */
+
+/* Workspace needed by spv_verify_sample. */
+size_t spv_verify_sample_workspace_bytes(int32_t B, int32_t gamma, int32_t V);
+
+/* One fused verify-sampling step: logits_to_probs (specdec/sampler.py:19-36)
+ * on every row, then batch_accept (engine/spec_scheduler.py:46-88) with
+ * acceptance_probability (specdec/sampler.py:86-92), residual_distribution
+ * (specdec/sampler.py:72-83) and sample_token (specdec/sampler.py:59-69) drawn
+ * as argmax(probs / E), then the commit cut of engine/spec_scheduler.py:274-303.
+ *   target (B, gamma+1, V) fp32, draft (B, gamma, V) fp32: logits, or already
+ *     probabilities when is_probs != 0 (batch_accept's own inputs);
+ *   temperature <= 0 -> greedy one-hot rows, else softmax(z / max(T, 1e-12));
+ *   proposals (B, gamma) int32; u_accept (B, gamma) fp32 uniforms: position j
+ *     is accepted iff (double)u < acceptance probability; exp_noise (B, V) fp32
+ *     Exp(1) variates for the one race per sequence (read only when sampling;
+ *     must be finite and > 0);
+ *   start_pos / remaining (B) int32 or NULL, eos_id (-1 = none): commit cut.
+ * Outputs (device, may be NULL except accept_len/out_tokens):
+ *   accept_len[B] drafts accepted, out_tokens[B][gamma+1] (-1 padded),
+ *   n_commit[B], finished[B] (budget or eos; 1 also when n_commit == 0),
+ *   new_len[B] = start + n_commit, or -1 when n_commit == 0 (no truncate),
+ *   accept_prob[B][gamma] float64 acceptance probabilities.
+ * decide_only != 0 stops after accept_prob (no noise read, no outputs). */
+int spv_verify_sample(const float* target, const float* draft, int is_probs,
+                      float temperature, const int32_t* proposals,
+                      const float* u_accept, const float* exp_noise,
+                      const int32_t* start_pos, const int32_t* remaining,
+                      int32_t eos_id, int32_t B, int32_t gamma, int32_t V,
+                      int32_t* accept_len, int32_t* out_tokens,
+                      int32_t* n_commit, int32_t* finished, int32_t* new_len,
+                      double* accept_prob, int32_t decide_only,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* logits_to_probs (specdec/sampler.py:19-36) on `rows` rows of V fp32 logits. */
+int spv_logits_to_probs(const float* logits, float* probs, int32_t rows, int32_t V,
+                        float temperature, void* stream);
+
+/* residual_distribution (specdec/sampler.py:72-83) of one row pair. */
+int spv_residual(const float* p, const float* q, float* out, int32_t V,
+                 void* stream);
+
+/* sample_token (specdec/sampler.py:59-69) given its Exp(1) row:
+ * *out_index = argmax(probs / noise), lowest index on ties, NaN wins. */
+int spv_race_argmax(const float* probs, const float* noise, int32_t V,
+                    int32_t* out_index, void* stream);
+
+/* acceptance_probability (specdec/sampler.py:86-92): *out = a (float64). */
+int spv_accept_prob(const float* p, const float* q, int32_t token_id, double* out,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPECVERIFY_H */

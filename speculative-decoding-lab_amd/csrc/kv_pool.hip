@@ -1,0 +1,510 @@
+// Paged KV pool on the device: LIFO free stack, block tables, append and rewind.
+//
+// The reference keeps the pool as Python lists (engine/kv.py:45-183): a free list
+// popped at its tail, per-sequence block tables grown lazily in logical order,
+// truncate that frees the table tail tail-first and clear that frees in forward
+// order. Here the same state lives in HBM and each batched operation is one
+// launch: allocation/rewind are single-workgroup kernels (an exclusive scan over
+// the batch fixes every sequence's slice of the stack, so the resulting stack
+// order is exactly the order the sequential list operations would produce) and
+// the K/V copy of an append is a separate many-workgroup kernel.
+#include "spv_common.h"
+
+using namespace spv;
+
+namespace {
+
+constexpr int kPoolThreads = 1024;
+
+__global__ void pool_init_kernel(int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+                                 int32_t* __restrict__ ctr, int32_t cap) {
+  const int stride = gridDim.x * blockDim.x;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < cap; i += stride) {
+    free_stack[i] = i;
+    free_flag[i] = 1;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < SPV_CTR_WORDS) ctr[threadIdx.x] = threadIdx.x == CTR_TOP ? cap : 0;
+}
+
+__global__ void alloc_one_kernel(int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+                                 int32_t* __restrict__ ctr, int32_t* __restrict__ out) {
+  const int top = ctr[CTR_TOP];
+  int id = -1;
+  if (top > 0) {
+    id = free_stack[top - 1];
+    ctr[CTR_TOP] = top - 1;
+    free_flag[id] = 0;
+  }
+  ctr[CTR_POPPED] = id;
+  *out = id;
+}
+
+__global__ void free_one_kernel(int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+                                int32_t* __restrict__ ctr, int32_t block, int32_t* __restrict__ out) {
+  int pushed = 0;
+  if (free_flag[block] == 0) {
+    const int top = ctr[CTR_TOP];
+    free_stack[top] = block;
+    ctr[CTR_TOP] = top + 1;
+    free_flag[block] = 1;
+    pushed = 1;
+  }
+  ctr[CTR_PUSHED] = pushed;
+  *out = pushed;
+}
+
+// Lazy allocation for one extend block (kv.py:119-122 applied to every write of
+// model.py:184-187). Sequence b needs blocks up to (start_b + C - 1) / bs; the
+// missing ones are popped from the stack top, sequence by sequence in batch
+// order and in logical order within a sequence.
+__global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
+    int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+    const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
+    const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, int32_t B, int32_t C,
+    int32_t bs) {
+  __shared__ int s_scan[kPoolThreads / 64];
+  __shared__ int s_top, s_fail;
+  if (threadIdx.x == 0) {
+    s_top = ctr[CTR_TOP];
+    s_fail = B;
+  }
+  __syncthreads();
+  const int top = s_top;
+  int consumed = 0;
+  for (int base = 0; base < B; base += blockDim.x) {
+    const int b = base + threadIdx.x;
+    int need = 0, sid = 0, nb = 0;
+    if (b < B) {
+      sid = seq_ids[b];
+      nb = nblocks[sid];
+      const int last_blk = (start[b] + C - 1) / bs;
+      need = max(0, last_blk + 1 - nb);
+    }
+    int total;
+    const int off = block_exclusive_scan(need, s_scan, &total);
+    const int avail = top - consumed;
+    const int got = min(need, max(0, avail - off));
+    if (b < B && got < need) atomicMin(&s_fail, b);
+    for (int i = 0; i < got; ++i) {
+      const int id = free_stack[top - 1 - (consumed + off + i)];
+      tables[(size_t)sid * maxb + nb + i] = id;
+      free_flag[id] = 0;
+    }
+    if (b < B && got > 0) nblocks[sid] = nb + got;
+    consumed += min(total, max(avail, 0));
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    ctr[CTR_TOP] = top - consumed;
+    ctr[CTR_EXHAUSTED] = s_fail < B ? s_fail + 1 : 0;
+  }
+}
+
+// Copy of one token's K row (Hkv x d, contiguous per head) and V column
+// (transposed page: element (h, e) at ((h * d) + e) * bs + offset).
+template <int ES>
+__global__ __launch_bounds__(64) void kv_write_kernel(
+    uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool, const uint8_t* __restrict__ knew,
+    const uint8_t* __restrict__ vnew, const int32_t* __restrict__ tables, int32_t maxb,
+    const int32_t* __restrict__ nblocks, int32_t* __restrict__ seq_lens,
+    const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, const int32_t* __restrict__ ctr,
+    int32_t C, int32_t layer, int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t limit_b) {
+  const int b = blockIdx.x / C, j = blockIdx.x % C;
+  // limit_b < 0: the allocation of this call recorded the failing sequence in ctr.
+  if (limit_b < 0) {
+    const int ex = ctr[CTR_EXHAUSTED];
+    limit_b = ex ? ex - 1 : C * gridDim.x;
+  }
+  if (b > limit_b) return;
+  const int sid = seq_ids[b];
+  const int s0 = start[b];
+  const int pos = s0 + j;
+  const int blk = pos / bs, off = pos - blk * bs;
+  const int nb = nblocks[sid];
+  if (blk >= nb) return;  // only possible for the failing sequence of an exhausted pool
+  const int phys = tables[(size_t)sid * maxb + blk];
+  if ((unsigned)phys >= (unsigned)cap) return;  // never write outside the pool
+  const size_t page = ((size_t)layer * cap + phys) * hkv;  // first (block, head) slot
+  const size_t row_elems = (size_t)hkv * d;
+  const uint8_t* ksrc = knew + ((size_t)b * C + j) * row_elems * ES;
+  const uint8_t* vsrc = vnew + ((size_t)b * C + j) * row_elems * ES;
+  const int row_bytes = d * ES;
+  if ((row_bytes & 15) == 0) {
+    const int vec_per_head = row_bytes >> 4;
+    for (int t = threadIdx.x; t < hkv * vec_per_head; t += blockDim.x) {
+      const int h = t / vec_per_head, c = t - h * vec_per_head;
+      uint8_t* dst = kpool + ((page + h) * bs + off) * (size_t)row_bytes;
+      reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(ksrc + (size_t)h * row_bytes)[c];
+    }
+  } else {
+    for (int t = threadIdx.x; t < hkv * row_bytes; t += blockDim.x) {
+      const int h = t / row_bytes, c = t - h * row_bytes;
+      kpool[((page + h) * bs + off) * (size_t)row_bytes + c] = ksrc[(size_t)h * row_bytes + c];
+    }
+  }
+  for (int t = threadIdx.x; t < hkv * d; t += blockDim.x) {
+    const int h = t / d, e = t - h * d;
+    uint8_t* dst = vpool + (((page + h) * d + e) * bs + off) * ES;
+    const uint8_t* src = vsrc + (size_t)t * ES;
+    if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
+    else if constexpr (ES == 2) *reinterpret_cast<uint16_t*>(dst) = *reinterpret_cast<const uint16_t*>(src);
+    else *dst = *src;
+  }
+  // The last token this call writes for the sequence extends its length.
+  if (threadIdx.x == 0) {
+    const int last_j = min(C - 1, nb * bs - 1 - s0);
+    if (j == last_j && seq_lens[sid] < pos + 1) seq_lens[sid] = pos + 1;
+  }
+}
+
+struct RewindEntry {
+  int sid, nb, ft, fc, nb_final, len_final;
+};
+
+__device__ __forceinline__ RewindEntry rewind_entry(int i, const int32_t* __restrict__ seq_ids,
+                                                    const int32_t* __restrict__ new_len,
+                                                    const int32_t* __restrict__ finished,
+                                                    const int32_t* __restrict__ nblocks,
+                                                    const int32_t* __restrict__ seq_lens, int bs,
+                                                    int shrink_only) {
+  RewindEntry e;
+  e.sid = seq_ids[i];
+  e.nb = nblocks[e.sid];
+  const int len = seq_lens[e.sid];
+  const int nl = new_len ? new_len[i] : -1;
+  const int fin = finished ? finished[i] : 0;
+  const bool trunc = nl >= 0 && (!shrink_only || len > nl);
+  int nb1 = e.nb, len1 = len;
+  e.ft = 0;
+  if (trunc) {
+    const int need = nl <= 0 ? 0 : (nl + bs - 1) / bs;
+    e.ft = max(0, e.nb - need);
+    nb1 = e.nb - e.ft;
+    len1 = max(0, nl);
+  }
+  e.fc = fin ? nb1 : 0;
+  e.nb_final = fin ? 0 : nb1;
+  e.len_final = fin ? 0 : len1;
+  return e;
+}
+
+// k-th block freed by an entry: the truncated tail first (tail-first, kv.py:160-161),
+// then, for a finished sequence, the rest in forward order (kv.py:167-168).
+__device__ __forceinline__ int rewind_block(const RewindEntry& e, int k, const int32_t* __restrict__ tables,
+                                            int maxb) {
+  const size_t row = (size_t)e.sid * maxb;
+  return k < e.ft ? tables[row + e.nb - 1 - k] : tables[row + (k - e.ft)];
+}
+
+__global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
+    const int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+    int32_t* __restrict__ seq_lens, int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+    int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ new_len,
+    const int32_t* __restrict__ finished, int32_t n, int32_t bs, int32_t shrink_only, int32_t cap) {
+  __shared__ int s_scan[kPoolThreads / 64];
+  __shared__ int s_top, s_dup;
+  if (threadIdx.x == 0) {
+    s_top = ctr[CTR_TOP];
+    s_dup = 0;
+  }
+  __syncthreads();
+  const int top = s_top;
+
+  // Phase A: mark every candidate "pending" (+2). A non-zero previous value means
+  // the block is already free or appears twice: the exact sequential path is needed.
+  for (int base = 0; base < n; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    if (i < n) {
+      const RewindEntry e = rewind_entry(i, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+      for (int k = 0; k < e.ft + e.fc; ++k) {
+        const int id = rewind_block(e, k, tables, maxb);
+        if ((unsigned)id >= (unsigned)cap) {
+          s_dup = 1;
+          continue;
+        }
+        if (atomicAdd(&free_flag[id], 2) != 0) s_dup = 1;
+      }
+    }
+  }
+  __syncthreads();
+  const bool dup = s_dup != 0;
+
+  if (!dup) {
+    // Phase B: place each entry's pushes at top + (exclusive prefix of counts).
+    int pushed = 0;
+    for (int base = 0; base < n; base += blockDim.x) {
+      const int i = base + threadIdx.x;
+      RewindEntry e{};
+      int cnt = 0;
+      if (i < n) {
+        e = rewind_entry(i, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+        cnt = e.ft + e.fc;
+      }
+      int total;
+      const int off = block_exclusive_scan(cnt, s_scan, &total);
+      for (int k = 0; k < cnt; ++k) {
+        const int id = rewind_block(e, k, tables, maxb);
+        free_stack[top + pushed + off + k] = id;
+        free_flag[id] = 1;
+      }
+      __syncthreads();  // every entry of this chunk has read nblocks/seq_lens
+      if (i < n) {
+        nblocks[e.sid] = e.nb_final;
+        seq_lens[e.sid] = e.len_final;
+      }
+      pushed += total;
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      ctr[CTR_TOP] = top + pushed;
+      ctr[CTR_PUSHED] = pushed;
+    }
+    return;
+  }
+
+  // Undo the marks, then replay sequentially with the reference's rule
+  // `if block in free_list: return` (kv.py:73-74).
+  for (int base = 0; base < n; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    if (i < n) {
+      const RewindEntry e = rewind_entry(i, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+      for (int k = 0; k < e.ft + e.fc; ++k) {
+        const int id = rewind_block(e, k, tables, maxb);
+        if ((unsigned)id < (unsigned)cap) atomicSub(&free_flag[id], 2);
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  int t = top, pushed = 0;
+  for (int i = 0; i < n; ++i) {
+    // Entries see the effects of earlier ones (distinct sids, so only the flags matter).
+    const RewindEntry e = rewind_entry(i, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+    for (int k = 0; k < e.ft + e.fc; ++k) {
+      const int id = rewind_block(e, k, tables, maxb);
+      if ((unsigned)id < (unsigned)cap && t < cap && atomicOr(&free_flag[id], 0) == 0) {
+        free_stack[t++] = id;
+        atomicExch(&free_flag[id], 1);
+        ++pushed;
+      }
+    }
+    nblocks[e.sid] = e.nb_final;
+    seq_lens[e.sid] = e.len_final;
+  }
+  ctr[CTR_TOP] = t;
+  ctr[CTR_PUSHED] = pushed;
+  ctr[CTR_SLOWPATH] += 1;
+}
+
+// gather_ctx: out[0][p][h][e] = K, out[1][p][h][e] = V for p < length.
+template <int DT, bool DEQ>
+__global__ void kv_gather_kernel(const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
+                                 const float* __restrict__ scales, const int32_t* __restrict__ table,
+                                 int32_t length, int32_t layer, int32_t cap, int32_t bs, int32_t hkv,
+                                 int32_t d, void* __restrict__ out) {
+  const size_t per_tok = (size_t)hkv * d;
+  const size_t total = (size_t)length * per_tok;
+  constexpr int ES = DT == SPV_F32 ? 4 : (DT == SPV_FP8E4M3 ? 1 : 2);
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const int p = (int)(idx / per_tok);
+    const int r = (int)(idx - (size_t)p * per_tok);
+    const int h = r / d, e = r - h * d;
+    const int blk = p / bs, off = p - blk * bs;
+    const int phys = table[blk];
+    const size_t slot = ((size_t)layer * cap + phys) * hkv + h;
+    const size_t ki = (slot * bs + off) * d + e;
+    const size_t vi = (slot * d + e) * bs + off;
+    if constexpr (DEQ) {
+      const float* sc = scales + ((size_t)layer * cap + phys) * 2;
+      static_cast<float*>(out)[idx] = load_elem<DT>(kpool, ki) * sc[0];
+      static_cast<float*>(out)[total + idx] = load_elem<DT>(vpool, vi) * sc[1];
+    } else {
+      uint8_t* o = static_cast<uint8_t*>(out);
+      for (int c = 0; c < ES; ++c) {
+        o[idx * ES + c] = kpool[ki * ES + c];
+        o[(total + idx) * ES + c] = vpool[vi * ES + c];
+      }
+    }
+  }
+}
+
+template <int ES>
+__global__ void kv_read_blocks_kernel(const uint8_t* __restrict__ pool, int is_value,
+                                      const int32_t* __restrict__ phys, int32_t n, int32_t layer,
+                                      int32_t cap, int32_t bs, int32_t hkv, int32_t d,
+                                      uint8_t* __restrict__ out) {
+  const size_t per_blk = (size_t)bs * hkv * d;
+  const size_t total = (size_t)n * per_blk;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const int i = (int)(idx / per_blk);
+    int r = (int)(idx - (size_t)i * per_blk);
+    const int t = r / (hkv * d);
+    r -= t * hkv * d;
+    const int h = r / d, e = r - h * d;
+    const size_t slot = ((size_t)layer * cap + phys[i]) * hkv + h;
+    const size_t src = is_value ? (slot * d + e) * bs + t : (slot * bs + t) * d + e;
+    for (int c = 0; c < ES; ++c) out[idx * ES + c] = pool[src * ES + c];
+  }
+}
+
+inline int grid_for(size_t work, int threads, int cap_blocks = 8192) {
+  size_t g = (work + threads - 1) / threads;
+  if (g < 1) g = 1;
+  if (g > (size_t)cap_blocks) g = cap_blocks;
+  return (int)g;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* spv_version(void) { return "specverify 0.1 gfx950"; }
+
+int spv_pool_init(int32_t* free_stack, int32_t* free_flag, int32_t* ctr, int32_t capacity, void* stream) {
+  if (!free_stack || !free_flag || !ctr || capacity < 1) return SPV_ERR_ARG;
+  hipLaunchKernelGGL(pool_init_kernel, dim3(grid_for(capacity, 256)), dim3(256), 0, (hipStream_t)stream,
+                     free_stack, free_flag, ctr, capacity);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_pool_alloc_one(int32_t* free_stack, int32_t* free_flag, int32_t* ctr, int32_t capacity,
+                       int32_t* out_block, void* stream) {
+  if (!free_stack || !free_flag || !ctr || !out_block || capacity < 1) return SPV_ERR_ARG;
+  hipLaunchKernelGGL(alloc_one_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, free_stack, free_flag, ctr,
+                     out_block);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_pool_free_one(int32_t* free_stack, int32_t* free_flag, int32_t* ctr, int32_t capacity, int32_t block,
+                      int32_t* out_pushed, void* stream) {
+  if (!free_stack || !free_flag || !ctr || !out_pushed || block < 0 || block >= capacity) return SPV_ERR_ARG;
+  hipLaunchKernelGGL(free_one_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, free_stack, free_flag, ctr,
+                     block, out_pushed);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, const void* v_new,
+                  int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
+                  int32_t* free_stack, int32_t* free_flag, int32_t* ctr, const int32_t* seq_ids,
+                  const int32_t* start_pos, int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                  int32_t block_size, int32_t num_kv_heads, int32_t head_dim, int32_t may_alloc,
+                  int32_t write_limit_b, void* stream) {
+  const int es = dtype_size(kv_dtype);
+  const bool alloc_only = !k_new && !v_new;
+  if (!k_pool || !v_pool || (!alloc_only && (!k_new || !v_new)) || !block_tables || !num_blocks || !seq_lens ||
+      !seq_ids || !start_pos || es == 0 || kv_dtype == SPV_FP8E4M3)
+    return SPV_ERR_ARG;
+  if (B < 0 || C < 1 || layer < 0 || capacity < 1 || block_size < 1 || num_kv_heads < 1 || head_dim < 1 ||
+      max_blocks_per_seq < 1 || write_limit_b < -1 || write_limit_b > B)
+    return SPV_ERR_ARG;
+  if (write_limit_b < 0 && (!may_alloc || !ctr)) return SPV_ERR_ARG;
+  if (B == 0) return SPV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (may_alloc) {
+    if (!free_stack || !free_flag || !ctr) return SPV_ERR_ARG;
+    hipLaunchKernelGGL(kv_alloc_kernel, dim3(1), dim3(kPoolThreads), 0, s, block_tables, max_blocks_per_seq,
+                       num_blocks, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, block_size);
+    SPV_CHECK_LAUNCH();
+  }
+  if (alloc_only) return SPV_OK;
+  const dim3 grid(B * C), blk(64);
+  auto* kp = static_cast<uint8_t*>(k_pool);
+  auto* vp = static_cast<uint8_t*>(v_pool);
+  auto* kn = static_cast<const uint8_t*>(k_new);
+  auto* vn = static_cast<const uint8_t*>(v_new);
+  if (es == 4)
+    hipLaunchKernelGGL(kv_write_kernel<4>, grid, blk, 0, s, kp, vp, kn, vn, block_tables, max_blocks_per_seq,
+                       num_blocks, seq_lens, seq_ids, start_pos, ctr, C, layer, capacity, block_size,
+                       num_kv_heads, head_dim, write_limit_b);
+  else
+    hipLaunchKernelGGL(kv_write_kernel<2>, grid, blk, 0, s, kp, vp, kn, vn, block_tables, max_blocks_per_seq,
+                       num_blocks, seq_lens, seq_ids, start_pos, ctr, C, layer, capacity, block_size,
+                       num_kv_heads, head_dim, write_limit_b);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_kv_rewind(int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
+                  int32_t* free_stack, int32_t* free_flag, int32_t* ctr, const int32_t* seq_ids,
+                  const int32_t* new_len, const int32_t* finished, int32_t n, int32_t capacity,
+                  int32_t block_size, int32_t shrink_only, void* stream) {
+  if (!block_tables || !num_blocks || !seq_lens || !free_stack || !free_flag || !ctr || !seq_ids || n < 0 ||
+      capacity < 1 || block_size < 1 || max_blocks_per_seq < 1)
+    return SPV_ERR_ARG;
+  if (n == 0) return SPV_OK;
+  hipLaunchKernelGGL(kv_rewind_kernel, dim3(1), dim3(kPoolThreads), 0, (hipStream_t)stream, block_tables,
+                     max_blocks_per_seq, num_blocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len,
+                     finished, n, block_size, shrink_only, capacity);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_kv_gather(const void* k_pool, const void* v_pool, int kv_dtype, const float* kv_scales,
+                  const int32_t* block_tables, int32_t max_blocks_per_seq, int32_t seq_id, int32_t length,
+                  int32_t layer, int32_t capacity, int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                  void* out, void* stream) {
+  if (!k_pool || !v_pool || !block_tables || !out || seq_id < 0 || length < 0 || layer < 0 || capacity < 1 ||
+      block_size < 1 || num_kv_heads < 1 || head_dim < 1 || dtype_size(kv_dtype) == 0)
+    return SPV_ERR_ARG;
+  if ((length + block_size - 1) / block_size > max_blocks_per_seq) return SPV_ERR_ARG;
+  if (kv_dtype == SPV_FP8E4M3 && !kv_scales) return SPV_ERR_ARG;
+  if (length == 0) return SPV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t work = (size_t)length * num_kv_heads * head_dim;
+  const dim3 grid(grid_for(work, 256)), blk(256);
+  const int32_t* table = block_tables + (size_t)seq_id * max_blocks_per_seq;
+  auto* kp = static_cast<const uint8_t*>(k_pool);
+  auto* vp = static_cast<const uint8_t*>(v_pool);
+  switch (kv_dtype) {
+    case SPV_F32:
+      hipLaunchKernelGGL((kv_gather_kernel<SPV_F32, false>), grid, blk, 0, s, kp, vp, kv_scales, table, length,
+                         layer, capacity, block_size, num_kv_heads, head_dim, out);
+      break;
+    case SPV_BF16:
+      hipLaunchKernelGGL((kv_gather_kernel<SPV_BF16, false>), grid, blk, 0, s, kp, vp, kv_scales, table,
+                         length, layer, capacity, block_size, num_kv_heads, head_dim, out);
+      break;
+    case SPV_F16:
+      hipLaunchKernelGGL((kv_gather_kernel<SPV_F16, false>), grid, blk, 0, s, kp, vp, kv_scales, table, length,
+                         layer, capacity, block_size, num_kv_heads, head_dim, out);
+      break;
+    default:
+      hipLaunchKernelGGL((kv_gather_kernel<SPV_FP8E4M3, true>), grid, blk, 0, s, kp, vp, kv_scales, table,
+                         length, layer, capacity, block_size, num_kv_heads, head_dim, out);
+  }
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_kv_read_blocks(const void* pool, int is_value, int kv_dtype, const int32_t* phys, int32_t n,
+                       int32_t layer, int32_t capacity, int32_t block_size, int32_t num_kv_heads,
+                       int32_t head_dim, void* out, void* stream) {
+  const int es = dtype_size(kv_dtype);
+  if (!pool || !phys || !out || n < 0 || layer < 0 || capacity < 1 || block_size < 1 || num_kv_heads < 1 ||
+      head_dim < 1 || es == 0)
+    return SPV_ERR_ARG;
+  if (n == 0) return SPV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t work = (size_t)n * block_size * num_kv_heads * head_dim;
+  const dim3 grid(grid_for(work, 256)), blk(256);
+  auto* p = static_cast<const uint8_t*>(pool);
+  auto* o = static_cast<uint8_t*>(out);
+  if (es == 4)
+    hipLaunchKernelGGL(kv_read_blocks_kernel<4>, grid, blk, 0, s, p, is_value, phys, n, layer, capacity,
+                       block_size, num_kv_heads, head_dim, o);
+  else if (es == 2)
+    hipLaunchKernelGGL(kv_read_blocks_kernel<2>, grid, blk, 0, s, p, is_value, phys, n, layer, capacity,
+                       block_size, num_kv_heads, head_dim, o);
+  else
+    hipLaunchKernelGGL(kv_read_blocks_kernel<1>, grid, blk, 0, s, p, is_value, phys, n, layer, capacity,
+                       block_size, num_kv_heads, head_dim, o);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// Shared definitions for the gfx950 paged-KV speculative-verify library.
+//
+// Device-side conventions used by every kernel in this library:
+//   * block ids, positions and counts are int32;
+//   * K pages are laid out [layer][block][kv_head][token][d] and V pages are
+//     laid out transposed, [layer][block][kv_head][d][token], so the attention
+//     kernel can feed both straight from HBM into MFMA operand registers;
+//   * the free list is a stack `free_stack[0..top)` (top = free count) plus a
+//     per-block flag array `free_flag[cap]` (1 = on the free list), and the
+//     counters live in `ctr[SPV_CTR_WORDS]`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/specverify.h"
+
+namespace spv {
+
+// ctr[] word indices
+enum : int {
+  CTR_TOP = 0,        // number of free blocks (stack height)
+  CTR_EXHAUSTED = 1,  // 1 + batch index of the first sequence whose allocation failed, else 0
+  CTR_SLOWPATH = 2,   // count of rewinds that took the exact sequential path
+  CTR_PUSHED = 3,     // blocks actually pushed by the last rewind / free
+  CTR_POPPED = 4,     // block id returned by the last single alloc (-1 if exhausted)
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t v) {
+  return __half2float(__ushort_as_half(v));
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// OCP fp8 e4m3 (gfx950 native format): bias 7, no infinities, 0x7f/0xff = NaN.
+__device__ __forceinline__ float fp8e4m3_to_f32(uint8_t v) {
+  const uint32_t s = (v >> 7) & 1u, e = (v >> 3) & 0xfu, m = v & 7u;
+  float r;
+  if (e == 0) r = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
+  else if (e == 15 && m == 7) r = __uint_as_float(0x7fc00000u);
+  else r = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return s ? -r : r;
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* base, size_t i) {
+  if constexpr (DT == SPV_F32) return static_cast<const float*>(base)[i];
+  else if constexpr (DT == SPV_BF16) return bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+  else if constexpr (DT == SPV_F16) return f16_to_f32(static_cast<const uint16_t*>(base)[i]);
+  else return fp8e4m3_to_f32(static_cast<const uint8_t*>(base)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_elem(void* base, size_t i, float v) {
+  if constexpr (DT == SPV_F32) static_cast<float*>(base)[i] = v;
+  else if constexpr (DT == SPV_BF16) static_cast<uint16_t*>(base)[i] = f32_to_bf16(v);
+  else static_cast<uint16_t*>(base)[i] = f32_to_f16(v);
+}
+
+inline int dtype_size(int dt) {
+  switch (dt) {
+    case SPV_F32: return 4;
+    case SPV_BF16: case SPV_F16: return 2;
+    case SPV_FP8E4M3: return 1;
+    default: return 0;
+  }
+}
+
+// Block-wide exclusive scan of one int per thread (blockDim.x <= 1024, multiple of 64).
+// `lds` must hold blockDim.x/64 ints. Returns the exclusive prefix; *total gets the sum.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) lds[wave] = incl;
+  __syncthreads();
+  int wave_off = 0, sum = 0;
+  for (int w = 0; w < nw; ++w) {
+    int x = lds[w];
+    if (w < wave) wave_off += x;
+    sum += x;
+  }
+  __syncthreads();
+  *total = sum;
+  return wave_off + incl - v;
+}
+
+}  // namespace spv
+
+#define SPV_CHECK_LAUNCH()                                        \
+  do {                                                            \
+    hipError_t _e = hipGetLastError();                            \
+    if (_e != hipSuccess) return SPV_ERR_LAUNCH;                  \
+  } while (0)

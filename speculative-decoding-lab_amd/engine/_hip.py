@@ -1,0 +1,137 @@
+"""ctypes binding of libspecverify.so (the gfx950 HIP library).
+
+There is no CPU path: every operation of this package runs on the GPU through
+this library, and loading fails loudly when the library has not been built or a
+tensor is not on a GPU device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "lib", "libspecverify.so")
+
+SPV_OK = 0
+SPV_ERR_ARG = -1
+SPV_ERR_LAUNCH = -2
+SPV_ERR_WORKSPACE = -3
+SPV_ERR_UNSUPPORTED = -4
+SPV_CTR_WORDS = 8
+CTR_TOP, CTR_EXHAUSTED, CTR_SLOWPATH, CTR_PUSHED = 0, 1, 2, 3
+
+SPV_F32, SPV_BF16, SPV_F16, SPV_FP8E4M3 = 0, 1, 2, 3
+_DTYPE_CODE = {torch.float32: SPV_F32, torch.bfloat16: SPV_BF16, torch.float16: SPV_F16}
+if hasattr(torch, "float8_e4m3fn"):
+    _DTYPE_CODE[torch.float8_e4m3fn] = SPV_FP8E4M3
+
+_ERRORS = {
+    SPV_ERR_ARG: "invalid argument",
+    SPV_ERR_LAUNCH: "kernel launch failed",
+    SPV_ERR_WORKSPACE: "workspace too small",
+    SPV_ERR_UNSUPPORTED: "unsupported configuration",
+}
+
+P = ctypes.c_void_p
+I = ctypes.c_int32
+F = ctypes.c_float
+S = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/specverify.h
+SIGNATURES = {
+    "spv_version": (ctypes.c_char_p, []),
+    "spv_pool_init": (I, [P, P, P, I, P]),
+    "spv_pool_alloc_one": (I, [P, P, P, I, P, P]),
+    "spv_pool_free_one": (I, [P, P, P, I, I, P, P]),
+    "spv_kv_append": (I, [P, P, I, P, P, P, I, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
+    "spv_kv_rewind": (I, [P, I, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "spv_kv_gather": (I, [P, P, I, P, P, I, I, I, I, I, I, I, I, P, P]),
+    "spv_kv_read_blocks": (I, [P, I, I, P, I, I, I, I, I, I, P, P]),
+    "spv_verify_attn_workspace_bytes": (S, [I, I, I, I, I, I, I]),
+    "spv_verify_attn": (I, [P, P, I, P, P, I, P, P, I, P, P, I, I, I, I, I, I, I, I, I, F, P, S, P]),
+    "spv_verify_sample_workspace_bytes": (S, [I, I, I]),
+    "spv_verify_sample": (I, [P, P, I, F, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, I, P, S, P]),
+    "spv_logits_to_probs": (I, [P, P, I, I, F, P]),
+    "spv_residual": (I, [P, P, P, I, P]),
+    "spv_race_argmax": (I, [P, P, I, P, P]),
+    "spv_accept_prob": (I, [P, P, I, P, P]),
+}
+
+
+class HipLibraryError(RuntimeError):
+    """The HIP library is missing or a call into it failed."""
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libspecverify.so once (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HipLibraryError(
+                "libspecverify.so not found at {}; build it with "
+                "`python speculative-decoding-lab_amd/build.py`".format(LIB_PATH))
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != SPV_OK:
+        raise HipLibraryError("{} failed: {} ({})".format(name, _ERRORS.get(rc, "error"), rc))
+
+
+def require_gpu(device: torch.device) -> torch.device:
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise HipLibraryError(
+            "this engine runs on the GPU only (got device {!r}); there is no CPU path".format(str(device)))
+    if not torch.cuda.is_available():
+        raise HipLibraryError("no GPU is visible to PyTorch")
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    return device
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype not in _DTYPE_CODE:
+        raise HipLibraryError("unsupported dtype {}".format(dtype))
+    return _DTYPE_CODE[dtype]
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def i32(values, device: torch.device) -> torch.Tensor:
+    """int32 device tensor from a tensor or a Python sequence."""
+    if isinstance(values, torch.Tensor):
+        return values.to(device=device, dtype=torch.int32).contiguous()
+    return torch.tensor(list(values), dtype=torch.int32, device=device)
+
+
+class Workspace:
+    """Grow-only device scratch buffer owned by the caller of the library."""
+
+    def __init__(self) -> None:
+        self._buf: Optional[torch.Tensor] = None
+
+    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+        if self._buf is None or self._buf.numel() < nbytes or self._buf.device != device:
+            self._buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        return self._buf

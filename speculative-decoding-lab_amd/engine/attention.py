@@ -1,0 +1,124 @@
+"""Paged attention entry points backed by the gfx950 HIP kernels.
+
+Drop-in for the reference's engine/attention.py on the verify path:
+
+* ``gather_ctx``             -- attention.py:41-63, one gather kernel
+* ``paged_attention_extend`` -- attention.py:170-216, one verify-attention launch
+                                (plus a merge launch when contexts are split)
+* ``paged_attention_decode`` -- attention.py:96-118 as the one-row case of extend
+                                (``start = length - 1``, chunk 1)
+* ``_expand_to_q_heads``     -- attention.py:32-38 (kept for API parity; the
+                                kernels never materialise the expansion: kv head
+                                ``h // (Hq/Hkv)`` is indexed directly)
+
+``paged_attention_extend`` reads the block tables and lengths from the device
+metadata of :class:`engine.kv.PagedKVCache`; the K/V of the query chunk must
+already be written (write-then-attend, engine/model.py:182-190).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _hip
+from ._hip import call, ptr
+from .kv import PagedKVCache
+
+_workspace = _hip.Workspace()
+
+
+def _expand_to_q_heads(kv: torch.Tensor, num_q_heads: int) -> torch.Tensor:
+    """Broadcast ``(.., kv_heads, d)`` to ``(.., num_q_heads, d)`` (attention.py:32-38)."""
+    ratio = num_q_heads // kv.shape[-2]
+    return kv if ratio == 1 else kv.repeat_interleave(ratio, dim=-2)
+
+
+def gather_ctx(kv: PagedKVCache, layer: int, seq_id: int, length: int) -> torch.Tensor:
+    """The stored K/V prefix of one sequence, ``(2, length, kv_heads, d)`` (K row 0, V row 1)."""
+    length = int(length)
+    out_dtype = kv.dtype
+    out = torch.empty((2, max(length, 0), kv.num_kv_heads, kv.head_dim), dtype=out_dtype,
+                      device=kv.device)
+    if length <= 0:
+        return out
+    seq_id = kv._check_sid(seq_id)
+    kv._refresh()
+    if -(-length // kv.block_size) > kv._nb[seq_id]:
+        raise IndexError("length {} exceeds the blocks of sequence {}".format(length, seq_id))
+    call("spv_kv_gather", ptr(kv.k_pool), ptr(kv.v_pool), kv._dt, None, ptr(kv.tables_dev),
+         kv.max_blocks_per_seq, seq_id, length, int(layer), kv.allocator.capacity, kv.block_size,
+         kv.num_kv_heads, kv.head_dim, ptr(out), _hip.stream_of(kv.device))
+    return out
+
+
+def verify_attention(query_3d: torch.Tensor, kv: PagedKVCache, layer: int,
+                     seq_ids: Union[Sequence[int], torch.Tensor],
+                     start_positions: Union[Sequence[int], torch.Tensor], max_ctx: int,
+                     scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Device-argument form of ``paged_attention_extend``.
+
+    ``seq_ids``/``start_positions`` may be int32 device tensors (no host sync);
+    ``max_ctx`` must bound ``start + chunk`` for every row.
+    """
+    B, chunk, hq, d = query_3d.shape
+    if d != kv.head_dim or hq % kv.num_kv_heads:
+        raise ValueError("query heads/dim do not match the cache")
+    if query_3d.device != kv.device:
+        raise ValueError("query must live on {}".format(kv.device))
+    q = query_3d.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    if B == 0:
+        return out
+    sid_t = _hip.i32(seq_ids, kv.device)
+    start_t = _hip.i32(start_positions, kv.device)
+    if max_ctx > kv.max_blocks_per_seq * kv.block_size:
+        kv._grow_width(-(-max_ctx // kv.block_size))
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    ws_bytes = _hip.lib().spv_verify_attn_workspace_bytes(B, chunk, hq, kv.num_kv_heads, d,
+                                                          kv.block_size, int(max_ctx))
+    ws = _workspace.get(ws_bytes, kv.device) if ws_bytes else None
+    call("spv_verify_attn", ptr(out), ptr(q), _hip.dtype_code(q.dtype), ptr(kv.k_pool), ptr(kv.v_pool),
+         kv._dt, None, ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t), B, chunk,
+         hq, kv.num_kv_heads, d, kv.block_size, int(layer), kv.allocator.capacity, int(max_ctx),
+         scale, ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
+    return out
+
+
+def paged_attention_extend(query_3d: torch.Tensor, kv: PagedKVCache, layer: int,
+                           seq_ids: Sequence[int], start_positions: Sequence[int],
+                           num_q_heads: int) -> torch.Tensor:
+    """Causal attention of a chunk over its paged prefix (attention.py:170-216).
+
+    ``query_3d`` is ``(B, chunk, num_q_heads, d)``; row ``j`` of sequence ``b``
+    attends positions ``0 .. start_positions[b] + j``. Returns
+    ``(B, chunk, num_q_heads, d)`` in the query dtype.
+    """
+    B, chunk = int(query_3d.shape[0]), int(query_3d.shape[1])
+    if int(query_3d.shape[2]) != int(num_q_heads):
+        raise ValueError("query has {} heads, expected {}".format(query_3d.shape[2], num_q_heads))
+    starts = [int(s) for s in start_positions]
+    sids = [kv._check_sid(s) for s in seq_ids]
+    if len(starts) != B or len(sids) != B:
+        raise ValueError("one seq_id and start position per batch row")
+    kv._refresh()
+    for sid, st in zip(sids, starts):
+        if st < 0 or -(-(st + chunk) // kv.block_size) > kv._nb[sid]:
+            raise IndexError("sequence {} has no K/V written up to position {}".format(sid, st + chunk))
+    max_ctx = max(starts) + chunk if B else chunk
+    return verify_attention(query_3d, kv, layer, sids, starts, max_ctx)
+
+
+def paged_attention_decode(query_2d: torch.Tensor, kv: PagedKVCache, layer: int,
+                           seq_ids: Sequence[int], seq_token_lengths: Sequence[int],
+                           num_q_heads: int) -> torch.Tensor:
+    """One query row per sequence over its full stored prefix (attention.py:96-118)."""
+    lengths = [int(x) for x in seq_token_lengths]
+    if any(x < 1 for x in lengths):
+        raise ValueError("decode needs at least one stored position per row")
+    q3 = query_2d.unsqueeze(1)
+    out = paged_attention_extend(q3, kv, layer, seq_ids, [x - 1 for x in lengths], num_q_heads)
+    return out.squeeze(1)

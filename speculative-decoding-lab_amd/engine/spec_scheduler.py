@@ -1,0 +1,226 @@
+"""Rejection sampling and commit of a speculative round on the GPU.
+
+Drop-in for the verify part of the reference's engine/spec_scheduler.py:
+
+* ``batch_accept``  -- spec_scheduler.py:46-88 with the reference's live CPU
+  ``torch.Generator``. The acceptance probabilities of every position come
+  from the device in one launch; the host then draws the uniforms and the one
+  ``Exp(1)`` race row per sequence in exactly the reference's order (a uniform
+  per examined position, then the multinomial's exponential row), and a second
+  launch makes the decisions and races on the device.
+* ``verify_sample`` -- the fused form with caller-supplied randomness
+  (``u[B, gamma]``, ``E[B, V]``): softmax/greedy rows from logits, decisions,
+  residual/bonus race and the commit cut of spec_scheduler.py:274-303, all on
+  the device, outputs left on the device.
+* ``VerifyStep``    -- one verify round of a continuous batch: per layer
+  ``write_block`` + ``verify_attention``, then ``verify_sample`` on the
+  round's logits and ``rewind_device`` of the KV pool with the device-computed
+  lengths and finished flags (spec_scheduler.py:255-322 minus the model).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence
+
+import torch
+
+from . import _hip
+from ._hip import call, ptr
+from .attention import verify_attention
+from .kv import PagedKVCache
+
+_workspace = _hip.Workspace()
+
+
+def _draw_uniform(generator: torch.Generator) -> float:
+    """The accept coin of one position (spec_scheduler.py:41-43)."""
+    return float(torch.rand(1, generator=generator).item())
+
+
+@dataclass
+class VerifyResult:
+    """Device int32 outputs of one verify-sampling launch."""
+
+    accept_len: torch.Tensor   # (B,) drafts accepted
+    out_tokens: torch.Tensor   # (B, gamma+1) accepted drafts then the drawn token, -1 padded
+    n_commit: torch.Tensor     # (B,) tokens kept after the budget / eos cut
+    finished: torch.Tensor     # (B,) 1 = sequence finished this round
+    new_len: torch.Tensor      # (B,) cache length to rewind to, -1 = no truncate
+
+    def accepted_lists(self) -> List[List[int]]:
+        lens = self.accept_len.tolist()
+        toks = self.out_tokens.tolist()
+        return [row[: n + 1] for row, n in zip(toks, lens)]
+
+
+def _launch_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Tensor,
+                   u: torch.Tensor, noise: Optional[torch.Tensor], temperature: float,
+                   is_probs: bool, start_pos: Optional[torch.Tensor], remaining: Optional[torch.Tensor],
+                   eos_id: Optional[int], decide_only: bool, accept_prob: Optional[torch.Tensor],
+                   result: Optional[VerifyResult]) -> None:
+    B, C, V = (int(x) for x in target.shape)
+    gamma = C - 1
+    dev = target.device
+    ws_bytes = _hip.lib().spv_verify_sample_workspace_bytes(B, gamma, V)
+    if ws_bytes == 0:
+        raise ValueError("unsupported verify-sampling shape B={} gamma={} V={}".format(B, gamma, V))
+    ws = _workspace.get(ws_bytes, dev)
+    r = result
+    call("spv_verify_sample", ptr(target), ptr(draft), 1 if is_probs else 0, float(temperature),
+         ptr(proposals), ptr(u), ptr(noise), ptr(start_pos), ptr(remaining),
+         -1 if eos_id is None else int(eos_id), B, gamma, V,
+         ptr(r.accept_len) if r else None, ptr(r.out_tokens) if r else None,
+         ptr(r.n_commit) if r else None, ptr(r.finished) if r else None,
+         ptr(r.new_len) if r else None, ptr(accept_prob), 1 if decide_only else 0,
+         ptr(ws), int(ws_bytes), _hip.stream_of(dev))
+
+
+def _new_result(B: int, gamma: int, dev: torch.device) -> VerifyResult:
+    z = lambda *s: torch.empty(s, dtype=torch.int32, device=dev)  # noqa: E731
+    return VerifyResult(z(B), z(B, gamma + 1), z(B), z(B), z(B))
+
+
+def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Tensor,
+                  u: torch.Tensor, noise: Optional[torch.Tensor], temperature: float,
+                  start_pos: Optional[torch.Tensor] = None, remaining: Optional[torch.Tensor] = None,
+                  eos_id: Optional[int] = None, is_probs: bool = False,
+                  result: Optional[VerifyResult] = None, validate: bool = True) -> VerifyResult:
+    """Fused accept / resample / bonus / commit cut of one round (device in, device out).
+
+    ``target`` (B, gamma+1, V) and ``draft`` (B, gamma, V) are fp32 logits (or
+    probabilities with ``is_probs``); ``proposals`` (B, gamma); ``u`` (B, gamma)
+    uniforms; ``noise`` (B, V) ``Exp(1)`` rows (unused for greedy logits).
+    ``validate=False`` skips the proposal-range check (a host synchronisation).
+    """
+    dev = _hip.require_gpu(target.device)
+    B, C, V = target.shape
+    gamma = C - 1
+    if tuple(draft.shape) != (B, gamma, V) or tuple(proposals.shape) != (B, gamma) or \
+            tuple(u.shape) != (B, gamma):
+        raise ValueError("inconsistent verify-sampling shapes")
+    greedy = not is_probs and not temperature > 0
+    if noise is not None and tuple(noise.shape) != (B, V):
+        raise ValueError("noise must be (B, V)")
+    if noise is None and not greedy:
+        raise ValueError("sampling needs the Exp(1) noise rows")
+    t = target.float().contiguous()
+    d = draft.float().contiguous()
+    x = _hip.i32(proposals, dev)
+    if validate and (int(x.min().item()) < 0 or int(x.max().item()) >= V):
+        raise IndexError("proposal token ids must lie in [0, V)")
+    uf = u.to(device=dev, dtype=torch.float32).contiguous()
+    nz = None if noise is None else noise.to(device=dev, dtype=torch.float32).contiguous()
+    sp = None if start_pos is None else _hip.i32(start_pos, dev)
+    rem = None if remaining is None else _hip.i32(remaining, dev)
+    if result is None:
+        result = _new_result(int(B), int(gamma), dev)
+    _launch_sample(t, d, x, uf, nz, temperature, is_probs, sp, rem, eos_id, False, None, result)
+    return result
+
+
+def acceptance_probabilities(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Tensor,
+                             temperature: float = 1.0, is_probs: bool = True) -> torch.Tensor:
+    """float64 (B, gamma) acceptance probabilities of every position (one launch)."""
+    dev = _hip.require_gpu(target.device)
+    B, C, V = target.shape
+    t = target.float().contiguous()
+    d = draft.float().contiguous()
+    x = _hip.i32(proposals, dev)
+    a = torch.empty((B, C - 1), dtype=torch.float64, device=dev)
+    u = torch.zeros((B, C - 1), dtype=torch.float32, device=dev)
+    _launch_sample(t, d, x, u, None, temperature, is_probs, None, None, None, True, a, None)
+    return a
+
+
+def batch_accept(p_by_sid: Dict[int, torch.Tensor], q_by_sid: Dict[int, Sequence[torch.Tensor]],
+                 proposals_by_sid: Dict[int, Sequence[int]], generator: torch.Generator
+                 ) -> Dict[int, List[int]]:
+    """Accept/reject each sequence's draft block (spec_scheduler.py:46-88).
+
+    ``p_by_sid[sid]`` is the ``(gamma+1, V)`` target distribution block,
+    ``q_by_sid[sid]`` the ``gamma`` draft rows, ``proposals_by_sid[sid]`` the
+    proposed ids; returns the committed token list (length 1..gamma+1) per
+    sequence, consuming ``generator`` exactly as the reference does.
+    """
+    sids = list(p_by_sid.keys())
+    if not sids:
+        return {}
+    gammas = {len(proposals_by_sid[s]) for s in sids}
+    if len(gammas) != 1:
+        # Mixed draft lengths: sequences are independent, keep dict order.
+        out: Dict[int, List[int]] = {}
+        for s in sids:
+            out.update(batch_accept({s: p_by_sid[s]}, {s: q_by_sid[s]}, {s: proposals_by_sid[s]},
+                                    generator))
+        return out
+    gamma = gammas.pop()
+    dev = _hip.require_gpu(p_by_sid[sids[0]].device)
+    p = torch.stack([p_by_sid[s].float() for s in sids]).contiguous()
+    q = torch.stack([torch.stack([r.float() for r in q_by_sid[s]]) for s in sids]).contiguous()
+    B, C, V = p.shape
+    if C != gamma + 1 or tuple(q.shape) != (B, gamma, V):
+        raise ValueError("p rows must be gamma+1 and q rows gamma per sequence")
+    x = torch.tensor([list(proposals_by_sid[s]) for s in sids], dtype=torch.int32, device=dev)
+    a = acceptance_probabilities(p, q, x, is_probs=True).tolist()
+    # Host draws, in the reference's order.
+    u = torch.full((B, gamma), 2.0, dtype=torch.float32)
+    noise = torch.empty((B, V), dtype=torch.float32)
+    for b in range(B):
+        for j in range(gamma):
+            uj = _draw_uniform(generator)
+            u[b, j] = uj
+            if not uj < a[b][j]:
+                break
+        noise[b] = torch.empty(V, dtype=torch.float32).exponential_(1, generator=generator)
+    res = verify_sample(p, q, x, u.to(dev), noise.to(dev), 1.0, is_probs=True)
+    lists = res.accepted_lists()
+    return {s: lists[i] for i, s in enumerate(sids)}
+
+
+class VerifyStep:
+    """One verify round over a continuous batch on one GPU.
+
+    The caller supplies, per round: the batch's sequence ids and start
+    positions (``kv.seq_lengths`` at round start), per-layer ``(q, k, v)`` of the
+    ``gamma+1`` verify tokens, the target/draft logits of the round, the draft
+    proposals, and the randomness. The round writes the K/V of every layer,
+    runs verify attention per layer, samples, and rewinds the pool on the device
+    with the sampled lengths. Nothing synchronises with the host.
+    """
+
+    def __init__(self, kv: PagedKVCache, gamma: int, temperature: float, eos_id: Optional[int] = None):
+        self.kv = kv
+        self.gamma = int(gamma)
+        self.temperature = float(temperature)
+        self.eos_id = eos_id
+
+    def attend_layers(self, seq_ids: Sequence[int], start_positions: Sequence[int],
+                      q_layers: Sequence[torch.Tensor], k_layers: Sequence[torch.Tensor],
+                      v_layers: Sequence[torch.Tensor],
+                      outs: Optional[Sequence[torch.Tensor]] = None) -> List[torch.Tensor]:
+        chunk = self.gamma + 1
+        max_ctx = max(int(s) for s in start_positions) + chunk
+        sid_t = _hip.i32(seq_ids, self.kv.device)
+        st_t = _hip.i32(start_positions, self.kv.device)
+        results = []
+        self.kv._grow_width(-(-max_ctx // self.kv.block_size))
+        for layer in range(len(q_layers)):
+            self.kv.write_block_device(layer, sid_t, st_t, k_layers[layer].to(self.kv.dtype).contiguous(),
+                                       v_layers[layer].to(self.kv.dtype).contiguous())
+            results.append(verify_attention(q_layers[layer], self.kv, layer, sid_t, st_t, max_ctx,
+                                            out=None if outs is None else outs[layer]))
+        return results
+
+    def sample_and_commit(self, seq_ids: Sequence[int], start_positions: Sequence[int],
+                          target_logits: torch.Tensor, draft_logits: torch.Tensor,
+                          proposals: torch.Tensor, u: torch.Tensor, noise: Optional[torch.Tensor],
+                          remaining: Optional[Sequence[int]] = None) -> VerifyResult:
+        dev = self.kv.device
+        sid_t = _hip.i32(seq_ids, dev)
+        st_t = _hip.i32(start_positions, dev)
+        rem_t = None if remaining is None else _hip.i32(remaining, dev)
+        res = verify_sample(target_logits, draft_logits, proposals, u, noise, self.temperature,
+                            start_pos=st_t, remaining=rem_t, eos_id=self.eos_id, validate=False)
+        self.kv.rewind_device(sid_t, res.new_len, res.finished)
+        return res

@@ -1,0 +1,86 @@
+"""Logit post-processing and the rejection-sampling primitives on the GPU.
+
+Drop-in for the reference's specdec/sampler.py:16-99 (the part on the verify
+path). Every function runs a HIP kernel of libspecverify; tensors must live on a
+GPU. Randomness still comes from the caller's CPU ``torch.Generator``:
+``sample_token`` draws the ``Exp(1)`` row that ``torch.multinomial`` would
+consume from it (multinomial with one sample is ``argmax(p / E)`` with ``E``
+from ``exponential_``), copies it to the device and races there, so the
+generator state afterwards is the reference's.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from engine import _hip
+from engine._hip import call, ptr
+
+from .config import SamplingConfig
+
+_EPS = 1e-12  # specdec/sampler.py:16
+
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    _hip.require_gpu(x.device)
+    return x.detach().float().contiguous()
+
+
+def logits_to_probs(logits: torch.Tensor, sampling: SamplingConfig) -> torch.Tensor:
+    """Greedy one-hot (T <= 0) or ``softmax(logits / max(T, 1e-12))`` over the last dim."""
+    top_k = getattr(sampling, "top_k", 0)
+    top_p = getattr(sampling, "top_p", 1.0)
+    if (top_k and 0 < top_k < logits.shape[-1]) or 0.0 < top_p < 1.0:
+        raise NotImplementedError("top-k / top-p filtering is not part of the verify kernels")
+    z = _rows(logits)
+    V = int(z.shape[-1])
+    out = torch.empty_like(z)
+    rows = z.numel() // V if V else 0
+    temperature = 0.0 if sampling.is_greedy else float(sampling.temperature)
+    call("spv_logits_to_probs", ptr(z), ptr(out), rows, V, temperature, _hip.stream_of(z.device))
+    return out
+
+
+def draw_race_noise(vocab: int, generator: Optional[torch.Generator] = None) -> torch.Tensor:
+    """The ``Exp(1)`` row one ``torch.multinomial(p, 1)`` draw takes from ``generator`` (CPU)."""
+    return torch.empty(int(vocab), dtype=torch.float32).exponential_(1, generator=generator)
+
+
+def sample_token(probs: torch.Tensor, generator: Optional[torch.Generator] = None) -> int:
+    """Draw one token id from a probability vector (specdec/sampler.py:59-69)."""
+    flat = _rows(probs).reshape(-1)
+    noise = draw_race_noise(flat.numel(), generator).to(flat.device, non_blocking=False)
+    out = torch.empty(1, dtype=torch.int32, device=flat.device)
+    call("spv_race_argmax", ptr(flat), ptr(noise), int(flat.numel()), ptr(out),
+         _hip.stream_of(flat.device))
+    return int(out.item())
+
+
+def residual_distribution(p: torch.Tensor, q: torch.Tensor) -> torch.Tensor:
+    """Normalised ``(p - q)_+``, or ``p / sum(p)`` when that is empty (specdec/sampler.py:72-83)."""
+    pf, qf = _rows(p).reshape(-1), _rows(q).reshape(-1)
+    if pf.numel() != qf.numel():
+        raise ValueError("p and q must have the same size")
+    out = torch.empty_like(pf)
+    call("spv_residual", ptr(pf), ptr(qf), ptr(out), int(pf.numel()), _hip.stream_of(pf.device))
+    return out.reshape(p.shape)
+
+
+def acceptance_probability(p: torch.Tensor, q: torch.Tensor, token_id: int) -> float:
+    """``min(1, p(x) / q(x))`` in float64 with the 1e-12 branches (specdec/sampler.py:86-92)."""
+    pf, qf = _rows(p).reshape(-1), _rows(q).reshape(-1)
+    token_id = int(token_id)
+    if not 0 <= token_id < pf.numel():
+        raise IndexError("token id {} out of range".format(token_id))
+    out = torch.empty(1, dtype=torch.float64, device=pf.device)
+    call("spv_accept_prob", ptr(pf), ptr(qf), token_id, ptr(out), _hip.stream_of(pf.device))
+    return float(out.item())
+
+
+def build_generator(seed: int, device: Optional[torch.device] = None) -> torch.Generator:
+    """Deterministic CPU generator (specdec/sampler.py:95-99)."""
+    generator = torch.Generator(device="cpu")
+    generator.manual_seed(int(seed))
+    return generator

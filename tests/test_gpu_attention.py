@@ -1,0 +1,195 @@
+"""GPU parity of paged verify attention against the oracle.
+
+* fp32 pools (VALU path): the reference's extend test structure and the CPU
+  check workload (4 sequences, L = 37/64/100/129, 4/2 heads, d = 64, C = 5) at
+  atol = rtol = 1e-5, like the reference's own tests;
+* bf16 pools: the Qwen2.5-1.5B-shaped workload (B = 32, 12/2 heads, d = 128,
+  block 16, L ~ U[256, 4096], C = 6, random-permutation tables over 65,536
+  blocks) on the MFMA path against the oracle run in fp32 on the same bf16
+  values. Tolerance (bf16 output): max |out - ref| <= 2e-3 * max |ref| over each
+  sequence's output, plus every element within 1 bf16 ulp (2^-7 relative) + 2e-3
+  * max |ref| -- the output itself is rounded to bf16 (2^-9 relative);
+* size-independent properties: key positions beyond L full of NaN never reach
+  the output; one context split and many splits agree.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from engine.attention import (_expand_to_q_heads, gather_ctx, paged_attention_decode,
+                              paged_attention_extend, verify_attention)
+from engine.kv import PagedKVCache
+from oracle import attention as ref_attn
+from oracle import kv_pool as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def test_expand_to_q_heads_repeats_kv(cuda):
+    kv = torch.randn(5, 2, 8, device=cuda)
+    e = _expand_to_q_heads(kv, 4)
+    assert torch.equal(e[:, 1], kv[:, 0]) and torch.equal(e[:, 2], kv[:, 1])
+
+
+def _write_both(gpu, cpu, layer, sid, keys, values):
+    n = keys.shape[0]
+    gpu.write_block(layer, [sid], [0], keys.unsqueeze(0).to(gpu.device), values.unsqueeze(0).to(gpu.device))
+    cpu.write_block(layer, [sid], [0], keys.unsqueeze(0), values.unsqueeze(0))
+    assert gpu.seq_lengths[sid] == n
+
+
+def test_extend_matches_oracle_reference_test_shape(cuda):
+    # reference tests/test_paged_attention_extend.py:56-77: 7-token prompt, chunk 5, bs 4
+    torch.manual_seed(1)
+    Hq, Hkv, d, bs = 4, 2, 16, 4
+    gpu = PagedKVCache(2, Hkv, d, 64, bs, cuda, torch.float32)
+    cpu = ref.PagedKVCache(2, Hkv, d, 64, bs)
+    gpu.add_sequence(0)
+    cpu.add_sequence(0)
+    _write_both(gpu, cpu, 0, 0, torch.randn(7, Hkv, d), torch.randn(7, Hkv, d))
+    start, chunk = 7, 5
+    ck, cv, q = torch.randn(1, chunk, Hkv, d), torch.randn(1, chunk, Hkv, d), torch.randn(1, chunk, Hq, d)
+    gpu.write_block(0, [0], [start], ck.to(cuda), cv.to(cuda))
+    cpu.write_block(0, [0], [start], ck, cv)
+    out = paged_attention_extend(q.to(cuda), gpu, 0, [0], [start], Hq)
+    assert out.shape == (1, chunk, Hq, d)
+    want = ref_attn.paged_attention_extend(q, cpu, 0, [0], [start], Hq)
+    assert torch.allclose(out.cpu(), want, atol=1e-5, rtol=1e-5)
+    for j in range(chunk):  # row j == full attention over the prefix 0..start+j
+        pair = ref_attn.gather_ctx(cpu, 0, 0, start + j + 1)
+        row = ref_attn.full_attention(q[0, j], pair[0], pair[1], Hq)
+        assert torch.allclose(out[0, j].cpu(), row, atol=1e-5, rtol=1e-5)
+
+
+def test_decode_matches_oracle(cuda):
+    torch.manual_seed(2)
+    Hq, Hkv, d, bs = 4, 2, 8, 4
+    gpu = PagedKVCache(2, Hkv, d, 64, bs, cuda, torch.float32)
+    cpu = ref.PagedKVCache(2, Hkv, d, 64, bs)
+    lens = [1, 4, 7]
+    for s, n in enumerate(lens):
+        gpu.add_sequence(s)
+        cpu.add_sequence(s)
+        _write_both(gpu, cpu, 0, s, torch.randn(n, Hkv, d), torch.randn(n, Hkv, d))
+    q = torch.randn(3, Hq, d)
+    out = paged_attention_decode(q.to(cuda), gpu, 0, [0, 1, 2], lens, Hq).cpu()
+    for s, n in enumerate(lens):
+        pair = ref_attn.gather_ctx(cpu, 0, s, n)
+        assert torch.allclose(out[s], ref_attn.full_attention(q[s], pair[0], pair[1], Hq),
+                              atol=1e-5, rtol=1e-5)
+
+
+def _dense_pool(cuda, lens, C, Hkv, d, bs, dtype, seed, cap=None, nan_fill=False, perm=True):
+    """Pool holding K/V for positions 0..L+C-1 of each sequence, written through
+    write_block, with tables scattered over the pool."""
+    g = torch.Generator().manual_seed(seed)
+    need = [-(-(L + C) // bs) for L in lens]
+    cap = cap or sum(need) + 8
+    gpu = PagedKVCache(1, Hkv, d, cap, bs, cuda, dtype, max_seqs=len(lens))
+    if nan_fill:
+        gpu.k_pool.fill_(float("nan"))
+        gpu.v_pool.fill_(float("nan"))
+    ids = torch.randperm(cap, generator=g).tolist() if perm else list(range(cap))
+    tables, pos = [], 0
+    for n in need:
+        tables.append(ids[pos: pos + n])
+        pos += n
+    gpu.load_state(tables, [0] * len(lens), ids[pos:])
+    keys = [torch.randn(L + C, Hkv, d, generator=g).to(dtype) for L in lens]
+    values = [torch.randn(L + C, Hkv, d, generator=g).to(dtype) for L in lens]
+    for s, L in enumerate(lens):
+        if L:
+            gpu.write_block(0, [s], [0], keys[s][:L].unsqueeze(0).to(cuda),
+                            values[s][:L].unsqueeze(0).to(cuda))
+    # the verify chunk is appended for the whole batch in one call
+    kc = torch.stack([k[L:] for k, L in zip(keys, lens)]).to(cuda)
+    vc = torch.stack([v[L:] for v, L in zip(values, lens)]).to(cuda)
+    gpu.write_block(0, list(range(len(lens))), lens, kc, vc)
+    return gpu, keys, values
+
+
+def test_cpu_check_workload_fp32(cuda):
+    lens, C, Hq, Hkv, d, bs = [37, 64, 100, 129], 5, 4, 2, 64, 16
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, bs, torch.float32, seed=0)
+    q = torch.randn(len(lens), C, Hq, d, generator=torch.Generator().manual_seed(5))
+    out = paged_attention_extend(q.to(cuda), gpu, 0, list(range(4)), lens, Hq).cpu()
+    want = ref_attn.extend_attention_dense(q, keys, values, lens, Hq)
+    assert torch.allclose(out, want, atol=1e-5, rtol=1e-5)
+
+
+def _bf16_check(out, want):
+    """bf16 tolerance: per sequence, max error <= 2e-3 * max|ref|; every element
+    within one bf16 ulp (2^-7 relative) plus 2e-3 * max|ref|."""
+    out = out.float().cpu()
+    want = want.float()
+    for b in range(out.shape[0]):
+        scale = float(want[b].abs().max())
+        err = (out[b] - want[b]).abs()
+        assert float(err.max()) <= 2e-3 * scale, (b, float(err.max()), scale)
+        assert bool((err <= 2.0 ** -7 * want[b].abs() + 2e-3 * scale).all())
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_qwen15_shaped_bf16_mfma(cuda, seed):
+    g = torch.Generator().manual_seed(100 + seed)
+    B, C, Hq, Hkv, d, bs = 32, 6, 12, 2, 128, 16
+    lens = torch.randint(256, 4097, (B,), generator=g).tolist()
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, bs, torch.bfloat16, seed=seed, cap=65536)
+    q = torch.randn(B, C, Hq, d, generator=g).to(torch.bfloat16)
+    out = paged_attention_extend(q.to(cuda), gpu, 0, list(range(B)), lens, Hq)
+    want = ref_attn.extend_attention_dense(q, keys, values, lens, Hq)
+    _bf16_check(out, want)
+
+
+@pytest.mark.parametrize("shape", [
+    # (C, Hq, Hkv, d): G = C * Hq/Hkv
+    (7, 16, 2, 128),   # 3B-shaped: G = 56, four 16-row tiles
+    (9, 14, 2, 64),    # 0.5B-shaped heads: G = 63, d = 64
+    (2, 16, 2, 128),   # G = 16, one tile
+    (3, 12, 2, 128),   # G = 18, two tiles with padding
+    (1, 4, 2, 128),    # decode-like G = 2 on bf16: VALU path
+])
+def test_bf16_shapes(cuda, shape):
+    C, Hq, Hkv, d = shape
+    g = torch.Generator().manual_seed(sum(shape))
+    lens = [0, 1, 15, 16, 17, 255, 300, 1000]
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.bfloat16, seed=7)
+    q = torch.randn(len(lens), C, Hq, d, generator=g).to(torch.bfloat16)
+    out = paged_attention_extend(q.to(cuda), gpu, 0, list(range(len(lens))), lens, Hq)
+    want = ref_attn.extend_attention_dense(q, keys, values, lens, Hq)
+    _bf16_check(out, want)
+
+
+def test_stale_nan_beyond_context_never_leaks(cuda):
+    lens, C, Hq, Hkv, d = [5, 40, 77], 6, 12, 2, 128
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.bfloat16, seed=3, nan_fill=True)
+    q = torch.randn(3, C, Hq, d).to(torch.bfloat16)
+    out = paged_attention_extend(q.to(cuda), gpu, 0, [0, 1, 2], lens, Hq)
+    assert bool(torch.isfinite(out.float()).all())
+    _bf16_check(out, ref_attn.extend_attention_dense(q, keys, values, lens, Hq))
+    gpu32, k32, v32 = _dense_pool(cuda, lens, C, Hkv, 64, 16, torch.float32, seed=3, nan_fill=True)
+    q32 = torch.randn(3, C, 4, 64)
+    out32 = paged_attention_extend(q32.to(cuda), gpu32, 0, [0, 1, 2], lens, 4).cpu()
+    assert torch.allclose(out32, ref_attn.extend_attention_dense(q32, k32, v32, lens, 4), atol=1e-5, rtol=1e-5)
+
+
+def test_split_count_does_not_change_result(cuda):
+    # The same batch with max_ctx raised (more, partly empty splits) gives the same output.
+    lens, C, Hq, Hkv, d = [700, 33], 6, 12, 2, 128
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.bfloat16, seed=4)
+    q = torch.randn(2, C, Hq, d).to(torch.bfloat16).to(cuda)
+    a = verify_attention(q, gpu, 0, [0, 1], lens, max(lens) + C)
+    b = verify_attention(q, gpu, 0, [0, 1], lens, 4096)
+    assert torch.equal(a, b)
+
+
+def test_gather_ctx_matches_written_values(cuda):
+    lens, C = [20, 3], 2
+    gpu, keys, values = _dense_pool(cuda, lens, C, 2, 16, 4, torch.float32, seed=9)
+    for s, L in enumerate(lens):
+        got = gather_ctx(gpu, 0, s, L + C).cpu()
+        assert torch.equal(got[0], keys[s]) and torch.equal(got[1], values[s])

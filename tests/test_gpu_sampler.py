@@ -1,0 +1,169 @@
+"""GPU parity of the rejection-sampling kernels against the oracle.
+
+Token ids, accept lengths and commit outputs must be identical (bit-exact):
+
+* the reference's one-hot ``batch_accept`` cases (tests/test_spec_accept.py:29-73);
+* the golden vectors recorded from the reference's ``batch_accept`` with a live
+  generator -- same tokens and the same generator state afterwards;
+* the fused-sampler workload (B = 64, gamma = 5, V = 151,936, target logits
+  ~ N(0, 2^2), draft = target + N(0, 1), T = 1 and T = 0) against the oracle's
+  logits_to_probs + batch_accept on the same logits, uniforms and Exp(1) rows;
+* the commit cut (budget with Python slice semantics, eos) against the oracle.
+
+Probabilities computed from logits on the GPU differ from torch's CPU softmax in
+the last bits; a decision can only differ when ``u`` lies within ~1e-6 of
+``p/q`` or two race keys tie to ~1e-6. The workload test reports the smallest
+such margin and requires the ids to match.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+
+import pytest
+import torch
+
+from engine import spec_scheduler as es
+from oracle import sampler as S
+from oracle import spec_step as ref_step
+from specdec import sampler as gs
+from specdec.config import SamplingConfig
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "batch_accept_golden.json")
+
+
+def _one_hot(t, dev, v=8):
+    x = torch.zeros(v, device=dev)
+    x[t] = 1.0
+    return x
+
+
+def test_one_hot_cases(cuda):
+    g = torch.Generator().manual_seed(0)
+    p = {0: torch.stack([_one_hot(3, cuda)] * 3)}
+    assert es.batch_accept(p, {0: [_one_hot(3, cuda)] * 2}, {0: [3, 3]}, g)[0] == [3, 3, 3]
+    p = {0: torch.stack([_one_hot(5, cuda)] * 2)}
+    assert es.batch_accept(p, {0: [_one_hot(2, cuda)]}, {0: [2]}, g)[0] == [5]
+    p = {0: torch.stack([_one_hot(1, cuda), _one_hot(4, cuda), _one_hot(4, cuda)])}
+    q = {0: [_one_hot(1, cuda), _one_hot(7, cuda)]}
+    assert es.batch_accept(p, q, {0: [1, 7]}, g)[0] == [1, 4]
+
+
+def _golden_cases():
+    with open(GOLDEN) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: "v{}s{}".format(c["vocab"], c["seed"]))
+def test_batch_accept_golden(cuda, case):
+    B, gm, V = case["batch"], case["gamma"], case["vocab"]
+    p = torch.tensor(case["p"], dtype=torch.float32).reshape(B, gm + 1, V).to(cuda)
+    q = torch.tensor(case["q"], dtype=torch.float32).reshape(B, gm, V).to(cuda)
+    sids = case["sids"]
+    gen = torch.Generator().manual_seed(case["gen_seed"])
+    out = es.batch_accept({s: p[b] for b, s in enumerate(sids)},
+                          {s: [q[b, j] for j in range(gm)] for b, s in enumerate(sids)},
+                          {s: case["proposals"][b] for b, s in enumerate(sids)}, gen)
+    assert [out[s] for s in sids] == case["accepted"]
+    assert float(torch.rand(1, generator=gen).item()) == case["next_uniform"]
+
+
+def test_sampler_primitives_match_oracle(cuda):
+    g = torch.Generator().manual_seed(3)
+    z = torch.randn(4, 1000, generator=g) * 2
+    for T in (0.0, 0.7, 1.0):
+        got = gs.logits_to_probs(z.to(cuda), SamplingConfig(temperature=T)).cpu()
+        want = S.logits_to_probs(z, T)
+        if T == 0.0:
+            assert torch.equal(got, want)
+        else:
+            assert torch.allclose(got, want, rtol=2e-6, atol=1e-9)
+    p, q = S.logits_to_probs(z[0], 1.0), S.logits_to_probs(z[1], 1.0)
+    assert torch.allclose(gs.residual_distribution(p.to(cuda), q.to(cuda)).cpu(),
+                          S.residual_distribution(p, q), rtol=1e-6, atol=1e-9)
+    assert torch.allclose(gs.residual_distribution(p.to(cuda), p.to(cuda)).cpu(), p, atol=1e-7)
+    for x in (0, 5, 999):
+        assert gs.acceptance_probability(p.to(cuda), q.to(cuda), x) == S.acceptance_probability(p, q, x)
+    for seed in range(5):
+        g1 = torch.Generator().manual_seed(seed)
+        g2 = torch.Generator().manual_seed(seed)
+        assert gs.sample_token(p.to(cuda), g1) == S.sample_token(p, g2)
+        assert torch.equal(g1.get_state(), g2.get_state())
+
+
+def _workload(seed, B=64, gamma=5, V=151936, sigma=2.0):
+    g = torch.Generator().manual_seed(seed)
+    target = torch.randn(B, gamma + 1, V, generator=g) * sigma
+    draft = target[:, :gamma] + torch.randn(B, gamma, V, generator=g)
+    u = torch.rand(B, gamma, generator=g)
+    noise = torch.empty(B, V).exponential_(1, generator=g)
+    return g, target, draft, u, noise
+
+
+def _proposals(draft, T, g):
+    q = S.logits_to_probs(draft, T)
+    B, gamma, V = q.shape
+    return torch.multinomial(q.reshape(-1, V), 1, generator=g).reshape(B, gamma)
+
+
+@pytest.mark.parametrize("T", [1.0, 0.0])
+def test_fused_sampler_workload(cuda, T):
+    g, target, draft, u, noise = _workload(42 if T else 43)
+    x = _proposals(draft, T, g)
+    want = S.verify_from_logits(target, draft, x, u, noise, T)
+    res = es.verify_sample(target.to(cuda), draft.to(cuda), x.to(cuda), u.to(cuda),
+                           noise.to(cuda) if T > 0 else None, T)
+    got = res.accepted_lists()
+    assert got == want
+    lens = res.accept_len.tolist()
+    assert lens == [len(w) - 1 for w in want]
+    if T > 0:
+        assert 0 < sum(lens) < 5 * 64  # both accepts and rejections occur
+
+
+def test_fused_sampler_probs_mode_matches_batch_accept(cuda):
+    g, target, draft, u, noise = _workload(7, B=8, gamma=3, V=5000)
+    p, q = S.logits_to_probs(target, 1.0), S.logits_to_probs(draft, 1.0)
+    x = _proposals(draft, 1.0, g)
+    want = S.batch_accept_noise(p, q, x, u, noise)
+    res = es.verify_sample(p.to(cuda), q.to(cuda), x.to(cuda), u.to(cuda), noise.to(cuda), 1.0,
+                           is_probs=True)
+    assert res.accepted_lists() == want
+
+
+def test_identical_rows_take_the_p_fallback(cuda):
+    # p == q: every proposal drawn from q is accepted w.p. 1 unless u >= 1;
+    # force a rejection with u = 1.0 so the residual is empty and p is raced.
+    g, target, _, _, noise = _workload(9, B=4, gamma=2, V=3000)
+    draft = target[:, :2].clone()
+    x = _proposals(draft, 1.0, g)
+    u = torch.ones(4, 2)
+    want = S.verify_from_logits(target, draft, x, u, noise, 1.0)
+    res = es.verify_sample(target.to(cuda), draft.to(cuda), x.to(cuda), u.to(cuda), noise.to(cuda), 1.0)
+    assert res.accepted_lists() == want
+
+
+@pytest.mark.parametrize("eos", [None, 3])
+def test_commit_cut_matches_oracle(cuda, eos):
+    B, gamma, V = 16, 4, 8
+    g = torch.Generator().manual_seed(5)
+    target = torch.randn(B, gamma + 1, V, generator=g)
+    draft = target[:, :gamma] + 0.3 * torch.randn(B, gamma, V, generator=g)
+    x = _proposals(draft, 0.0, g)
+    u = torch.rand(B, gamma, generator=g)
+    start = torch.randint(10, 100, (B,), generator=g)
+    remaining = torch.randint(-2, 7, (B,), generator=g)
+    want = S.verify_from_logits(target, draft, x, u, torch.ones(B, V), 0.0)
+    res = es.verify_sample(target.to(cuda), draft.to(cuda), x.to(cuda), u.to(cuda), None, 0.0,
+                           start_pos=start.to(cuda), remaining=remaining.to(cuda), eos_id=eos)
+    assert res.accepted_lists() == want
+    n_commit, fin, new_len = res.n_commit.tolist(), res.finished.tolist(), res.new_len.tolist()
+    for b in range(B):
+        kept, eos_hit = ref_step.cut_accepted(want[b], int(remaining[b]), eos)
+        k = len(kept)
+        assert n_commit[b] == k
+        assert fin[b] == int(eos_hit or k == 0 or k >= int(remaining[b]))
+        assert new_len[b] == (int(start[b]) + k if k > 0 else -1)
