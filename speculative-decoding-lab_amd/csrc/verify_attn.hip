@@ -5,21 +5,24 @@
 // of kv head hq / (Hq/Hkv) with softmax(scale * q.k) -- the chunk's own keys are
 // already in the pool (write-then-attend, engine/model.py:182-190).
 //
-// Work decomposition: one workgroup per (sequence, kv head, row group, KV split).
-// All G = C * (Hq/Hkv) query rows that share a kv head are processed together,
-// so every K/V page is read from HBM once per kv head and reused for all G rows.
-// Splits along the context produce (m, l, O) partials in log2 units that a small
-// merge kernel combines; a sequence that fits one split is written directly.
+// Work decomposition (MFMA path): all G = C * (Hq/Hkv) query rows that share a
+// kv head are processed together, so every K/V page is read from HBM once per kv
+// head and reused for all G rows. A persistent grid of workgroups splits the
+// flattened (sequence, kv head, page) list into equal contiguous shares; shares
+// that cut a sequence produce (m, l, O) partials in log2 units that a small merge
+// kernel combines, and a sequence seen by one workgroup is written directly.
 //
-// MFMA path (bf16 K/V, head_dim 64/128, block_size 16, G >= 16):
-//   S^T = K Q^T  with v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims of the
-//         page, B = Q^T held in registers for the whole kernel),
-//   O^T += V^T P^T with v_mfma_f32_16x16x16_bf16 (A = V^T straight from the
-//         transposed V page, B = P^T, which is exactly the accumulator layout of
-//         S^T: lane l holds keys 4*(l/16)+0..3 of query column l%16).
-// The online-softmax rescale therefore stays inside a lane (query = lane % 16
-// in both S^T and O^T); the row max needs two cross-lane steps (xor 16, 32).
-// VALU path: any dtype / head_dim <= 256 / block size, fp32 math with LDS tiles.
+// MFMA path (bf16 K/V, head_dim 64/128, block_size 16, G >= 16), per page:
+//   S^T = K Q^T  with v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims straight
+//         from the K page, B = Q^T from the LDS-staged query rows);
+//   O^T += V^T P^T with v_mfma_f32_16x16x32_bf16 where A = {V^T, V^T} straight
+//         from the transposed V page and B = {P_hi^T, P_lo^T}: P is split into
+//         two bf16 halves so P V is accumulated to ~16 bits, not bf16's 8.
+// P^T's layout is exactly the accumulator layout of S^T (lane l holds keys
+// 4*(l/16)+0..3 of query column l%16), so the online-softmax rescale stays
+// inside a lane; the row max needs two cross-lane steps (xor 16, 32).
+// VALU path: any dtype / head_dim <= 256 / block size, fp32 math with LDS tiles,
+// a (sequence, kv head, row group, split) grid and its own merge.
 #include <math.h>
 
 #include "spv_common.h"
@@ -29,7 +32,6 @@ using namespace spv;
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -204,242 +206,438 @@ __global__ __launch_bounds__(kAttnThreads) void attn_valu_kernel(AttnParams p) {
 }
 
 // ------------------------------------------------------------------ MFMA path
-__device__ __forceinline__ short4_t pack_bf16x4(float a, float b, float c, float d) {
-  short4_t r;
-  r[0] = (short)f32_to_bf16(a);
-  r[1] = (short)f32_to_bf16(b);
-  r[2] = (short)f32_to_bf16(c);
-  r[3] = (short)f32_to_bf16(d);
-  return r;
+//
+// Persistent, length-balanced decomposition. Every (sequence b, kv head h,
+// row group rg) is a "segment" of npages(b) pages; segments are laid end to end
+// in (b, h, rg) order and the resident workgroups each take an equal contiguous
+// share of that page list, so ragged context lengths cost no tail. A workgroup
+// walks the segments its share touches: it stages the segment's query rows in
+// LDS, its two wave pairs take every other page (three pages in flight per
+// wave in rotating register buffers), the waves merge through LDS, and the workgroup writes either the
+// final output (it covered the whole segment) or a partial (m, l, O) into slot
+// `workgroup + segment` (unique along the staircase of shares). The merge
+// kernel combines the contiguous run of slots of every split segment.
+// Resident workgroups on 256 CUs (two per CU) and register page buffers per wave.
+constexpr int kMfmaWGsMax = 512;
+__host__ __device__ constexpr int mfma_wgs(int) { return kMfmaWGsMax; }
+// Register page buffers per wave: three pages in flight up to 48 query rows.
+__host__ __device__ constexpr int page_bufs(int nt) { return nt >= 4 ? 2 : 4; }
+
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
 }
 
-// NT: 16-row query tiles per workgroup; D: head_dim (64 or 128); bf16 K/V and Q.
+// s_pref[b] = pages (per segment) of sequences before b; s_pref[B] = total.
+__device__ void build_page_prefix(const AttnParams& p, int* s_pref, int* scan_tmp) {
+  int carry = 0;
+  for (int base = 0; base < p.B; base += blockDim.x) {
+    const int b = base + threadIdx.x;
+    const int np = b < p.B ? context_pages(p, p.start[b] + p.C) : 0;
+    int total;
+    const int off = block_exclusive_scan(np, scan_tmp, &total);
+    if (b < p.B) s_pref[b] = carry + off;
+    carry += total;
+  }
+  if (threadIdx.x == 0) s_pref[p.B] = carry;
+  __syncthreads();
+}
+
+// Values that are the same in every lane of a wave, moved to scalar registers
+// so that page addresses become scalar base + lane offset.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Largest b with hr_count * s_pref[b] <= x.
+__device__ __forceinline__ int seq_of_page(const int* s_pref, int B, long long hr_count, long long x) {
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (hr_count * s_pref[mid] <= x) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Workgroup whose share [floor(w T / NW), floor((w+1) T / NW)) holds page x.
+__device__ __forceinline__ int wg_of_page(long long x, long long T, int nw) {
+  return (int)(((x + 1) * nw - 1) / T);
+}
+
+// One page as a wave holds it: the whole K slice (S^T needs every dimension)
+// and the V^T tiles of the wave's half of the head dimensions.
+template <int NT, int D>
+struct PageFrag {
+  uint4 k[D / 32];
+  uint2 v[D / 32];
+};
+
 template <int NT, int D, int QT>
-__global__ __launch_bounds__(kAttnThreads, NT >= 4 ? 1 : 2) void attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p) {
   constexpr int KS = D / 32;  // 32-dim k-steps of S^T
-  constexpr int MT = D / 16;  // 16-dim output tiles of O^T
+  constexpr int MTH = D / 32; // 16-dim output tiles of O^T per wave (half of d)
   constexpr int BS = 16;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int RPG = 16 * NT;
+  constexpr int QSTR = D + 8;  // bf16 row stride of the staged queries
+  extern __shared__ int s_pref[];
+  __shared__ int s_scan[kAttnThreads / 64];
+  __shared__ __align__(16) uint16_t sQ[RPG * QSTR];
+  __shared__ float sm_m[2][RPG];
+  __shared__ float sm_l[2][RPG];
+  __shared__ float sm_o[RPG][D + 4];
+
+  // Waves 2k and 2k+1 form pair k: both compute S^T and the softmax of the
+  // pair's pages; wave half `hf` accumulates O^T for dimensions [hf*d/2, (hf+1)*d/2).
+  const int lane = threadIdx.x & 63, w = uni(threadIdx.x >> 6);
+  const int pair = w >> 1, hf = w & 1;
   const int i16 = lane & 15, g = lane >> 4;
-  const int s = blockIdx.x, h = blockIdx.y / p.nrg, rg = blockIdx.y % p.nrg, b = blockIdx.z;
-  const int start = p.start[b];
-  const int L = start + p.C;
-  const int npages = context_pages(p, L);
-  const int pg0 = s * p.pages_per_split;
-  if (pg0 >= npages) return;
-  const int pg1 = min(npages, pg0 + p.pages_per_split);
-  const int nsplit = (npages + p.pages_per_split - 1) / p.pages_per_split;
-  const int r0 = rg * (16 * NT);
-  const int nr = min(16 * NT, p.G - r0);
-  const int sid = p.seq_ids[b];
-  const int32_t* table = p.tables + (size_t)sid * p.maxb;
-
-  // Q^T fragments (B operand of S^T): query column 16*nt + i16, dims 32*ks + 8*g + 0..7.
-  bf16x8_t qf[NT][KS];
-  int jrow[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int rr = 16 * nt + i16;
-    const int r = r0 + min(rr, nr - 1);
-    const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
-    jrow[nt] = j;
-    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + (((size_t)b * p.C + j) * p.Hq + hq) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      uint4 v = rr < nr ? *reinterpret_cast<const uint4*>(qp + 32 * ks + 8 * g) : make_uint4(0, 0, 0, 0);
-      qf[nt][ks] = __builtin_bit_cast(bf16x8_t, v);
-    }
-  }
-
-  f32x4_t o[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m[NT], l[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    m[nt] = -INFINITY;
-    l[nt] = 0.f;
-  }
-
+  const int wg = blockIdx.x, nw = gridDim.x;
+  build_page_prefix(p, s_pref, s_scan);
+  const long long HR = (long long)p.Hkv * p.nrg;
+  const long long T = HR * s_pref[p.B];
+  if (T == 0) return;
+  const long long r0 = (long long)wg * T / nw, r1 = (long long)(wg + 1) * T / nw;
+  if (r0 >= r1) return;
+  int b = uni(seq_of_page(s_pref, p.B, HR, r0));
+  int hr = uni((int)((r0 - HR * s_pref[b]) / (s_pref[b + 1] - s_pref[b])));
   const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
   const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
   const float sl2 = p.scale_log2;
 
-  int pg = pg0 + w;
-  uint4 kf_n[KS];
-  uint2 vf_n[MT];
-  auto load_page = [&](int page, uint4* kf, uint2* vf) {
-    const int phys = safe_block(p, table[page]);
-    const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
-    const uint16_t* kp = kbase + slot;
-    const uint16_t* vp = vbase + slot;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) vf[mt] = *reinterpret_cast<const uint2*>(vp + (i16 + 16 * mt) * BS + 4 * g);
-  };
-  if (pg < pg1) load_page(pg, kf_n, vf_n);
+  for (long long x = r0; x < r1;) {
+    const int np = uni(s_pref[b + 1] - s_pref[b]);
+    const long long seg0 = HR * uni(s_pref[b]) + (long long)hr * np;
+    const int lp0 = (int)(x - seg0);
+    const int lp1 = (int)(min(r1, seg0 + np) - seg0);
+    const int h = hr / p.nrg, rg = hr - h * p.nrg;
+    const int seg = b * (int)HR + hr;
+    const int start = uni(p.start[b]);
+    const int L = start + p.C;
+    const int qr0 = rg * RPG;
+    const int nr = min(RPG, p.G - qr0);
+    const int32_t* table = p.tables + (size_t)uni(p.seq_ids[b]) * p.maxb;
 
-  for (; pg < pg1; pg += 4) {
-    uint4 kf[KS];
-    uint2 vf[MT];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = kf_n[ks];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) vf[mt] = vf_n[mt];
-    if (pg + 4 < pg1) load_page(pg + 4, kf_n, vf_n);
-
-    const int kpos0 = pg * BS + 4 * g;  // key position of this lane's accumulator element 0
-    if (pg == npages - 1) {
-      // Keys at or beyond L are stale pool contents: zero their V so a masked
-      // (p = 0) key cannot inject a non-finite value.
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        uint32_t lo = vf[mt].x, hi = vf[mt].y;
-        if (kpos0 + 0 >= L) lo &= 0xffff0000u;
-        if (kpos0 + 1 >= L) lo &= 0x0000ffffu;
-        if (kpos0 + 2 >= L) hi &= 0xffff0000u;
-        if (kpos0 + 3 >= L) hi &= 0x0000ffffu;
-        vf[mt] = make_uint2(lo, hi);
+    // Stage the segment's query rows (zero rows past nr).
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < RPG * (D / 8); idx += blockDim.x) {
+      const int rr = idx / (D / 8), c = idx - rr * (D / 8);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (rr < nr) {
+        const int r = qr0 + rr, j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
+        v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) +
+                                            (((size_t)b * p.C + j) * p.Hq + hq) * D + 8 * c);
       }
-    }
-
-    f32x4_t sc[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      sc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[ks]), qf[nt][ks],
-                                                         sc[nt], 0, 0, 0);
-    }
-    const bool need_mask = pg * BS + BS - 1 > start;
-    short4_t pf[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float x[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        x[jj] = sc[nt][jj] * sl2;
-        if (need_mask && kpos0 + jj > start + jrow[nt]) x[jj] = -INFINITY;
-      }
-      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m[nt], mx);
-      float alpha, e[4];
-      if (m_new == -INFINITY) {
-        alpha = 1.f;
-        e[0] = e[1] = e[2] = e[3] = 0.f;
-      } else {
-        alpha = exp2f(m[nt] - m_new);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) e[jj] = exp2f(x[jj] - m_new);
-      }
-      l[nt] = l[nt] * alpha + ((e[0] + e[1]) + (e[2] + e[3]));
-      m[nt] = m_new;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) o[mt][nt] *= alpha;
-      pf[nt] = pack_bf16x4(e[0], e[1], e[2], e[3]);
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const short4_t va = __builtin_bit_cast(short4_t, vf[mt]);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pf[nt], o[mt][nt], 0, 0, 0);
-    }
-  }
-
-  // Row sums: the four lane groups hold disjoint keys of the same query column.
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    l[nt] += __shfl_xor(l[nt], 16, 64);
-    l[nt] += __shfl_xor(l[nt], 32, 64);
-  }
-
-  // Merge the four waves of the workgroup through LDS.
-  __shared__ float sm_m[4][64];
-  __shared__ float sm_l[4][64];
-  __shared__ float sm_o[64][D + 4];
-  if (g == 0) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      sm_m[w][16 * nt + i16] = m[nt];
-      sm_l[w][16 * nt + i16] = l[nt];
-    }
-  }
-  __syncthreads();
-  float fac[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int qc = 16 * nt + i16;
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, sm_m[ww][qc]);
-    fac[nt] = (m[nt] == -INFINITY) ? 0.f : exp2f(m[nt] - M);
-  }
-  for (int ww = 0; ww < 4; ++ww) {
-    if (w == ww) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            float* dst = &sm_o[16 * nt + i16][16 * mt + 4 * g + jj];
-            const float v = o[mt][nt][jj] * fac[nt];
-            *dst = ww == 0 ? v : *dst + v;
-          }
+      *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = v;
     }
     __syncthreads();
-  }
 
-  // Write: row rr of this group, 8 dims per thread.
-  constexpr int kVec = 8;
-  for (int idx = threadIdx.x; idx < nr * (D / kVec); idx += blockDim.x) {
-    const int rr = idx / (D / kVec), e0 = (idx - rr * (D / kVec)) * kVec;
-    float M = -INFINITY;
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, sm_m[ww][rr]);
-    float Lsum = 0.f;
-    for (int ww = 0; ww < 4; ++ww) {
-      const float mw = sm_m[ww][rr];
-      if (mw != -INFINITY) Lsum += sm_l[ww][rr] * exp2f(mw - M);
+    int jrow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + i16, nr - 1)) / p.ratio;
+
+    f32x4_t o[MTH][NT];
+#pragma unroll
+    for (int mt = 0; mt < MTH; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m[NT], l[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      m[nt] = -INFINITY;
+      l[nt] = 0.f;
     }
-    const int r = r0 + rr;
-    if (nsplit == 1) {
-      const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
-      const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
-      const float inv = 1.f / Lsum;
-      if constexpr (QT == SPV_BF16) {
-        uint16_t t[kVec];
+
+    auto load_page = [&](PageFrag<NT, D>& f, int page) {
+      const int phys = uni(safe_block(p, table[page]));
+      const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
+      const uint16_t* kp = kbase + slot;
+      const uint16_t* vp = vbase + slot;
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) t[k] = f32_to_bf16(sm_o[rr][e0 + k] * inv);
-        uint4 v;
-        v.x = t[0] | ((uint32_t)t[1] << 16);
-        v.y = t[2] | ((uint32_t)t[3] << 16);
-        v.z = t[4] | ((uint32_t)t[5] << 16);
-        v.w = t[6] | ((uint32_t)t[7] << 16);
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + ob) = v;
+      for (int ks = 0; ks < KS; ++ks) f.k[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
+#pragma unroll
+      for (int mt = 0; mt < MTH; ++mt)
+        f.v[mt] = *reinterpret_cast<const uint2*>(vp + (i16 + 16 * (hf * MTH + mt)) * BS + 4 * g);
+    };
+
+    auto compute_page = [&](PageFrag<NT, D>& f, int page) {
+      const int kpos0 = page * BS + 4 * g;  // key position of accumulator element 0
+      if (page * BS + BS > L) {
+        // Keys at or beyond L are stale pool contents: zero their V.
+#pragma unroll
+        for (int mt = 0; mt < MTH; ++mt) {
+          uint32_t lo = f.v[mt].x, hi = f.v[mt].y;
+          if (kpos0 + 0 >= L) lo &= 0xffff0000u;
+          if (kpos0 + 1 >= L) lo &= 0x0000ffffu;
+          if (kpos0 + 2 >= L) hi &= 0xffff0000u;
+          if (kpos0 + 3 >= L) hi &= 0x0000ffffu;
+          f.v[mt] = make_uint2(lo, hi);
+        }
+      }
+      // Re-read the query fragments from LDS for every page instead of letting
+      // them be hoisted into 16*NT*KS/4 long-lived registers.
+      asm volatile("" ::: "memory");
+      f32x4_t sc[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        sc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint4 qv = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
+          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, f.k[ks]),
+                                                           __builtin_bit_cast(bf16x8_t, qv), sc[nt], 0, 0, 0);
+        }
+      }
+      const bool need_mask = page * BS + BS - 1 > start;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        float x4[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          x4[jj] = sc[nt][jj] * sl2;
+          if (need_mask && kpos0 + jj > start + jrow[nt]) x4[jj] = -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(x4[0], x4[1]), fmaxf(x4[2], x4[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m[nt], mx);
+        float alpha, e[4];
+        if (m_new == -INFINITY) {
+          alpha = 1.f;
+          e[0] = e[1] = e[2] = e[3] = 0.f;
+        } else {
+          alpha = exp2f(m[nt] - m_new);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) e[jj] = exp2f(x4[jj] - m_new);
+        }
+        l[nt] = l[nt] * alpha + ((e[0] + e[1]) + (e[2] + e[3]));
+        m[nt] = m_new;
+        // P = hi + lo, both bf16: slots 0..3 carry hi, 4..7 lo of the same keys,
+        // so one 16x16x32 MFMA against {V, V} accumulates P V to ~16 bits.
+        uint32_t hw0 = pack2_bf16(e[0], e[1]), hw1 = pack2_bf16(e[2], e[3]);
+        const uint32_t lw0 = pack2_bf16(e[0] - bf16_to_f32(hw0 & 0xffffu), e[1] - bf16_to_f32(hw0 >> 16));
+        const uint32_t lw1 = pack2_bf16(e[2] - bf16_to_f32(hw1 & 0xffffu), e[3] - bf16_to_f32(hw1 >> 16));
+        const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, make_uint4(hw0, hw1, lw0, lw1));
+#pragma unroll
+        for (int mt = 0; mt < MTH; ++mt) {
+          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(f.v[mt].x, f.v[mt].y, f.v[mt].x, f.v[mt].y));
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf, o[mt][nt] * alpha, 0, 0, 0);
+        }
+      }
+    };
+
+    // Pages lp0 + pair, lp0 + pair + 2, ...: kPageBufs rotating register
+    // buffers keep kPageBufs - 1 pages in flight while one is computed.
+    constexpr int kPageBufs = page_bufs(NT);
+    PageFrag<NT, D> buf[kPageBufs];
+    const int pg0 = lp0 + pair;
+#pragma unroll
+    for (int u = 0; u < kPageBufs - 1; ++u)
+      if (pg0 + 2 * u < lp1) load_page(buf[u], pg0 + 2 * u);
+    for (int it = 0; pg0 + 2 * it < lp1; it += kPageBufs) {
+#pragma unroll
+      for (int u = 0; u < kPageBufs; ++u) {
+        const int pg = pg0 + 2 * (it + u);
+        if (pg < lp1) {
+          const int nxt = pg + 2 * (kPageBufs - 1);
+          if (nxt < lp1) load_page(buf[(u + kPageBufs - 1) % kPageBufs], nxt);
+          compute_page(buf[u], pg);
+        }
+      }
+    }
+
+    // Row sums: the four lane groups hold disjoint keys of the same query column.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      l[nt] += __shfl_xor(l[nt], 16, 64);
+      l[nt] += __shfl_xor(l[nt], 32, 64);
+    }
+    if (g == 0 && hf == 0) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        sm_m[pair][16 * nt + i16] = m[nt];
+        sm_l[pair][16 * nt + i16] = l[nt];
+      }
+    }
+    __syncthreads();
+    float fac[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int qc = 16 * nt + i16;
+      const float M = fmaxf(sm_m[0][qc], sm_m[1][qc]);
+      fac[nt] = (m[nt] == -INFINITY) ? 0.f : exp2f(m[nt] - M);
+    }
+    for (int pp = 0; pp < 2; ++pp) {
+      if (pair == pp) {
+#pragma unroll
+        for (int mt = 0; mt < MTH; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            float4* dst = reinterpret_cast<float4*>(&sm_o[16 * nt + i16][16 * (hf * MTH + mt) + 4 * g]);
+            const float4 v = make_float4(o[mt][nt][0] * fac[nt], o[mt][nt][1] * fac[nt], o[mt][nt][2] * fac[nt],
+                                         o[mt][nt][3] * fac[nt]);
+            if (pp == 0) {
+              *dst = v;
+            } else {
+              const float4 a = *dst;
+              *dst = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+            }
+          }
+      }
+      __syncthreads();
+    }
+
+    // Final output when this workgroup saw the whole segment, else a partial.
+    const bool final_out = lp0 == 0 && lp1 == np;
+    const int slot = wg + seg;
+    constexpr int kVec = 8;
+    for (int idx = threadIdx.x; idx < nr * (D / kVec); idx += blockDim.x) {
+      const int rr = idx / (D / kVec), e0 = (idx - rr * (D / kVec)) * kVec;
+      const float M = fmaxf(sm_m[0][rr], sm_m[1][rr]);
+      float Lsum = 0.f;
+      for (int pp = 0; pp < 2; ++pp) {
+        const float mw = sm_m[pp][rr];
+        if (mw != -INFINITY) Lsum += sm_l[pp][rr] * exp2f(mw - M);
+      }
+      const int r = qr0 + rr;
+      if (final_out) {
+        const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
+        const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
+        const float inv = 1.f / Lsum;
+        if constexpr (QT == SPV_BF16) {
+          uint4 v;
+          v.x = pack2_bf16(sm_o[rr][e0 + 0] * inv, sm_o[rr][e0 + 1] * inv);
+          v.y = pack2_bf16(sm_o[rr][e0 + 2] * inv, sm_o[rr][e0 + 3] * inv);
+          v.z = pack2_bf16(sm_o[rr][e0 + 4] * inv, sm_o[rr][e0 + 5] * inv);
+          v.w = pack2_bf16(sm_o[rr][e0 + 6] * inv, sm_o[rr][e0 + 7] * inv);
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + ob) = v;
+        } else {
+#pragma unroll
+          for (int k = 0; k < kVec; ++k) store_out<QT>(p, ob + k, sm_o[rr][e0 + k] * inv);
+        }
       } else {
-#pragma unroll
-        for (int k = 0; k < kVec; ++k) store_out<QT>(p, ob + k, sm_o[rr][e0 + k] * inv);
+        const size_t base = (size_t)slot * p.G + r;
+        float4* po = reinterpret_cast<float4*>(p.part_o + base * D + e0);
+        po[0] = make_float4(sm_o[rr][e0 + 0], sm_o[rr][e0 + 1], sm_o[rr][e0 + 2], sm_o[rr][e0 + 3]);
+        po[1] = make_float4(sm_o[rr][e0 + 4], sm_o[rr][e0 + 5], sm_o[rr][e0 + 6], sm_o[rr][e0 + 7]);
+        if (e0 == 0) {
+          p.part_ml[base * 2] = M;
+          p.part_ml[base * 2 + 1] = Lsum;
+        }
       }
-    } else {
-      const size_t base = (((size_t)b * p.Hkv + h) * p.max_splits + s) * p.G + r;
-#pragma unroll
-      for (int k = 0; k < kVec; ++k) p.part_o[base * D + e0 + k] = sm_o[rr][e0 + k];
-      if (e0 == 0) {
-        p.part_ml[base * 2] = M;
-        p.part_ml[base * 2 + 1] = Lsum;
-      }
+    }
+
+    x = seg0 + lp1;
+    if (++hr == HR) {
+      hr = 0;
+      ++b;
     }
   }
 }
 
-// ------------------------------------------------------------------ merge
+// Combine the partial slots of every segment that more than one workgroup saw.
+// Workgroups with an empty share (fewer pages than workgroups) wrote nothing
+// and are skipped. Per workgroup of this kernel: one segment, all its rows.
+template <int QT>
+__global__ __launch_bounds__(kAttnThreads) void attn_merge_slots_kernel(AttnParams p, int nw) {
+  extern __shared__ int s_pref[];
+  __shared__ int s_scan[kAttnThreads / 64];
+  __shared__ float s_f[64][33];   // per row, per contributing slot: exp2(m - M)
+  __shared__ float s_inv[64];     // per row: 1 / sum(l * f)
+  __shared__ int s_slot[32];
+  __shared__ int s_ns;
+  build_page_prefix(p, s_pref, s_scan);
+  const long long HR = (long long)p.Hkv * p.nrg;
+  const long long T = HR * s_pref[p.B];
+  const int seg = blockIdx.x;
+  const int b = (int)(seg / HR), hr = (int)(seg - b * HR);
+  const int np = s_pref[b + 1] - s_pref[b];
+  const long long seg0 = HR * s_pref[b] + (long long)hr * np;
+  const int w0 = wg_of_page(seg0, T, nw), w1 = wg_of_page(seg0 + np - 1, T, nw);
+  if (w0 == w1) return;
+  const int h = hr / p.nrg, rg = hr - h * p.nrg;
+  const int qr0 = rg * p.rows_per_group;
+  const int nr = min(p.rows_per_group, p.G - qr0);
+  const int D = p.d;
+  if (w1 - w0 < 32) {
+    // Common case: the contributing slots fit LDS; scale factors once per row.
+    if (threadIdx.x == 0) {
+      int ns = 0;
+      for (int k = w0; k <= w1; ++k)
+        if ((long long)k * T / nw < (long long)(k + 1) * T / nw) s_slot[ns++] = k + seg;
+      s_ns = ns;
+    }
+    __syncthreads();
+    const int ns = s_ns;
+    for (int idx = threadIdx.x; idx < nr; idx += blockDim.x) {
+      const int r = qr0 + idx;
+      float M = -INFINITY;
+      for (int k = 0; k < ns; ++k) M = fmaxf(M, p.part_ml[((size_t)s_slot[k] * p.G + r) * 2]);
+      float Lsum = 0.f;
+      for (int k = 0; k < ns; ++k) {
+        const size_t base = (size_t)s_slot[k] * p.G + r;
+        const float ms = p.part_ml[base * 2];
+        const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
+        s_f[idx][k] = f;
+        Lsum += p.part_ml[base * 2 + 1] * f;
+      }
+      s_inv[idx] = 1.f / Lsum;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nr * (D / 4); idx += blockDim.x) {
+      const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
+      const int r = qr0 + rr;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+      for (int k = 0; k < ns; ++k) {
+        const float f = s_f[rr][k];
+        const float4 v = *reinterpret_cast<const float4*>(p.part_o + ((size_t)s_slot[k] * p.G + r) * D + e0);
+        acc.x += v.x * f;
+        acc.y += v.y * f;
+        acc.z += v.z * f;
+        acc.w += v.w * f;
+      }
+      const float inv = s_inv[rr];
+      const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
+      const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
+      store_out<QT>(p, ob + 0, acc.x * inv);
+      store_out<QT>(p, ob + 1, acc.y * inv);
+      store_out<QT>(p, ob + 2, acc.z * inv);
+      store_out<QT>(p, ob + 3, acc.w * inv);
+    }
+    return;
+  }
+  // Many slots (a tiny workload spread over many workgroups): direct loops.
+  for (int idx = threadIdx.x; idx < nr * (D / 4); idx += blockDim.x) {
+    const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
+    const int r = qr0 + rr;
+    float M = -INFINITY;
+    for (int k = w0; k <= w1; ++k)
+      if ((long long)k * T / nw < (long long)(k + 1) * T / nw)
+        M = fmaxf(M, p.part_ml[((size_t)(k + seg) * p.G + r) * 2]);
+    float Lsum = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = w0; k <= w1; ++k) {
+      if (!((long long)k * T / nw < (long long)(k + 1) * T / nw)) continue;
+      const size_t base = (size_t)(k + seg) * p.G + r;
+      const float ms = p.part_ml[base * 2];
+      if (ms == -INFINITY) continue;
+      const float f = exp2f(ms - M);
+      Lsum += p.part_ml[base * 2 + 1] * f;
+      const float4 v = *reinterpret_cast<const float4*>(p.part_o + base * D + e0);
+      acc.x += v.x * f;
+      acc.y += v.y * f;
+      acc.z += v.z * f;
+      acc.w += v.w * f;
+    }
+    const float inv = 1.f / Lsum;
+    const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
+    const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
+    store_out<QT>(p, ob + 0, acc.x * inv);
+    store_out<QT>(p, ob + 1, acc.y * inv);
+    store_out<QT>(p, ob + 2, acc.z * inv);
+    store_out<QT>(p, ob + 3, acc.w * inv);
+  }
+}
+
+// ------------------------------------------------------------------ merge (VALU splits)
 template <int QT>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnParams p) {
   const int h = blockIdx.y, b = blockIdx.z;
@@ -480,22 +678,29 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
   if (pl.mfma) {
     pl.nt = G >= 64 ? 4 : (G + 15) / 16;
     pl.rows_per_group = 16 * pl.nt;
-    pl.pages_per_split = 16;
+    pl.pages_per_split = 0;
+    pl.max_splits = 0;
   } else {
     pl.nt = 0;
     pl.rows_per_group = 64;
     pl.pages_per_split = bs >= 16 ? 8 : 128 / bs;
+    pl.max_splits = (max_pages + pl.pages_per_split - 1) / pl.pages_per_split;
   }
   pl.nrg = (G + pl.rows_per_group - 1) / pl.rows_per_group;
-  pl.max_splits = (max_pages + pl.pages_per_split - 1) / pl.pages_per_split;
   (void)B;
   return pl;
 }
 
 size_t workspace_for(const Plan& pl, int B, int C, int Hq, int Hkv, int d) {
   const size_t G = (size_t)C * (Hq / Hkv);
-  if (pl.max_splits <= 1) return 0;
-  const size_t rows = (size_t)B * Hkv * pl.max_splits * G;
+  size_t slots;
+  if (pl.mfma) {
+    slots = (size_t)kMfmaWGsMax + (size_t)B * Hkv * pl.nrg;
+  } else {
+    if (pl.max_splits <= 1) return 0;
+    slots = (size_t)B * Hkv * pl.max_splits;
+  }
+  const size_t rows = slots * G;
   return rows * d * sizeof(float) + rows * 2 * sizeof(float) + 256;
 }
 
@@ -521,12 +726,14 @@ int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s) {
 }
 
 template <int D>
-void launch_mfma(const AttnParams& p, int nt, dim3 grid, hipStream_t s) {
+void launch_mfma(const AttnParams& p, int nt, hipStream_t s) {
+  const size_t smem = (size_t)(p.B + 1) * sizeof(int);
+  const dim3 grid(mfma_wgs(nt)), blk(kAttnThreads);
   switch (nt) {
-    case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16>), grid, dim3(kAttnThreads), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16>), grid, dim3(kAttnThreads), 0, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_mfma_kernel<3, D, SPV_BF16>), grid, dim3(kAttnThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((attn_mfma_kernel<4, D, SPV_BF16>), grid, dim3(kAttnThreads), 0, s, p); break;
+    case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16>), grid, blk, smem, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16>), grid, blk, smem, s, p); break;
+    case 3: hipLaunchKernelGGL((attn_mfma_kernel<3, D, SPV_BF16>), grid, blk, smem, s, p); break;
+    default: hipLaunchKernelGGL((attn_mfma_kernel<4, D, SPV_BF16>), grid, blk, smem, s, p); break;
   }
 }
 
@@ -555,9 +762,9 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
   if (q_dtype != SPV_F32 && q_dtype != SPV_BF16 && q_dtype != SPV_F16) return SPV_ERR_ARG;
   if (dtype_size(kv_dtype) == 0) return SPV_ERR_ARG;
   if (kv_dtype == SPV_FP8E4M3 && !kv_scales) return SPV_ERR_ARG;
-  if (B < 0 || C < 1 || num_kv_heads < 1 || num_q_heads < num_kv_heads || num_q_heads % num_kv_heads ||
-      head_dim < 1 || head_dim > 256 || block_size < 1 || layer < 0 || capacity < 1 || max_ctx < C ||
-      max_blocks_per_seq < (max_ctx + block_size - 1) / block_size)
+  if (B < 0 || B > 65535 || C < 1 || num_kv_heads < 1 || num_q_heads < num_kv_heads ||
+      num_q_heads % num_kv_heads || head_dim < 1 || head_dim > 256 || block_size < 1 || layer < 0 ||
+      capacity < 1 || max_ctx < C || max_blocks_per_seq < (max_ctx + block_size - 1) / block_size)
     return SPV_ERR_ARG;
   if (B == 0) return SPV_OK;
   const Plan pl = make_plan(B, C, num_q_heads, num_kv_heads, head_dim, block_size, max_ctx, kv_dtype, q_dtype);
@@ -591,33 +798,49 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
   p.max_pages = (max_ctx + block_size - 1) / block_size;
   p.scale_log2 = scale * kLog2e;
   if (need > 0) {
-    const size_t rows = (size_t)B * num_kv_heads * pl.max_splits * p.G;
+    const size_t rows = (need - 256) / (sizeof(float) * (head_dim + 2));
     p.part_o = static_cast<float*>(workspace);
     p.part_ml = p.part_o + rows * head_dim;
   }
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(pl.max_splits, num_kv_heads * pl.nrg, B);
   if (pl.mfma) {
-    if (head_dim == 128) launch_mfma<128>(p, pl.nt, grid, s);
-    else launch_mfma<64>(p, pl.nt, grid, s);
-  } else {
-    int rc;
+    if (head_dim == 128) launch_mfma<128>(p, pl.nt, s);
+    else launch_mfma<64>(p, pl.nt, s);
+    SPV_CHECK_LAUNCH();
+    const int nseg = B * num_kv_heads * pl.nrg;
+    const int nwg = mfma_wgs(pl.nt);
+    const size_t smem = (size_t)(B + 1) * sizeof(int);
+    const dim3 mgrid(nseg);
     switch (q_dtype) {
-      case SPV_F32: rc = launch_valu_q<SPV_F32>(p, kv_dtype, grid, s); break;
-      case SPV_BF16: rc = launch_valu_q<SPV_BF16>(p, kv_dtype, grid, s); break;
-      default: rc = launch_valu_q<SPV_F16>(p, kv_dtype, grid, s); break;
+      case SPV_F32:
+        hipLaunchKernelGGL(attn_merge_slots_kernel<SPV_F32>, mgrid, dim3(kAttnThreads), smem, s, p, nwg);
+        break;
+      case SPV_BF16:
+        hipLaunchKernelGGL(attn_merge_slots_kernel<SPV_BF16>, mgrid, dim3(kAttnThreads), smem, s, p, nwg);
+        break;
+      default:
+        hipLaunchKernelGGL(attn_merge_slots_kernel<SPV_F16>, mgrid, dim3(kAttnThreads), smem, s, p, nwg);
+        break;
     }
-    if (rc != SPV_OK) return rc;
+    SPV_CHECK_LAUNCH();
+    return SPV_OK;
   }
+  const dim3 grid(pl.max_splits, num_kv_heads * pl.nrg, B);
+  int rc;
+  switch (q_dtype) {
+    case SPV_F32: rc = launch_valu_q<SPV_F32>(p, kv_dtype, grid, s); break;
+    case SPV_BF16: rc = launch_valu_q<SPV_BF16>(p, kv_dtype, grid, s); break;
+    default: rc = launch_valu_q<SPV_F16>(p, kv_dtype, grid, s); break;
+  }
+  if (rc != SPV_OK) return rc;
   SPV_CHECK_LAUNCH();
   if (pl.max_splits > 1) {
-    const int per_block = kAttnThreads;
-    const int gx = (p.G * head_dim + per_block - 1) / per_block;
+    const int gx = (p.G * head_dim + kAttnThreads - 1) / kAttnThreads;
     const dim3 mgrid(gx, num_kv_heads, B);
     switch (q_dtype) {
-      case SPV_F32: hipLaunchKernelGGL(attn_merge_kernel<SPV_F32>, mgrid, dim3(per_block), 0, s, p); break;
-      case SPV_BF16: hipLaunchKernelGGL(attn_merge_kernel<SPV_BF16>, mgrid, dim3(per_block), 0, s, p); break;
-      default: hipLaunchKernelGGL(attn_merge_kernel<SPV_F16>, mgrid, dim3(per_block), 0, s, p); break;
+      case SPV_F32: hipLaunchKernelGGL(attn_merge_kernel<SPV_F32>, mgrid, dim3(kAttnThreads), 0, s, p); break;
+      case SPV_BF16: hipLaunchKernelGGL(attn_merge_kernel<SPV_BF16>, mgrid, dim3(kAttnThreads), 0, s, p); break;
+      default: hipLaunchKernelGGL(attn_merge_kernel<SPV_F16>, mgrid, dim3(kAttnThreads), 0, s, p); break;
     }
     SPV_CHECK_LAUNCH();
   }

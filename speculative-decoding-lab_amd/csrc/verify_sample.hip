@@ -11,13 +11,16 @@
 //   The draw is torch.multinomial(r, 1) == argmax(r / E) with E ~ Exp(1)^V
 //   supplied by the caller (first index on ties, NaN wins, as torch.argmax).
 //
-// Kernels (HBM-bound; every row is read once by the stats pass, and only the
-// one row pair that is raced is re-read):
-//   1. row_stats   grid (chunks, rows): per chunk max & sum exp (or argmax)
-//   2. decide      grid (B): combine chunks, decide k, greedy token, race setup
-//   3. resid_sum   grid (chunks, B): residual / p sums of the raced row pair
-//   4. race        grid (chunks, B): per chunk argmax of rhat / E
-//   5. finalize    grid (B): race winner, accepted list, budget/eos cut, new_len
+// Kernels (HBM-bound; every logits row is read once by the stats pass, the one
+// raced row pair and its noise row once more by the race pass):
+//   1. row_stats  grid (chunks, rows): per 8192-entry chunk max & sum exp (or argmax)
+//   2. decide     grid (B): combine the chunks, gather p[x], q[x], decide k
+//   3. race       grid (chunks, B): residual sum and the top-2 of r/E per chunk
+//   4. finalize   grid (B): the draw, the accepted list, budget/eos cut, new_len
+// The race compares r/E instead of (r/t)/E (t, the residual sum, is only known
+// after the pass). Both orders agree whenever the two best r/E differ by more
+// than 1e-6 relative (rounding moves a key by at most 2^-23); a closer pair, or
+// an empty residual (t <= 1e-12), is re-raced exactly by the finalize kernel.
 #include <math.h>
 
 #include "spv_common.h"
@@ -26,10 +29,12 @@ using namespace spv;
 
 namespace {
 
-constexpr int kChunk = 8192;   // elements of a row per stats / race workgroup
+constexpr int kChunk = 8192;  // elements of a row per stats / race workgroup
 constexpr int kThreads = 256;
+constexpr int kVecPerThread = kChunk / 4 / kThreads;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr double kEps = 1e-12;  // specdec/sampler.py:16
+constexpr double kEps = 1e-12;     // specdec/sampler.py:16
+constexpr float kTieRel = 1e-6f;   // top-2 gap below which the race is redone exactly
 
 enum RaceMode : int { RACE_NONE = 0, RACE_RESIDUAL = 1, RACE_BONUS = 2 };
 
@@ -41,13 +46,17 @@ struct RaceInfo {
   float mp, sp, mq, sq;  // softmax normalisers of the raced rows (logits mode)
 };
 
+struct RacePart {
+  float v1, v2;  // best and second-best r / E of the chunk
+  int i1, i2;
+  double rsum, psum;
+};
+
 struct SampleWs {
-  float* stat_m;     // [rows][nch]
-  float* stat_s;     // [rows][nch] (sum exp, or argmax index bits in greedy mode)
-  RaceInfo* info;    // [B]
-  double* rsum;      // [B][nch][2]  residual sum, p sum
-  float* race_v;     // [B][nch]
-  int* race_i;       // [B][nch]
+  float* stat_m;   // [rows][nch]
+  float* stat_s;   // [rows][nch] (sum exp, or argmax index bits in greedy mode)
+  RaceInfo* info;  // [B]
+  RacePart* race;  // [B][nch]
 };
 
 __host__ __device__ inline int num_chunks(int V) { return (V + kChunk - 1) / kChunk; }
@@ -64,17 +73,13 @@ size_t ws_layout(int B, int gamma, int V, SampleWs* ws, void* base) {
   const size_t o_m = take(rows * nch * sizeof(float));
   const size_t o_s = take(rows * nch * sizeof(float));
   const size_t o_info = take((size_t)B * sizeof(RaceInfo));
-  const size_t o_rsum = take((size_t)B * nch * 2 * sizeof(double));
-  const size_t o_rv = take((size_t)B * nch * sizeof(float));
-  const size_t o_ri = take((size_t)B * nch * sizeof(int));
+  const size_t o_race = take((size_t)B * nch * sizeof(RacePart));
   if (ws && base) {
     char* c = static_cast<char*>(base);
     ws->stat_m = reinterpret_cast<float*>(c + o_m);
     ws->stat_s = reinterpret_cast<float*>(c + o_s);
     ws->info = reinterpret_cast<RaceInfo*>(c + o_info);
-    ws->rsum = reinterpret_cast<double*>(c + o_rsum);
-    ws->race_v = reinterpret_cast<float*>(c + o_rv);
-    ws->race_i = reinterpret_cast<int*>(c + o_ri);
+    ws->race = reinterpret_cast<RacePart*>(c + o_race);
   }
   return off;
 }
@@ -99,25 +104,71 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
+// Argmax over the workgroup; every thread gets the result.
 __device__ __forceinline__ void block_argmax(float& v, int& i) {
-  __shared__ float sv[kThreads / 64];
-  __shared__ int si[kThreads / 64];
+  __shared__ float sv[16];
+  __shared__ int si[16];
   wave_argmax(v, i);
-  const int w = threadIdx.x >> 6;
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     sv[w] = v;
     si[w] = i;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int k = 1; k < (int)(blockDim.x >> 6); ++k)
-      if (better(sv[k], si[k], v, i)) {
-        v = sv[k];
-        i = si[k];
-      }
-  }
+  v = sv[0];
+  i = si[0];
+  for (int k = 1; k < nw; ++k)
+    if (better(sv[k], si[k], v, i)) {
+      v = sv[k];
+      i = si[k];
+    }
   __syncthreads();
 }
+
+// Top-2 (value, index) under `better`.
+struct Top2 {
+  float v1, v2;
+  int i1, i2;
+  __device__ __forceinline__ void init() {
+    v1 = v2 = -INFINITY;
+    i1 = i2 = 0x7fffffff;
+  }
+  __device__ __forceinline__ void push(float v, int i) {
+    if (better(v, i, v1, i1)) {
+      v2 = v1;
+      i2 = i1;
+      v1 = v;
+      i1 = i;
+    } else if (better(v, i, v2, i2)) {
+      v2 = v;
+      i2 = i;
+    }
+  }
+  __device__ __forceinline__ void merge(float w1, int j1, float w2, int j2) {
+    if (better(w1, j1, v1, i1)) {  // the other side's best leads
+      if (better(v1, i1, w2, j2)) {
+        v2 = v1;
+        i2 = i1;
+      } else {
+        v2 = w2;
+        i2 = j2;
+      }
+      v1 = w1;
+      i1 = j1;
+    } else if (better(w1, j1, v2, i2)) {
+      v2 = w1;
+      i2 = j1;
+    }
+  }
+  __device__ __forceinline__ void wave_reduce() {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float w1 = __shfl_xor(v1, o, 64), w2 = __shfl_xor(v2, o, 64);
+      const int j1 = __shfl_xor(i1, o, 64), j2 = __shfl_xor(i2, o, 64);
+      merge(w1, j1, w2, j2);
+    }
+  }
+};
 
 // Combine (m, s) pairs of sum exp(x - m) (natural-log units).
 __device__ __forceinline__ void lse_combine(float& m, float& s, float m2, float s2) {
@@ -135,22 +186,25 @@ __device__ __forceinline__ void lse_combine(float& m, float& s, float m2, float 
   }
 }
 
-__device__ __forceinline__ void block_lse(float& m, float& s) {
-  __shared__ float sm[kThreads / 64], ss[kThreads / 64];
+__device__ __forceinline__ void wave_lse(float& m, float& s) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
     lse_combine(m, s, m2, s2);
   }
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    sm[w] = m;
-    ss[w] = s;
-  }
+}
+
+__device__ __forceinline__ double block_sum_f64(double x) {
+  __shared__ double sd[16];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) sd[w] = x;
   __syncthreads();
-  if (threadIdx.x == 0)
-    for (int k = 1; k < (int)(blockDim.x >> 6); ++k) lse_combine(m, s, sm[k], ss[k]);
+  double t = 0.0;
+  for (int k = 0; k < nw; ++k) t += sd[k];
   __syncthreads();
+  return t;
 }
 
 __device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int row, int B,
@@ -162,6 +216,9 @@ __device__ __forceinline__ const float* row_ptr(const float* target, const float
 // x = z / T in float32 (torch divides the fp32 tensor by the scalar in fp32).
 __device__ __forceinline__ float scaled(float z, float tf, bool unit) { return unit ? z : z / tf; }
 
+// Element i of this thread's slice of a chunk: 8 float4 per thread.
+__device__ __forceinline__ int vec_index(int c, int k) { return c * (kChunk / 4) + threadIdx.x + k * kThreads; }
+
 // ------------------------------------------------------------- 1. row stats
 template <bool GREEDY>
 __global__ __launch_bounds__(kThreads) void row_stats_kernel(const float* __restrict__ target,
@@ -169,43 +226,53 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(const float* __rest
                                                              int gamma, int V, float tf, SampleWs ws) {
   const int c = blockIdx.x, row = blockIdx.y, nch = gridDim.x;
   const float* z = row_ptr(target, draft, row, B, gamma, V);
-  const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
   const bool unit = tf == 1.0f;
-  if (GREEDY) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
-      const float v = z[i];
-      if (better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
-      }
+  float bv = -INFINITY, m = -INFINITY, s = 0.f;
+  int bi = 0x7fffffff;
+  if ((V & 3) == 0) {
+    // All loads of the slice are issued before any is used.
+    const int n4 = V >> 2;
+    float4 v[kVecPerThread];
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i4 = vec_index(c, k);
+      v[k] = i4 < n4 ? reinterpret_cast<const float4*>(z)[i4]
+                     : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     }
-    block_argmax(bv, bi);
-    if (threadIdx.x == 0) {
-      ws.stat_m[(size_t)row * nch + c] = bv;
-      ws.stat_s[(size_t)row * nch + c] = __int_as_float(bi);
-    }
-  } else {
-    float m = -INFINITY, s = 0.f;
-    const bool vec = ((V & 3) == 0);
-    if (vec) {
-      const float4* z4 = reinterpret_cast<const float4*>(z);
-      for (int i = (i0 >> 2) + threadIdx.x; i < (i1 >> 2); i += kThreads) {
-        const float4 v = z4[i];
-        const float x0 = scaled(v.x, tf, unit), x1 = scaled(v.y, tf, unit);
-        const float x2 = scaled(v.z, tf, unit), x3 = scaled(v.w, tf, unit);
-        const float mx = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
-        if (mx > m) {
-          s = (m == -INFINITY) ? 0.f : s * exp2f((m - mx) * kLog2e);
-          m = mx;
-        }
-        s += exp2f((x0 - m) * kLog2e) + exp2f((x1 - m) * kLog2e) + exp2f((x2 - m) * kLog2e) +
-             exp2f((x3 - m) * kLog2e);
+    if (GREEDY) {
+#pragma unroll
+      for (int k = 0; k < kVecPerThread; ++k) {
+        const int i = 4 * vec_index(c, k);
+        if (i >= V) continue;
+        if (better(v[k].x, i, bv, bi)) bv = v[k].x, bi = i;
+        if (better(v[k].y, i + 1, bv, bi)) bv = v[k].y, bi = i + 1;
+        if (better(v[k].z, i + 2, bv, bi)) bv = v[k].z, bi = i + 2;
+        if (better(v[k].w, i + 3, bv, bi)) bv = v[k].w, bi = i + 3;
       }
     } else {
-      for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
-        const float x = scaled(z[i], tf, unit);
+#pragma unroll
+      for (int k = 0; k < kVecPerThread; ++k) {
+        v[k].x = scaled(v[k].x, tf, unit);
+        v[k].y = scaled(v[k].y, tf, unit);
+        v[k].z = scaled(v[k].z, tf, unit);
+        v[k].w = scaled(v[k].w, tf, unit);
+        m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
+      }
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int k = 0; k < kVecPerThread; ++k)
+          s += exp2f((v[k].x - m) * kLog2e) + exp2f((v[k].y - m) * kLog2e) + exp2f((v[k].z - m) * kLog2e) +
+               exp2f((v[k].w - m) * kLog2e);
+      }
+    }
+  } else {
+    const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
+    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
+      const float zi = z[i];
+      if (GREEDY) {
+        if (better(zi, i, bv, bi)) bv = zi, bi = i;
+      } else {
+        const float x = scaled(zi, tf, unit);
         if (x > m) {
           s = (m == -INFINITY) ? 0.f : s * exp2f((m - x) * kLog2e);
           m = x;
@@ -213,8 +280,23 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(const float* __rest
         s += exp2f((x - m) * kLog2e);
       }
     }
-    block_lse(m, s);
+  }
+  if (GREEDY) {
+    block_argmax(bv, bi);
     if (threadIdx.x == 0) {
+      ws.stat_m[(size_t)row * nch + c] = bv;
+      ws.stat_s[(size_t)row * nch + c] = __int_as_float(bi);
+    }
+  } else {
+    __shared__ float sm[kThreads / 64], ss[kThreads / 64];
+    wave_lse(m, s);
+    if ((threadIdx.x & 63) == 0) {
+      sm[threadIdx.x >> 6] = m;
+      ss[threadIdx.x >> 6] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int k = 1; k < kThreads / 64; ++k) lse_combine(m, s, sm[k], ss[k]);
       ws.stat_m[(size_t)row * nch + c] = m;
       ws.stat_s[(size_t)row * nch + c] = s;
     }
@@ -234,94 +316,75 @@ struct DecideArgs {
   float tf;
 };
 
-// Normalisers of one row: lanes combine the chunk partials.
-__device__ void row_norm(const SampleWs& ws, int row, int nch, bool greedy, float& m, float& s, int& amax) {
-  const int lane = threadIdx.x & 63;
-  if (greedy) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int c = lane; c < nch; c += 64) {
-      const float v = ws.stat_m[(size_t)row * nch + c];
-      const int i = __float_as_int(ws.stat_s[(size_t)row * nch + c]);
-      if (better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
-      }
-    }
-    wave_argmax(bv, bi);
-    amax = bi;
-    m = bv;
-    s = 0.f;
-  } else {
-    float mm = -INFINITY, ss = 0.f;
-    for (int c = lane; c < nch; c += 64) lse_combine(mm, ss, ws.stat_m[(size_t)row * nch + c], ws.stat_s[(size_t)row * nch + c]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float m2 = __shfl_xor(mm, o, 64), s2 = __shfl_xor(ss, o, 64);
-      lse_combine(mm, ss, m2, s2);
-    }
-    m = mm;
-    s = ss;
-    amax = -1;
-  }
-}
-
-// p[x] of a softmax row, float32 as torch.softmax produces it: exp(x - max) / sum.
+// p[x] of a softmax row, float32 as torch.softmax forms it: exp(x - max) / sum.
 __device__ __forceinline__ float softmax_at(float z, float m, float s, float tf) {
   const float x = tf == 1.0f ? z : z / tf;
   return expf(x - m) / s;
 }
 
-__global__ __launch_bounds__(64) void decide_kernel(DecideArgs a, SampleWs ws) {
-  const int b = blockIdx.x, lane = threadIdx.x;
-  const int C = a.gamma + 1, nch = num_chunks(a.V);
+__global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a, SampleWs ws) {
+  const int b = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int C = a.gamma + 1, nch = num_chunks(a.V), nrows = 2 * a.gamma + 1;
   const bool greedy = a.greedy && !a.is_probs;
-  const bool logits = !a.is_probs;
-  // Row normalisers for the decision rows (target 0..gamma, draft 0..gamma-1).
-  __shared__ float s_mt[33], s_st[33], s_md[32], s_sd[32];
-  __shared__ int s_at[33], s_ad[32];
-  if (logits) {
-    for (int j = 0; j < C; ++j) {
-      float m, s;
-      int am;
-      row_norm(ws, b * C + j, nch, greedy, m, s, am);
-      if (lane == 0) {
-        s_mt[j] = m;
-        s_st[j] = s;
-        s_at[j] = am;
-      }
-    }
-    for (int j = 0; j < a.gamma; ++j) {
-      float m, s;
-      int am;
-      row_norm(ws, a.B * C + b * a.gamma + j, nch, greedy, m, s, am);
-      if (lane == 0) {
-        s_md[j] = m;
-        s_sd[j] = s;
-        s_ad[j] = am;
+  // Row r < C: target row r; row C + j: draft row j.
+  __shared__ float s_m[65], s_s[65];
+  __shared__ int s_am[65];
+  __shared__ float s_zp[32], s_zq[32];
+  if (!a.is_probs) {
+    for (int r = w; r < nrows; r += blockDim.x >> 6) {
+      const int grow = r < C ? b * C + r : a.B * C + b * a.gamma + (r - C);
+      if (greedy) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int c = lane; c < nch; c += 64) {
+          const float v = ws.stat_m[(size_t)grow * nch + c];
+          const int i = __float_as_int(ws.stat_s[(size_t)grow * nch + c]);
+          if (better(v, i, bv, bi)) bv = v, bi = i;
+        }
+        wave_argmax(bv, bi);
+        if (lane == 0) s_am[r] = bi;
+      } else {
+        float mm = -INFINITY, ss = 0.f;
+        for (int c = lane; c < nch; c += 64)
+          lse_combine(mm, ss, ws.stat_m[(size_t)grow * nch + c], ws.stat_s[(size_t)grow * nch + c]);
+        wave_lse(mm, ss);
+        if (lane == 0) {
+          s_m[r] = mm;
+          s_s[r] = ss;
+        }
       }
     }
   }
+  // Gather the target / draft entries at the proposals, one lane each.
+  if (threadIdx.x < a.gamma) {
+    const int j = threadIdx.x;
+    const int x = a.proposals[(size_t)b * a.gamma + j];
+    float zp = 0.f, zq = 0.f;
+    if ((unsigned)x < (unsigned)a.V && !greedy) {  // an out-of-vocabulary proposal is never read
+      zp = a.target[((size_t)b * C + j) * a.V + x];
+      zq = a.draft[((size_t)b * a.gamma + j) * a.V + x];
+    }
+    s_zp[j] = zp;
+    s_zq[j] = zq;
+  }
   __syncthreads();
-  if (lane != 0) return;
+  if (threadIdx.x != 0) return;
 
   int k = a.gamma;
   for (int j = 0; j < a.gamma; ++j) {
     const int x = a.proposals[(size_t)b * a.gamma + j];
     float pp, qq;
-    const float* prow = a.target + ((size_t)b * C + j) * a.V;
-    const float* qrow = a.draft + ((size_t)b * a.gamma + j) * a.V;
     if ((unsigned)x >= (unsigned)a.V) {
-      pp = qq = 0.f;  // an out-of-vocabulary proposal is never read, only rejected
+      pp = qq = 0.f;
     } else if (a.is_probs) {
-      pp = prow[x];
-      qq = qrow[x];
+      pp = s_zp[j];
+      qq = s_zq[j];
     } else if (greedy) {
-      pp = s_at[j] == x ? 1.f : 0.f;
-      qq = s_ad[j] == x ? 1.f : 0.f;
+      pp = s_am[j] == x ? 1.f : 0.f;
+      qq = s_am[C + j] == x ? 1.f : 0.f;
     } else {
-      pp = softmax_at(prow[x], s_mt[j], s_st[j], a.tf);
-      qq = softmax_at(qrow[x], s_md[j], s_sd[j], a.tf);
+      pp = softmax_at(s_zp[j], s_m[j], s_s[j], a.tf);
+      qq = softmax_at(s_zq[j], s_m[C + j], s_s[C + j], a.tf);
     }
     const double qd = (double)qq, pd = (double)pp;
     const double acc = qd <= kEps ? (pd > kEps ? 1.0 : 0.0) : fmin(1.0, pd / qd);
@@ -340,14 +403,14 @@ __global__ __launch_bounds__(64) void decide_kernel(DecideArgs a, SampleWs ws) {
     // One-hot rows: the residual is one-hot at the target argmax (or equals p,
     // when both rows agree), and the bonus row is one-hot: the draw is the
     // target row's argmax for any positive finite E.
-    info.token = s_at[k];
+    info.token = s_am[k];
     info.mode = RACE_NONE;
-  } else if (logits) {
-    info.mp = s_mt[k];
-    info.sp = s_st[k];
+  } else if (!a.is_probs) {
+    info.mp = s_m[k];
+    info.sp = s_s[k];
     if (k < a.gamma) {
-      info.mq = s_md[k];
-      info.sq = s_sd[k];
+      info.mq = s_m[C + k];
+      info.sq = s_s[C + k];
     }
   }
   ws.info[b] = info;
@@ -360,10 +423,13 @@ __global__ __launch_bounds__(64) void decide_kernel(DecideArgs a, SampleWs ws) {
 struct RaceRows {
   const float* p;
   const float* q;
-  float mp, sp, mq, sq, tf;
-  bool probs;
-  __device__ __forceinline__ float pval(int i) const { return probs ? p[i] : softmax_at(p[i], mp, sp, tf); }
-  __device__ __forceinline__ float qval(int i) const { return probs ? q[i] : softmax_at(q[i], mq, sq, tf); }
+  float mp, isp, mq, isq, tf;
+  bool probs, unit;
+  __device__ __forceinline__ float prob(float z, float m, float is) const {
+    return probs ? z : exp2f((scaled(z, tf, unit) - m) * kLog2e) * is;
+  }
+  __device__ __forceinline__ float pval(float z) const { return prob(z, mp, isp); }
+  __device__ __forceinline__ float qval(float z) const { return prob(z, mq, isq); }
 };
 
 __device__ __forceinline__ RaceRows race_rows(const DecideArgs& a, const RaceInfo& info, int b) {
@@ -372,130 +438,163 @@ __device__ __forceinline__ RaceRows race_rows(const DecideArgs& a, const RaceInf
   r.p = a.target + ((size_t)b * C + info.k) * a.V;
   r.q = info.k < a.gamma ? a.draft + ((size_t)b * a.gamma + info.k) * a.V : nullptr;
   r.mp = info.mp;
-  r.sp = info.sp;
+  r.isp = 1.f / info.sp;
   r.mq = info.mq;
-  r.sq = info.sq;
+  r.isq = info.k < a.gamma ? 1.f / info.sq : 0.f;
   r.tf = a.tf;
   r.probs = a.is_probs;
+  r.unit = a.tf == 1.0f;
   return r;
 }
 
-// ------------------------------------------------------------ 3. resid sum
-__global__ __launch_bounds__(kThreads) void resid_sum_kernel(DecideArgs a, SampleWs ws) {
-  const int c = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
-  const RaceInfo info = ws.info[b];
-  if (info.mode != RACE_RESIDUAL) return;
-  const RaceRows rr = race_rows(a, info, b);
-  const int i0 = c * kChunk, i1 = min(a.V, i0 + kChunk);
-  double rs = 0.0, ps = 0.0;
-  for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
-    const float p = rr.pval(i), q = rr.qval(i);
-    const float d = p - q;
-    const float r = d < 0.f ? 0.f : d;  // torch.clamp(p - q, min=0): NaN stays NaN
-    rs += (double)r;
-    ps += (double)p;
-  }
-  __shared__ double s_r[kThreads / 64], s_p[kThreads / 64];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    rs += __shfl_xor(rs, o, 64);
-    ps += __shfl_xor(ps, o, 64);
-  }
-  if ((threadIdx.x & 63) == 0) {
-    s_r[threadIdx.x >> 6] = rs;
-    s_p[threadIdx.x >> 6] = ps;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double tr = 0.0, tp = 0.0;
-    for (int k = 0; k < kThreads / 64; ++k) {
-      tr += s_r[k];
-      tp += s_p[k];
-    }
-    ws.rsum[((size_t)b * nch + c) * 2] = tr;
-    ws.rsum[((size_t)b * nch + c) * 2 + 1] = tp;
-  }
-}
-
-// ---------------------------------------------------------------- 4. race
+// ---------------------------------------------------------------- 3. race
 __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, const float* __restrict__ noise,
                                                         SampleWs ws) {
   const int c = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
   const RaceInfo info = ws.info[b];
   if (info.mode == RACE_NONE) return;
   const RaceRows rr = race_rows(a, info, b);
-  // Residual normaliser: fp32 sum (accumulated in fp64, rounded once).
-  bool use_resid = false, fallback = false;
-  float t = 0.f, psum = 0.f;
-  if (info.mode == RACE_RESIDUAL) {
-    double tr = 0.0, tp = 0.0;
-    for (int k = 0; k < nch; ++k) {
-      tr += ws.rsum[((size_t)b * nch + k) * 2];
-      tp += ws.rsum[((size_t)b * nch + k) * 2 + 1];
-    }
-    t = (float)tr;
-    psum = fmaxf((float)tp, 1e-12f);  // p.sum().clamp_min(1e-12)
-    fallback = (double)t <= kEps;
-    use_resid = !fallback;
-  }
+  const bool resid = info.mode == RACE_RESIDUAL;
   const float* e = noise + (size_t)b * a.V;
-  const int i0 = c * kChunk, i1 = min(a.V, i0 + kChunk);
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
-    const float p = rr.pval(i);
-    float rhat;
-    if (use_resid) {
-      const float d = p - rr.qval(i);
-      rhat = (d < 0.f ? 0.f : d) / t;
-    } else if (fallback) {
-      rhat = p / psum;
-    } else {
-      rhat = p;
+  Top2 t2;
+  t2.init();
+  float rs = 0.f, ps = 0.f;
+  auto visit = [&](int i, float zp, float zq, float ei) {
+    const float p = rr.pval(zp);
+    float r = p;
+    if (resid) {
+      const float d = p - rr.qval(zq);
+      r = d < 0.f ? 0.f : d;  // torch.clamp(p - q, min=0): NaN stays NaN
+      rs += r;
+      ps += p;
     }
-    const float key = rhat / e[i];
-    if (better(key, i, bv, bi)) {
-      bv = key;
-      bi = i;
+    t2.push(r / ei, i);
+  };
+  if ((a.V & 3) == 0) {
+    const int n4 = a.V >> 2;
+    float4 zp[kVecPerThread], zq[kVecPerThread], ev[kVecPerThread];
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i4 = vec_index(c, k);
+      if (i4 < n4) {
+        zp[k] = reinterpret_cast<const float4*>(rr.p)[i4];
+        zq[k] = resid ? reinterpret_cast<const float4*>(rr.q)[i4] : zp[k];
+        ev[k] = reinterpret_cast<const float4*>(e)[i4];
+      }
     }
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i4 = vec_index(c, k);
+      if (i4 >= n4) continue;
+      visit(4 * i4 + 0, zp[k].x, zq[k].x, ev[k].x);
+      visit(4 * i4 + 1, zp[k].y, zq[k].y, ev[k].y);
+      visit(4 * i4 + 2, zp[k].z, zq[k].z, ev[k].z);
+      visit(4 * i4 + 3, zp[k].w, zq[k].w, ev[k].w);
+    }
+  } else {
+    const int i0 = c * kChunk, i1 = min(a.V, i0 + kChunk);
+    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) visit(i, rr.p[i], resid ? rr.q[i] : 0.f, e[i]);
   }
-  block_argmax(bv, bi);
+  t2.wave_reduce();
+  __shared__ float s_v1[kThreads / 64], s_v2[kThreads / 64];
+  __shared__ int s_i1[kThreads / 64], s_i2[kThreads / 64];
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_v1[w] = t2.v1;
+    s_v2[w] = t2.v2;
+    s_i1[w] = t2.i1;
+    s_i2[w] = t2.i2;
+  }
+  const double rsum = block_sum_f64((double)rs);
+  const double psum = block_sum_f64((double)ps);
   if (threadIdx.x == 0) {
-    ws.race_v[(size_t)b * nch + c] = bv;
-    ws.race_i[(size_t)b * nch + c] = bi;
+    for (int k = 1; k < kThreads / 64; ++k) t2.merge(s_v1[k], s_i1[k], s_v2[k], s_i2[k]);
+    RacePart part;
+    part.v1 = t2.v1;
+    part.v2 = t2.v2;
+    part.i1 = t2.i1;
+    part.i2 = t2.i2;
+    part.rsum = rsum;
+    part.psum = psum;
+    ws.race[(size_t)b * nch + c] = part;
   }
 }
 
-// ------------------------------------------------------------ 5. finalize
+// ------------------------------------------------------------ 4. finalize
 struct CommitArgs {
   const int32_t* start;
   const int32_t* remaining;
+  const float* noise;
   int eos;
   int32_t* n_commit;
   int32_t* finished;
   int32_t* new_len;
 };
 
-__global__ __launch_bounds__(64) void finalize_kernel(DecideArgs a, CommitArgs cm, SampleWs ws) {
-  const int b = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(kThreads) void finalize_kernel(DecideArgs a, CommitArgs cm, SampleWs ws) {
+  const int b = blockIdx.x;
   const int C = a.gamma + 1, nch = num_chunks(a.V);
   const RaceInfo info = ws.info[b];
   int token = info.token;
   if (info.mode != RACE_NONE) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int c = lane; c < nch; c += 64) {
-      const float v = ws.race_v[(size_t)b * nch + c];
-      const int i = ws.race_i[(size_t)b * nch + c];
-      if (better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
+    __shared__ int s_token, s_exact;
+    __shared__ float s_t, s_psum;
+    if (threadIdx.x < 64) {
+      Top2 t2;
+      t2.init();
+      double rs = 0.0, ps = 0.0;
+      for (int c = threadIdx.x; c < nch; c += 64) {
+        const RacePart part = ws.race[(size_t)b * nch + c];
+        t2.merge(part.v1, part.i1, part.v2, part.i2);
+        rs += part.rsum;
+        ps += part.psum;
+      }
+      t2.wave_reduce();
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        rs += __shfl_xor(rs, o, 64);
+        ps += __shfl_xor(ps, o, 64);
+      }
+      if (threadIdx.x == 0) {
+        int exact = 0;
+        if (info.mode == RACE_RESIDUAL) {
+          const float t = (float)rs;  // fp32 sum, accumulated in fp64 and rounded once
+          s_t = t;
+          s_psum = fmaxf((float)ps, 1e-12f);  // p.sum().clamp_min(1e-12)
+          if ((double)t <= kEps) exact = 2;                      // race p / sum(p) instead
+          else if (!isnan(t2.v1) && !(t2.v1 - t2.v2 > kTieRel * t2.v1)) exact = 1;  // near tie
+        }
+        s_exact = exact;
+        s_token = t2.i1;
       }
     }
-    wave_argmax(bv, bi);
-    token = bi;
+    __syncthreads();
+    if (s_exact) {
+      // Exact race over the whole row with the normaliser known (rare).
+      const RaceRows rr = race_rows(a, info, b);
+      const float* e = cm.noise + (size_t)b * a.V;
+      const float t = s_t, psum = s_psum;
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
+        const float p = rr.pval(rr.p[i]);
+        float rhat;
+        if (s_exact == 2) {
+          rhat = p / psum;
+        } else {
+          const float d = p - rr.qval(rr.q[i]);
+          rhat = (d < 0.f ? 0.f : d) / t;
+        }
+        const float key = rhat / e[i];
+        if (better(key, i, bv, bi)) bv = key, bi = i;
+      }
+      block_argmax(bv, bi);
+      token = bi;
+    } else {
+      token = s_token;
+    }
   }
-  if (lane != 0) return;
+  if (threadIdx.x != 0) return;
   const int k = info.k;
   a.out_tokens[(size_t)b * C + k] = token;
   // Commit cut (spec_scheduler.py:274-303): budget with Python slice semantics,
@@ -666,7 +765,7 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
                       int32_t V, int32_t* accept_len, int32_t* out_tokens, int32_t* n_commit, int32_t* finished,
                       int32_t* new_len, double* accept_prob, int32_t decide_only, void* workspace,
                       size_t workspace_bytes, void* stream) {
-  if (!target || !draft || !proposals || !u_accept || B < 0 || gamma < 1 || gamma > 32 || V < 1)
+  if (!target || !draft || !proposals || !u_accept || B < 0 || B > 65535 || gamma < 1 || gamma > 32 || V < 1)
     return SPV_ERR_ARG;
   if (decide_only && !accept_prob) return SPV_ERR_ARG;
   if (!decide_only && (!accept_len || !out_tokens)) return SPV_ERR_ARG;
@@ -679,6 +778,7 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
   ws_layout(B, gamma, V, &ws, workspace);
   hipStream_t s = (hipStream_t)stream;
   const int nch = num_chunks(V);
+  if ((size_t)B * (2 * gamma + 1) > 65535) return SPV_ERR_ARG;
   DecideArgs a{};
   a.target = target;
   a.draft = draft;
@@ -704,17 +804,15 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
                          ws);
     SPV_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(64), 0, s, a, ws);
+  hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kThreads), 0, s, a, ws);
   SPV_CHECK_LAUNCH();
   if (decide_only) return SPV_OK;
   if (!greedy) {
-    hipLaunchKernelGGL(resid_sum_kernel, dim3(nch, B), dim3(kThreads), 0, s, a, ws);
-    SPV_CHECK_LAUNCH();
     hipLaunchKernelGGL(race_kernel, dim3(nch, B), dim3(kThreads), 0, s, a, exp_noise, ws);
     SPV_CHECK_LAUNCH();
   }
-  CommitArgs cm{start_pos, remaining, eos_id, n_commit, finished, new_len};
-  hipLaunchKernelGGL(finalize_kernel, dim3(B), dim3(64), 0, s, a, cm, ws);
+  CommitArgs cm{start_pos, remaining, exp_noise, eos_id, n_commit, finished, new_len};
+  hipLaunchKernelGGL(finalize_kernel, dim3(B), dim3(kThreads), 0, s, a, cm, ws);
   SPV_CHECK_LAUNCH();
   return SPV_OK;
 }

@@ -189,13 +189,15 @@ def test_lifo_order_and_exhaustion_match_oracle(cuda):
     gpu.clear(1)
     cpu.clear(1)
     _same_state(gpu, cpu)
-    # exhaustion mid-batch: 2 + 4 blocks needed, 5 free
-    k = torch.zeros(2, 7, 1, 2, device=cuda)
+    # exhaustion mid-batch: seq 0 needs 4 more blocks, seq 1 needs 5, 7 are free
+    assert gpu.allocator.num_free == 7
+    k = torch.zeros(2, 9, 1, 2, device=cuda)
     with pytest.raises(BlockExhaustedError):
         gpu.write_block(0, [0, 1], [1, 0], k, k)
     with pytest.raises(ref.BlockExhaustedError):
-        cpu.write_block(0, [0, 1], [1, 0], None, None, chunk=7)
+        cpu.write_block(0, [0, 1], [1, 0], None, None, chunk=9)
     _same_state(gpu, cpu)
+    assert gpu.seq_lengths == [10, 6] and len(gpu.block_tables[1]) == 3
 
 
 def _random_trace(cuda, seed, n_ops=120, bs=4, cap=40, n_seq=6, dtype=torch.float32):
