@@ -222,9 +222,14 @@ constexpr int kMfmaWGsMax = 512;
 __host__ __device__ constexpr int mfma_wgs(int) { return kMfmaWGsMax; }
 // Register page buffers per wave: three pages in flight up to 48 query rows.
 __host__ __device__ constexpr int page_bufs(int nt) { return nt >= 4 ? 2 : 4; }
+constexpr int kTabChunk = 512;  // block ids staged in LDS per window
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 // s_pref[b] = pages (per segment) of sequences before b; s_pref[B] = total.
@@ -283,6 +288,10 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p
   __shared__ float sm_m[2][RPG];
   __shared__ float sm_l[2][RPG];
   __shared__ float sm_o[RPG][D + 4];
+  // Block ids of the pages being walked. Reading them from LDS keeps the page
+  // loads in flight: a vector load of a table entry would need vmcnt(0), which
+  // also waits for every prefetched page.
+  __shared__ int sTab[kTabChunk];
 
   // Waves 2k and 2k+1 form pair k: both compute S^T and the softmax of the
   // pair's pages; wave half `hf` accumulates O^T for dimensions [hf*d/2, (hf+1)*d/2).
@@ -315,8 +324,10 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p
     const int nr = min(RPG, p.G - qr0);
     const int32_t* table = p.tables + (size_t)uni(p.seq_ids[b]) * p.maxb;
 
-    // Stage the segment's query rows (zero rows past nr).
+    // Stage the segment's query rows (zero rows past nr) and the first block ids.
     __syncthreads();
+    for (int t = threadIdx.x; t < min(kTabChunk, lp1 - lp0); t += blockDim.x)
+      sTab[t] = safe_block(p, table[lp0 + t]);
     for (int idx = threadIdx.x; idx < RPG * (D / 8); idx += blockDim.x) {
       const int rr = idx / (D / 8), c = idx - rr * (D / 8);
       uint4 v = make_uint4(0, 0, 0, 0);
@@ -345,8 +356,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p
       l[nt] = 0.f;
     }
 
+    int tab0 = lp0;  // first page whose block id is sTab[0]
     auto load_page = [&](PageFrag<NT, D>& f, int page) {
-      const int phys = uni(safe_block(p, table[page]));
+      const int phys = uni(sTab[page - tab0]);
       const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
       const uint16_t* kp = kbase + slot;
       const uint16_t* vp = vbase + slot;
@@ -386,40 +398,49 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p
         }
       }
       const bool need_mask = page * BS + BS - 1 > start;
+      bf16x8_t va[MTH];  // {V^T, V^T}: the same keys in both halves of the k-slots
+#pragma unroll
+      for (int mt = 0; mt < MTH; ++mt)
+        va[mt] = __builtin_bit_cast(bf16x8_t, make_uint4(f.v[mt].x, f.v[mt].y, f.v[mt].x, f.v[mt].y));
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         float x4[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          x4[jj] = sc[nt][jj] * sl2;
-          if (need_mask && kpos0 + jj > start + jrow[nt]) x4[jj] = -INFINITY;
+        for (int jj = 0; jj < 4; ++jj) x4[jj] = sc[nt][jj] * sl2;
+        if (need_mask) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) x4[jj] = kpos0 + jj > start + jrow[nt] ? -INFINITY : x4[jj];
         }
         float mx = fmaxf(fmaxf(x4[0], x4[1]), fmaxf(x4[2], x4[3]));
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m[nt], mx);
-        float alpha, e[4];
-        if (m_new == -INFINITY) {
-          alpha = 1.f;
-          e[0] = e[1] = e[2] = e[3] = 0.f;
-        } else {
-          alpha = exp2f(m[nt] - m_new);
+        // Rescale only when some query column's running max grew (rare after the
+        // first pages); a column whose max did not grow gets alpha = 1.
+        if (__any(mx > m[nt])) {
+          const float m_new = fmaxf(m[nt], mx);
+          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[nt] - m_new);
+          l[nt] *= alpha;
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) e[jj] = exp2f(x4[jj] - m_new);
+          for (int mt = 0; mt < MTH; ++mt) o[mt][nt] *= alpha;
+          m[nt] = m_new;
         }
-        l[nt] = l[nt] * alpha + ((e[0] + e[1]) + (e[2] + e[3]));
-        m[nt] = m_new;
+        const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
+        float e[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(x4[jj] - mu);
+        l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
         // P = hi + lo, both bf16: slots 0..3 carry hi, 4..7 lo of the same keys,
         // so one 16x16x32 MFMA against {V, V} accumulates P V to ~16 bits.
-        uint32_t hw0 = pack2_bf16(e[0], e[1]), hw1 = pack2_bf16(e[2], e[3]);
-        const uint32_t lw0 = pack2_bf16(e[0] - bf16_to_f32(hw0 & 0xffffu), e[1] - bf16_to_f32(hw0 >> 16));
-        const uint32_t lw1 = pack2_bf16(e[2] - bf16_to_f32(hw1 & 0xffffu), e[3] - bf16_to_f32(hw1 >> 16));
-        const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, make_uint4(hw0, hw1, lw0, lw1));
+        const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
+        const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
+        const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
+        const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
+        const bf16x8_t pf = __builtin_bit_cast(
+            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
+                                 pack2_bf16(r01[0], r01[1]), pack2_bf16(r23[0], r23[1])));
 #pragma unroll
-        for (int mt = 0; mt < MTH; ++mt) {
-          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(f.v[mt].x, f.v[mt].y, f.v[mt].x, f.v[mt].y));
-          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf, o[mt][nt] * alpha, 0, 0, 0);
-        }
+        for (int mt = 0; mt < MTH; ++mt)
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[mt], pf, o[mt][nt], 0, 0, 0);
       }
     };
 
@@ -427,18 +448,27 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p
     // buffers keep kPageBufs - 1 pages in flight while one is computed.
     constexpr int kPageBufs = page_bufs(NT);
     PageFrag<NT, D> buf[kPageBufs];
-    const int pg0 = lp0 + pair;
+    // Shares longer than kTabChunk pages are walked in windows of block ids.
+    for (; tab0 < lp1; tab0 += kTabChunk) {
+      const int wend = min(lp1, tab0 + kTabChunk);
+      if (tab0 != lp0) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < wend - tab0; t += blockDim.x) sTab[t] = safe_block(p, table[tab0 + t]);
+        __syncthreads();
+      }
+      const int pg0 = tab0 + pair;
 #pragma unroll
-    for (int u = 0; u < kPageBufs - 1; ++u)
-      if (pg0 + 2 * u < lp1) load_page(buf[u], pg0 + 2 * u);
-    for (int it = 0; pg0 + 2 * it < lp1; it += kPageBufs) {
+      for (int u = 0; u < kPageBufs - 1; ++u)
+        if (pg0 + 2 * u < wend) load_page(buf[u], pg0 + 2 * u);
+      for (int it = 0; pg0 + 2 * it < wend; it += kPageBufs) {
 #pragma unroll
-      for (int u = 0; u < kPageBufs; ++u) {
-        const int pg = pg0 + 2 * (it + u);
-        if (pg < lp1) {
-          const int nxt = pg + 2 * (kPageBufs - 1);
-          if (nxt < lp1) load_page(buf[(u + kPageBufs - 1) % kPageBufs], nxt);
-          compute_page(buf[u], pg);
+        for (int u = 0; u < kPageBufs; ++u) {
+          const int pg = pg0 + 2 * (it + u);
+          if (pg < wend) {
+            const int nxt = pg + 2 * (kPageBufs - 1);
+            if (nxt < wend) load_page(buf[(u + kPageBufs - 1) % kPageBufs], nxt);
+            compute_page(buf[u], pg);
+          }
         }
       }
     }
@@ -534,14 +564,17 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p
 
 // Combine the partial slots of every segment that more than one workgroup saw.
 // Workgroups with an empty share (fewer pages than workgroups) wrote nothing
-// and are skipped. Per workgroup of this kernel: one segment, all its rows.
+// and are skipped. Grid: (segment, block of kMergeRows rows).
+constexpr int kMergeRows = 8;
+constexpr int kMergeSlots = 32;  // slots staged in LDS; more fall back to direct loops
+
 template <int QT>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_slots_kernel(AttnParams p, int nw) {
   extern __shared__ int s_pref[];
   __shared__ int s_scan[kAttnThreads / 64];
-  __shared__ float s_f[64][33];   // per row, per contributing slot: exp2(m - M)
-  __shared__ float s_inv[64];     // per row: 1 / sum(l * f)
-  __shared__ int s_slot[32];
+  __shared__ float s_f[kMergeRows][kMergeSlots];  // exp2(m_k - M) per row and slot
+  __shared__ float s_inv[kMergeRows];              // 1 / sum_k l_k f_k
+  __shared__ int s_slot[kMergeSlots];
   __shared__ int s_ns;
   build_page_prefix(p, s_pref, s_scan);
   const long long HR = (long long)p.Hkv * p.nrg;
@@ -553,32 +586,47 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_slots_kernel(AttnPara
   const int w0 = wg_of_page(seg0, T, nw), w1 = wg_of_page(seg0 + np - 1, T, nw);
   if (w0 == w1) return;
   const int h = hr / p.nrg, rg = hr - h * p.nrg;
-  const int qr0 = rg * p.rows_per_group;
-  const int nr = min(p.rows_per_group, p.G - qr0);
+  // Signed: a trailing row block of a padded group has no rows (nr <= 0).
+  const int row0 = (int)blockIdx.y * kMergeRows;
+  const int qr0 = rg * p.rows_per_group + row0;
+  const int nr = min(kMergeRows, min(p.rows_per_group, p.G - rg * p.rows_per_group) - row0);
+  if (nr <= 0) return;
   const int D = p.d;
-  if (w1 - w0 < 32) {
-    // Common case: the contributing slots fit LDS; scale factors once per row.
-    if (threadIdx.x == 0) {
-      int ns = 0;
-      for (int k = w0; k <= w1; ++k)
-        if ((long long)k * T / nw < (long long)(k + 1) * T / nw) s_slot[ns++] = k + seg;
-      s_ns = ns;
-    }
-    __syncthreads();
-    const int ns = s_ns;
-    for (int idx = threadIdx.x; idx < nr; idx += blockDim.x) {
-      const int r = qr0 + idx;
-      float M = -INFINITY;
-      for (int k = 0; k < ns; ++k) M = fmaxf(M, p.part_ml[((size_t)s_slot[k] * p.G + r) * 2]);
-      float Lsum = 0.f;
-      for (int k = 0; k < ns; ++k) {
-        const size_t base = (size_t)s_slot[k] * p.G + r;
-        const float ms = p.part_ml[base * 2];
-        const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
-        s_f[idx][k] = f;
-        Lsum += p.part_ml[base * 2 + 1] * f;
+  if (threadIdx.x == 0) {
+    int ns = 0;
+    for (int k = w0; k <= w1; ++k)
+      if ((long long)k * T / nw < (long long)(k + 1) * T / nw) {
+        if (ns < kMergeSlots) s_slot[ns] = k + seg;
+        ++ns;
       }
-      s_inv[idx] = 1.f / Lsum;
+    s_ns = ns;
+  }
+  __syncthreads();
+  const int ns = s_ns;
+  if (ns <= kMergeSlots) {
+    // One lane per (row, slot): the m / l of all slots are read in parallel.
+    const int lane = threadIdx.x & 63;
+    for (int base = 0; base < nr * kMergeSlots; base += blockDim.x) {
+      const int idx = base + threadIdx.x;
+      const int rr = idx / kMergeSlots, k = idx - rr * kMergeSlots;
+      float mk = -INFINITY, lk = 0.f;
+      if (rr < nr && k < ns) {
+        const size_t bse = (size_t)s_slot[k] * p.G + qr0 + rr;
+        mk = p.part_ml[bse * 2];
+        lk = p.part_ml[bse * 2 + 1];
+      }
+      // rows occupy 32-lane halves of a wave: reduce within the half
+      float M = mk;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+      const float f = mk == -INFINITY ? 0.f : exp2f(mk - M);
+      float L = lk * f;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+      if (rr < nr) {
+        s_f[rr][k] = f;
+        if ((lane & 31) == 0) s_inv[rr] = 1.f / L;
+      }
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < nr * (D / 4); idx += blockDim.x) {
@@ -810,7 +858,7 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
     const int nseg = B * num_kv_heads * pl.nrg;
     const int nwg = mfma_wgs(pl.nt);
     const size_t smem = (size_t)(B + 1) * sizeof(int);
-    const dim3 mgrid(nseg);
+    const dim3 mgrid(nseg, (pl.rows_per_group + kMergeRows - 1) / kMergeRows);
     switch (q_dtype) {
       case SPV_F32:
         hipLaunchKernelGGL(attn_merge_slots_kernel<SPV_F32>, mgrid, dim3(kAttnThreads), smem, s, p, nwg);

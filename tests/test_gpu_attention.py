@@ -180,6 +180,25 @@ def test_stale_nan_beyond_context_never_leaks(cuda):
     assert torch.allclose(out32, ref_attn.extend_attention_dense(q32, k32, v32, lens, 4), atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("C,Hq", [(6, 12), (3, 12), (7, 16)])
+def test_output_writes_stay_inside_the_batch(cuda, C, Hq):
+    # G = 36 / 18 rows leave padded query tiles; the output buffer sits between
+    # guard regions that must come back untouched, and every row is written.
+    lens, Hkv, d = [300, 17, 1000, 0, 129], 2, 128
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.bfloat16, seed=12)
+    B = len(lens)
+    q = torch.randn(B, C, Hq, d, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16)
+    n, guard = B * C * Hq * d, 4096
+    buf = torch.full((n + 2 * guard,), 3.0, dtype=torch.bfloat16, device=cuda)
+    buf[guard:guard + n] = float("nan")
+    out = buf[guard:guard + n].view(B, C, Hq, d)
+    verify_attention(q.to(cuda), gpu, 0, list(range(B)), lens, max(lens) + C, out=out)
+    host = buf.float().cpu()
+    assert bool((host[:guard] == 3.0).all()) and bool((host[guard + n:] == 3.0).all())
+    assert bool(torch.isfinite(host[guard:guard + n]).all())
+    _bf16_check(out, ref_attn.extend_attention_dense(q, keys, values, lens, Hq))
+
+
 def test_split_count_does_not_change_result(cuda):
     # The same batch with max_ctx raised (more, partly empty splits) gives the same output.
     lens, C, Hq, Hkv, d = [700, 33], 6, 12, 2, 128
