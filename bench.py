@@ -59,13 +59,48 @@ def sample_bytes(batch):
     return batch * ((C + GAMMA) * VOCAB * 4 + VOCAB * 4 + GAMMA * 8 + 12)
 
 
+def workload_lens(seed=0):
+    """Context lengths of the batch, U[256, 4096]; the generator continues into
+    the block-table permutation."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(256, 4097, (B,), generator=g).tolist(), g
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_attn_qwen15_b32_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per verify-attention call from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel factor), or None
+    when the summary was taken on a different verify_attn.hip."""
+    import hashlib
+
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+        src = open(os.path.join(PKG, "csrc", "verify_attn.hip"), "rb").read()
+    except OSError:
+        return None
+    fields = {}
+    for line in text.splitlines():
+        if ":" in line:
+            k, v = line.split(":", 1)
+            fields[k.strip()] = v.strip().strip("`")
+    if fields.get("verify_attn.hip source hash") != hashlib.sha256(src).hexdigest()[:16]:
+        return None
+    try:
+        return int(float(fields["traffic_bytes_per_call"]))
+    except (KeyError, ValueError):
+        return None
+
+
 def build_workload(dev, seed=0):
     import torch
 
     from engine.kv import PagedKVCache
 
-    g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(256, 4097, (B,), generator=g).tolist()
+    lens, g = workload_lens(seed)
     perm = torch.randperm(CAP, generator=g).tolist()
     tables, pos = [], 0
     for L in lens:
@@ -306,7 +341,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "cpu_baseline": None,
     }

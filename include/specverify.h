@@ -127,7 +127,14 @@ int spv_kv_read_blocks(const void* pool, int is_value, int kv_dtype,
 
 /* ------------------------------------------------------------- attention */
 
-/* Workspace needed by spv_verify_attn for contexts up to max_ctx tokens. */
+/* Bytes at the head of the attention workspace that hold per-segment arrival
+ * counters. They must be zero when a workspace is first used (allocate it
+ * zero-filled); every call leaves them zero again. Calls that share one
+ * workspace must be ordered (one stream), as they also share its partials. */
+#define SPV_ATTN_COUNTER_BYTES (1 << 18)
+
+/* Workspace needed by spv_verify_attn for contexts up to max_ctx tokens
+ * (0 when the call needs none). */
 size_t spv_verify_attn_workspace_bytes(int32_t B, int32_t C, int32_t num_q_heads,
                                        int32_t num_kv_heads, int32_t head_dim,
                                        int32_t block_size, int32_t max_ctx);

@@ -7,14 +7,14 @@
 //
 // Work decomposition (MFMA path): all G = C * (Hq/Hkv) query rows that share a
 // kv head are processed together, so every K/V page is read from HBM once per kv
-// head and reused for all G rows. A persistent grid of workgroups splits the
-// flattened (sequence, kv head, page) list into equal contiguous shares; shares
-// that cut a sequence produce (m, l, O) partials in log2 units that a small merge
-// kernel combines, and a sequence seen by one workgroup is written directly.
+// head and reused for all G rows. A persistent grid (one workgroup per CU)
+// splits the flattened (sequence, kv head, page) list into equal contiguous
+// shares; a sequence cut by share boundaries is combined by whichever of its
+// workgroups finishes last, inside the same kernel.
 //
 // MFMA path (bf16 K/V, head_dim 64/128, block_size 16, G >= 16), per page:
 //   S^T = K Q^T  with v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims straight
-//         from the K page, B = Q^T from the LDS-staged query rows);
+//         from the K page, B = Q^T fragments held in registers);
 //   O^T += V^T P^T with v_mfma_f32_16x16x32_bf16 where A = {V^T, V^T} straight
 //         from the transposed V page and B = {P_hi^T, P_lo^T}: P is split into
 //         two bf16 halves so P V is accumulated to ~16 bits, not bf16's 8.
@@ -22,7 +22,7 @@
 // 4*(l/16)+0..3 of query column l%16), so the online-softmax rescale stays
 // inside a lane; the row max needs two cross-lane steps (xor 16, 32).
 // VALU path: any dtype / head_dim <= 256 / block size, fp32 math with LDS tiles,
-// a (sequence, kv head, row group, split) grid and its own merge.
+// a (sequence, kv head, row group, split) grid and its own merge kernel.
 #include <math.h>
 
 #include "spv_common.h"
@@ -32,10 +32,16 @@ using namespace spv;
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kAttnThreads = 256;
+
+// Workspace layout, shared by both paths: arrival counters of the MFMA path
+// (zero between calls), then the partial (m, l) rows, then the partial O rows.
+constexpr int kCounterWords = SPV_ATTN_COUNTER_BYTES / 4;
 
 struct AttnParams {
   void* out;
@@ -46,8 +52,9 @@ struct AttnParams {
   const int32_t* tables;
   const int32_t* seq_ids;
   const int32_t* start;
-  float* part_o;   // [B][Hkv][max_splits][G][d]
-  float* part_ml;  // [B][Hkv][max_splits][G][2]  (m in log2 units, l)
+  int* counters;   // MFMA path: pages finished per segment, [B][Hkv][nrg]
+  float* part_o;   // partial rows x d
+  float* part_ml;  // partial rows x 2 (m in log2 units, l)
   int maxb, B, C, Hq, Hkv, ratio, G, d, bs, layer, cap;
   int pages_per_split, max_splits, nrg, rows_per_group;
   int max_pages;     // ceil(max_ctx / block_size): no table entry beyond it is read
@@ -207,440 +214,223 @@ __global__ __launch_bounds__(kAttnThreads) void attn_valu_kernel(AttnParams p) {
 
 // ------------------------------------------------------------------ MFMA path
 //
-// Persistent, length-balanced decomposition. Every (sequence b, kv head h,
-// row group rg) is a "segment" of npages(b) pages; segments are laid end to end
-// in (b, h, rg) order and the resident workgroups each take an equal contiguous
-// share of that page list, so ragged context lengths cost no tail. A workgroup
-// walks the segments its share touches: it stages the segment's query rows in
-// LDS, its two wave pairs take every other page (three pages in flight per
-// wave in rotating register buffers), the waves merge through LDS, and the workgroup writes either the
-// final output (it covered the whole segment) or a partial (m, l, O) into slot
-// `workgroup + segment` (unique along the staircase of shares). The merge
-// kernel combines the contiguous run of slots of every split segment.
-// Resident workgroups on 256 CUs (two per CU) and register page buffers per wave.
-constexpr int kMfmaWGsMax = 512;
-__host__ __device__ constexpr int mfma_wgs(int) { return kMfmaWGsMax; }
-// Register page buffers per wave: three pages in flight up to 48 query rows.
-__host__ __device__ constexpr int page_bufs(int nt) { return nt >= 4 ? 2 : 4; }
-constexpr int kTabChunk = 512;  // block ids staged in LDS per window
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// Persistent, length-balanced decomposition. Every (sequence b, kv head h, row
+// group rg) is a "segment" of npages(b) pages; segments are laid end to end in
+// (b, h, rg) order and the workgroups (one per CU) each take an equal
+// contiguous share of that page list, so ragged context lengths cost no tail.
+// A workgroup walks the segments its share touches. Per segment each of its
+// eight waves takes every eighth page of the share and holds the whole head
+// dimension: a ring of register page buffers (all but one in flight while one
+// is computed) and the O^T accumulators; the query rows are staged in LDS.
+// The waves combine through LDS. A workgroup that saw the whole segment writes
+// the output; otherwise it writes a partial (m, l, O) into slot
+// `share + segment` (unique along the staircase of shares) and adds its page
+// count to the segment's arrival counter. The workgroup that completes the
+// count merges the segment's partials and sets the counter back to zero, so the
+// counters are zero between calls.
+constexpr int kMfmaWGsMax = 512;  // bound on the persistent grid (slot numbering)
+constexpr int kMfmaMaxB = 512;    // the page and piece prefixes of the batch live in LDS
+// Register page buffers per wave: one page in flight while one is computed.
+// One workgroup of eight waves per CU (two per SIMD, <= 256 registers each, so
+// every operand stays in VGPRs) keeps eight pages in flight per CU.
+__host__ __device__ constexpr int ring_depth(int, int) { return 2; }
+constexpr int kMfmaThreads = 512;
+constexpr int kTabChunk = 512;    // block ids staged in LDS per window
+constexpr int kMergeSlots = 32;   // partial slots staged in LDS by the merging workgroup
+// log2 units a score may exceed its column's reference before O is rescaled.
+constexpr float kSlack = 8.f;
 
 // Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
-// s_pref[b] = pages (per segment) of sequences before b; s_pref[B] = total.
-__device__ void build_page_prefix(const AttnParams& p, int* s_pref, int* scan_tmp) {
-  int carry = 0;
-  for (int base = 0; base < p.B; base += blockDim.x) {
-    const int b = base + threadIdx.x;
-    const int np = b < p.B ? context_pages(p, p.start[b] + p.C) : 0;
-    int total;
-    const int off = block_exclusive_scan(np, scan_tmp, &total);
-    if (b < p.B) s_pref[b] = carry + off;
-    carry += total;
-  }
-  if (threadIdx.x == 0) s_pref[p.B] = carry;
-  __syncthreads();
+// Partials cross workgroups (and XCDs, whose L2s are not coherent with each
+// other): they are written and read with device-scope atomic accesses, which
+// go to the device coherence point (sc1), so publishing them needs only their
+// completion, not a write-back of the whole L2.
+__device__ __forceinline__ void store_coherent(float* dst, float a, float b) {
+  const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_coherent(const float* src) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
 }
 
 // Values that are the same in every lane of a wave, moved to scalar registers
 // so that page addresses become scalar base + lane offset.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Largest b with hr_count * s_pref[b] <= x.
-__device__ __forceinline__ int seq_of_page(const int* s_pref, int B, long long hr_count, long long x) {
+// Largest b with hr_count * pref[b] <= x.
+__device__ __forceinline__ int seq_of(const int* pref, int B, long long hr_count, long long x) {
   int lo = 0, hi = B - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (hr_count * s_pref[mid] <= x) lo = mid;
+    if (hr_count * pref[mid] <= x) lo = mid;
     else hi = mid - 1;
   }
   return lo;
 }
 
-// Workgroup whose share [floor(w T / NW), floor((w+1) T / NW)) holds page x.
-__device__ __forceinline__ int wg_of_page(long long x, long long T, int nw) {
-  return (int)(((x + 1) * nw - 1) / T);
-}
-
-// One page as a wave holds it: the whole K slice (S^T needs every dimension)
-// and the V^T tiles of the wave's half of the head dimensions.
-template <int NT, int D>
-struct PageFrag {
-  uint4 k[D / 32];
-  uint2 v[D / 32];
-};
-
-template <int NT, int D, int QT>
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_mfma_kernel(AttnParams p) {
-  constexpr int KS = D / 32;  // 32-dim k-steps of S^T
-  constexpr int MTH = D / 32; // 16-dim output tiles of O^T per wave (half of d)
-  constexpr int BS = 16;
-  constexpr int RPG = 16 * NT;
-  constexpr int QSTR = D + 8;  // bf16 row stride of the staged queries
-  extern __shared__ int s_pref[];
-  __shared__ int s_scan[kAttnThreads / 64];
-  __shared__ __align__(16) uint16_t sQ[RPG * QSTR];
-  __shared__ float sm_m[2][RPG];
-  __shared__ float sm_l[2][RPG];
-  __shared__ float sm_o[RPG][D + 4];
-  // Block ids of the pages being walked. Reading them from LDS keeps the page
-  // loads in flight: a vector load of a table entry would need vmcnt(0), which
-  // also waits for every prefetched page.
-  __shared__ int sTab[kTabChunk];
-
-  // Waves 2k and 2k+1 form pair k: both compute S^T and the softmax of the
-  // pair's pages; wave half `hf` accumulates O^T for dimensions [hf*d/2, (hf+1)*d/2).
-  const int lane = threadIdx.x & 63, w = uni(threadIdx.x >> 6);
-  const int pair = w >> 1, hf = w & 1;
-  const int i16 = lane & 15, g = lane >> 4;
-  const int wg = blockIdx.x, nw = gridDim.x;
-  build_page_prefix(p, s_pref, s_scan);
-  const long long HR = (long long)p.Hkv * p.nrg;
-  const long long T = HR * s_pref[p.B];
-  if (T == 0) return;
-  const long long r0 = (long long)wg * T / nw, r1 = (long long)(wg + 1) * T / nw;
-  if (r0 >= r1) return;
-  int b = uni(seq_of_page(s_pref, p.B, HR, r0));
-  int hr = uni((int)((r0 - HR * s_pref[b]) / (s_pref[b + 1] - s_pref[b])));
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
-  const float sl2 = p.scale_log2;
-
-  for (long long x = r0; x < r1;) {
-    const int np = uni(s_pref[b + 1] - s_pref[b]);
-    const long long seg0 = HR * uni(s_pref[b]) + (long long)hr * np;
-    const int lp0 = (int)(x - seg0);
-    const int lp1 = (int)(min(r1, seg0 + np) - seg0);
-    const int h = hr / p.nrg, rg = hr - h * p.nrg;
-    const int seg = b * (int)HR + hr;
-    const int start = uni(p.start[b]);
-    const int L = start + p.C;
-    const int qr0 = rg * RPG;
-    const int nr = min(RPG, p.G - qr0);
-    const int32_t* table = p.tables + (size_t)uni(p.seq_ids[b]) * p.maxb;
-
-    // Stage the segment's query rows (zero rows past nr) and the first block ids.
-    __syncthreads();
-    for (int t = threadIdx.x; t < min(kTabChunk, lp1 - lp0); t += blockDim.x)
-      sTab[t] = safe_block(p, table[lp0 + t]);
-    for (int idx = threadIdx.x; idx < RPG * (D / 8); idx += blockDim.x) {
-      const int rr = idx / (D / 8), c = idx - rr * (D / 8);
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (rr < nr) {
-        const int r = qr0 + rr, j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
-        v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) +
-                                            (((size_t)b * p.C + j) * p.Hq + hq) * D + 8 * c);
-      }
-      *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = v;
-    }
-    __syncthreads();
-
-    int jrow[NT];
+// Wave-wide inclusive sum of v (64 lanes).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + i16, nr - 1)) / p.ratio;
-
-    f32x4_t o[MTH][NT];
-#pragma unroll
-    for (int mt = 0; mt < MTH; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m[NT], l[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      m[nt] = -INFINITY;
-      l[nt] = 0.f;
-    }
-
-    int tab0 = lp0;  // first page whose block id is sTab[0]
-    auto load_page = [&](PageFrag<NT, D>& f, int page) {
-      const int phys = uni(sTab[page - tab0]);
-      const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
-      const uint16_t* kp = kbase + slot;
-      const uint16_t* vp = vbase + slot;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) f.k[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
-#pragma unroll
-      for (int mt = 0; mt < MTH; ++mt)
-        f.v[mt] = *reinterpret_cast<const uint2*>(vp + (i16 + 16 * (hf * MTH + mt)) * BS + 4 * g);
-    };
-
-    auto compute_page = [&](PageFrag<NT, D>& f, int page) {
-      const int kpos0 = page * BS + 4 * g;  // key position of accumulator element 0
-      if (page * BS + BS > L) {
-        // Keys at or beyond L are stale pool contents: zero their V.
-#pragma unroll
-        for (int mt = 0; mt < MTH; ++mt) {
-          uint32_t lo = f.v[mt].x, hi = f.v[mt].y;
-          if (kpos0 + 0 >= L) lo &= 0xffff0000u;
-          if (kpos0 + 1 >= L) lo &= 0x0000ffffu;
-          if (kpos0 + 2 >= L) hi &= 0xffff0000u;
-          if (kpos0 + 3 >= L) hi &= 0x0000ffffu;
-          f.v[mt] = make_uint2(lo, hi);
-        }
-      }
-      // Re-read the query fragments from LDS for every page instead of letting
-      // them be hoisted into 16*NT*KS/4 long-lived registers.
-      asm volatile("" ::: "memory");
-      f32x4_t sc[NT];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        sc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const uint4 qv = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
-          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, f.k[ks]),
-                                                           __builtin_bit_cast(bf16x8_t, qv), sc[nt], 0, 0, 0);
-        }
-      }
-      const bool need_mask = page * BS + BS - 1 > start;
-      bf16x8_t va[MTH];  // {V^T, V^T}: the same keys in both halves of the k-slots
-#pragma unroll
-      for (int mt = 0; mt < MTH; ++mt)
-        va[mt] = __builtin_bit_cast(bf16x8_t, make_uint4(f.v[mt].x, f.v[mt].y, f.v[mt].x, f.v[mt].y));
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        float x4[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) x4[jj] = sc[nt][jj] * sl2;
-        if (need_mask) {
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) x4[jj] = kpos0 + jj > start + jrow[nt] ? -INFINITY : x4[jj];
-        }
-        float mx = fmaxf(fmaxf(x4[0], x4[1]), fmaxf(x4[2], x4[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // Rescale only when some query column's running max grew (rare after the
-        // first pages); a column whose max did not grow gets alpha = 1.
-        if (__any(mx > m[nt])) {
-          const float m_new = fmaxf(m[nt], mx);
-          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[nt] - m_new);
-          l[nt] *= alpha;
-#pragma unroll
-          for (int mt = 0; mt < MTH; ++mt) o[mt][nt] *= alpha;
-          m[nt] = m_new;
-        }
-        const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
-        float e[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(x4[jj] - mu);
-        l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
-        // P = hi + lo, both bf16: slots 0..3 carry hi, 4..7 lo of the same keys,
-        // so one 16x16x32 MFMA against {V, V} accumulates P V to ~16 bits.
-        const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
-        const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
-        const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
-        const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
-        const bf16x8_t pf = __builtin_bit_cast(
-            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
-                                 pack2_bf16(r01[0], r01[1]), pack2_bf16(r23[0], r23[1])));
-#pragma unroll
-        for (int mt = 0; mt < MTH; ++mt)
-          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[mt], pf, o[mt][nt], 0, 0, 0);
-      }
-    };
-
-    // Pages lp0 + pair, lp0 + pair + 2, ...: kPageBufs rotating register
-    // buffers keep kPageBufs - 1 pages in flight while one is computed.
-    constexpr int kPageBufs = page_bufs(NT);
-    PageFrag<NT, D> buf[kPageBufs];
-    // Shares longer than kTabChunk pages are walked in windows of block ids.
-    for (; tab0 < lp1; tab0 += kTabChunk) {
-      const int wend = min(lp1, tab0 + kTabChunk);
-      if (tab0 != lp0) {
-        __syncthreads();
-        for (int t = threadIdx.x; t < wend - tab0; t += blockDim.x) sTab[t] = safe_block(p, table[tab0 + t]);
-        __syncthreads();
-      }
-      const int pg0 = tab0 + pair;
-#pragma unroll
-      for (int u = 0; u < kPageBufs - 1; ++u)
-        if (pg0 + 2 * u < wend) load_page(buf[u], pg0 + 2 * u);
-      for (int it = 0; pg0 + 2 * it < wend; it += kPageBufs) {
-#pragma unroll
-        for (int u = 0; u < kPageBufs; ++u) {
-          const int pg = pg0 + 2 * (it + u);
-          if (pg < wend) {
-            const int nxt = pg + 2 * (kPageBufs - 1);
-            if (nxt < wend) load_page(buf[(u + kPageBufs - 1) % kPageBufs], nxt);
-            compute_page(buf[u], pg);
-          }
-        }
-      }
-    }
-
-    // Row sums: the four lane groups hold disjoint keys of the same query column.
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      l[nt] += __shfl_xor(l[nt], 16, 64);
-      l[nt] += __shfl_xor(l[nt], 32, 64);
-    }
-    if (g == 0 && hf == 0) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        sm_m[pair][16 * nt + i16] = m[nt];
-        sm_l[pair][16 * nt + i16] = l[nt];
-      }
-    }
-    __syncthreads();
-    float fac[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int qc = 16 * nt + i16;
-      const float M = fmaxf(sm_m[0][qc], sm_m[1][qc]);
-      fac[nt] = (m[nt] == -INFINITY) ? 0.f : exp2f(m[nt] - M);
-    }
-    for (int pp = 0; pp < 2; ++pp) {
-      if (pair == pp) {
-#pragma unroll
-        for (int mt = 0; mt < MTH; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            float4* dst = reinterpret_cast<float4*>(&sm_o[16 * nt + i16][16 * (hf * MTH + mt) + 4 * g]);
-            const float4 v = make_float4(o[mt][nt][0] * fac[nt], o[mt][nt][1] * fac[nt], o[mt][nt][2] * fac[nt],
-                                         o[mt][nt][3] * fac[nt]);
-            if (pp == 0) {
-              *dst = v;
-            } else {
-              const float4 a = *dst;
-              *dst = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
-            }
-          }
-      }
-      __syncthreads();
-    }
-
-    // Final output when this workgroup saw the whole segment, else a partial.
-    const bool final_out = lp0 == 0 && lp1 == np;
-    const int slot = wg + seg;
-    constexpr int kVec = 8;
-    for (int idx = threadIdx.x; idx < nr * (D / kVec); idx += blockDim.x) {
-      const int rr = idx / (D / kVec), e0 = (idx - rr * (D / kVec)) * kVec;
-      const float M = fmaxf(sm_m[0][rr], sm_m[1][rr]);
-      float Lsum = 0.f;
-      for (int pp = 0; pp < 2; ++pp) {
-        const float mw = sm_m[pp][rr];
-        if (mw != -INFINITY) Lsum += sm_l[pp][rr] * exp2f(mw - M);
-      }
-      const int r = qr0 + rr;
-      if (final_out) {
-        const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
-        const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
-        const float inv = 1.f / Lsum;
-        if constexpr (QT == SPV_BF16) {
-          uint4 v;
-          v.x = pack2_bf16(sm_o[rr][e0 + 0] * inv, sm_o[rr][e0 + 1] * inv);
-          v.y = pack2_bf16(sm_o[rr][e0 + 2] * inv, sm_o[rr][e0 + 3] * inv);
-          v.z = pack2_bf16(sm_o[rr][e0 + 4] * inv, sm_o[rr][e0 + 5] * inv);
-          v.w = pack2_bf16(sm_o[rr][e0 + 6] * inv, sm_o[rr][e0 + 7] * inv);
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + ob) = v;
-        } else {
-#pragma unroll
-          for (int k = 0; k < kVec; ++k) store_out<QT>(p, ob + k, sm_o[rr][e0 + k] * inv);
-        }
-      } else {
-        const size_t base = (size_t)slot * p.G + r;
-        float4* po = reinterpret_cast<float4*>(p.part_o + base * D + e0);
-        po[0] = make_float4(sm_o[rr][e0 + 0], sm_o[rr][e0 + 1], sm_o[rr][e0 + 2], sm_o[rr][e0 + 3]);
-        po[1] = make_float4(sm_o[rr][e0 + 4], sm_o[rr][e0 + 5], sm_o[rr][e0 + 6], sm_o[rr][e0 + 7]);
-        if (e0 == 0) {
-          p.part_ml[base * 2] = M;
-          p.part_ml[base * 2 + 1] = Lsum;
-        }
-      }
-    }
-
-    x = seg0 + lp1;
-    if (++hr == HR) {
-      hr = 0;
-      ++b;
-    }
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
   }
+  return v;
 }
 
-// Combine the partial slots of every segment that more than one workgroup saw.
-// Workgroups with an empty share (fewer pages than workgroups) wrote nothing
-// and are skipped. Grid: (segment, block of kMergeRows rows).
-constexpr int kMergeRows = 8;
-constexpr int kMergeSlots = 32;  // slots staged in LDS; more fall back to direct loops
-
-template <int QT>
-__global__ __launch_bounds__(kAttnThreads) void attn_merge_slots_kernel(AttnParams p, int nw) {
-  extern __shared__ int s_pref[];
-  __shared__ int s_scan[kAttnThreads / 64];
-  __shared__ float s_f[kMergeRows][kMergeSlots];  // exp2(m_k - M) per row and slot
-  __shared__ float s_inv[kMergeRows];              // 1 / sum_k l_k f_k
-  __shared__ int s_slot[kMergeSlots];
-  __shared__ int s_ns;
-  build_page_prefix(p, s_pref, s_scan);
-  const long long HR = (long long)p.Hkv * p.nrg;
-  const long long T = HR * s_pref[p.B];
-  const int seg = blockIdx.x;
-  const int b = (int)(seg / HR), hr = (int)(seg - b * HR);
-  const int np = s_pref[b + 1] - s_pref[b];
-  const long long seg0 = HR * s_pref[b] + (long long)hr * np;
-  const int w0 = wg_of_page(seg0, T, nw), w1 = wg_of_page(seg0 + np - 1, T, nw);
-  if (w0 == w1) return;
-  const int h = hr / p.nrg, rg = hr - h * p.nrg;
-  // Signed: a trailing row block of a padded group has no rows (nr <= 0).
-  const int row0 = (int)blockIdx.y * kMergeRows;
-  const int qr0 = rg * p.rows_per_group + row0;
-  const int nr = min(kMergeRows, min(p.rows_per_group, p.G - rg * p.rows_per_group) - row0);
-  if (nr <= 0) return;
-  const int D = p.d;
-  if (threadIdx.x == 0) {
-    int ns = 0;
-    for (int k = w0; k <= w1; ++k)
-      if ((long long)k * T / nw < (long long)(k + 1) * T / nw) {
-        if (ns < kMergeSlots) s_slot[ns] = k + seg;
-        ++ns;
+// Pieces: every segment of np pages (one per (sequence b, kv head, row group))
+// is cut into k = ceil(np / P) near-equal page ranges, with P chosen so that
+// HR * sum_b k_b <= nw: each workgroup then holds at most one piece and pays
+// the per-piece costs (query staging, wave combine, partial, merge) once.
+// P starts at ceil(total / nw) and grows in proportion to the overshoot;
+// when the segments alone outnumber the workgroups, P is the longest context
+// and every piece is a whole segment. Wave 0 computes the whole plan with
+// wave-wide scans (no barrier until the end):
+//   s_pref[b]  = pages of the sequences before b (per segment), s_pref[B] = total;
+//   s_kpref[b] = pieces of one segment of each sequence before b, s_kpref[B] = total.
+__device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, long long HR, int nw) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const bool one = p.B <= 64;  // the common case keeps every count in a register
+    int np1 = 0, carry = 0, maxnp = 0;
+    for (int base = 0; base < p.B; base += 64) {
+      const int b = base + lane;
+      const int np = b < p.B ? context_pages(p, p.start[b] + p.C) : 0;
+      const int incl = wave_incl_scan(np);
+      if (b < p.B) s_pref[b] = carry + incl - np;
+      carry += __shfl(incl, 63, 64);
+      int mx = np;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+      maxnp = max(maxnp, mx);
+      np1 = np;
+    }
+    if (lane == 0) s_pref[p.B] = carry;
+    auto pages_of = [&](int b) { return one ? np1 : s_pref[b + 1] - s_pref[b]; };
+    const long long T = HR * carry;
+    int P = HR * p.B >= nw ? maxnp : (int)min((long long)maxnp, max(1LL, (T + nw - 1) / nw));
+    int npieces;
+    for (;;) {
+      npieces = 0;
+      for (int base = 0; base < p.B; base += 64) {
+        const int b = base + lane;
+        int k = b < p.B ? (pages_of(b) + P - 1) / P : 0;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+        npieces += k;
       }
-    s_ns = ns;
+      const long long n = HR * npieces;
+      if (n <= nw || P >= maxnp) break;  // P = maxnp gives n = HR * B <= nw here
+      P = (int)min((long long)maxnp, max((long long)P + 1, (P * n + nw - 1) / nw));
+    }
+    carry = 0;
+    for (int base = 0; base < p.B; base += 64) {
+      const int b = base + lane;
+      const int k = b < p.B ? (pages_of(b) + P - 1) / P : 0;
+      const int incl = wave_incl_scan(k);
+      if (b < p.B) s_kpref[b] = carry + incl - k;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) s_kpref[p.B] = carry;
   }
   __syncthreads();
-  const int ns = s_ns;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs; renumber them so each
+// XCD holds a contiguous run of pieces and a segment's partials, counter and
+// merge mostly stay within one L2.
+__device__ __forceinline__ int share_of_block(int bid, int nw) {
+  return (nw & 7) ? bid : (bid & 7) * (nw >> 3) + (bid >> 3);
+}
+
+// One page as a wave holds it: the K rows for S^T and the V^T tiles for O^T.
+template <int D>
+struct PageRegs {
+  uint4 k[D / 32];  // key i16, dims 32 ks + 8 g .. + 7
+  uint2 v[D / 16];  // dim 16 mt + i16, keys 4 g .. 4 g + 3
+};
+
+// Merge of one segment's partial slots (rows qr0 .. qr0 + nr - 1) into the
+// output. The O
+// rows of the first kPre slots are requested before the (m, l) phase so both
+// uncached round trips overlap.
+template <int QT, int RPG, int D>
+__device__ void merge_segment(const AttnParams& p, int x0, int ns, int b, int h, int qr0, int nr,
+                              float (*s_f)[kMergeSlots], float* s_inv, int* s_slot) {
+  constexpr int kPre = 4;
+  constexpr int kItems = (RPG * (D / 4) + kMfmaThreads - 1) / kMfmaThreads;  // float4 outputs per thread
+  // The segment's partial slots are its piece indices x0 .. x0 + ns - 1.
+  for (int k = threadIdx.x; k < kMergeSlots && k < ns; k += blockDim.x) s_slot[k] = x0 + k;
+  __syncthreads();
   if (ns <= kMergeSlots) {
-    // One lane per (row, slot): the m / l of all slots are read in parallel.
+    const int npre = min(ns, kPre);
+    float2 pre[kItems][kPre][2];
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kMfmaThreads;
+      const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
+#pragma unroll
+      for (int k = 0; k < kPre; ++k)
+        if (rr < nr && k < npre) {
+          const float* src = p.part_o + ((size_t)s_slot[k] * p.G + qr0 + rr) * D + e0;
+          pre[it][k][0] = load_coherent(src);
+          pre[it][k][1] = load_coherent(src + 2);
+        }
+    }
+    // One lane per (row, slot); the kMergeSlots lanes of a row are half a wave.
     const int lane = threadIdx.x & 63;
     for (int base = 0; base < nr * kMergeSlots; base += blockDim.x) {
       const int idx = base + threadIdx.x;
       const int rr = idx / kMergeSlots, k = idx - rr * kMergeSlots;
       float mk = -INFINITY, lk = 0.f;
       if (rr < nr && k < ns) {
-        const size_t bse = (size_t)s_slot[k] * p.G + qr0 + rr;
-        mk = p.part_ml[bse * 2];
-        lk = p.part_ml[bse * 2 + 1];
+        const float2 ml = load_coherent(p.part_ml + ((size_t)s_slot[k] * p.G + qr0 + rr) * 2);
+        mk = ml.x;
+        lk = ml.y;
       }
-      // rows occupy 32-lane halves of a wave: reduce within the half
       float M = mk;
 #pragma unroll
       for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
       const float f = mk == -INFINITY ? 0.f : exp2f(mk - M);
-      float L = lk * f;
+      float Ls = lk * f;
 #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+      for (int o = 16; o > 0; o >>= 1) Ls += __shfl_xor(Ls, o, 64);
       if (rr < nr) {
         s_f[rr][k] = f;
-        if ((lane & 31) == 0) s_inv[rr] = 1.f / L;
+        if ((lane & 31) == 0) s_inv[rr] = 1.f / Ls;
       }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < nr * (D / 4); idx += blockDim.x) {
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kMfmaThreads;
       const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
+      if (rr >= nr) continue;
       const int r = qr0 + rr;
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-      for (int k = 0; k < ns; ++k) {
+#pragma unroll
+      for (int k = 0; k < kPre; ++k)
+        if (k < npre) {
+          const float f = s_f[rr][k];
+          acc.x += pre[it][k][0].x * f;
+          acc.y += pre[it][k][0].y * f;
+          acc.z += pre[it][k][1].x * f;
+          acc.w += pre[it][k][1].y * f;
+        }
+      for (int k = kPre; k < ns; ++k) {
         const float f = s_f[rr][k];
-        const float4 v = *reinterpret_cast<const float4*>(p.part_o + ((size_t)s_slot[k] * p.G + r) * D + e0);
-        acc.x += v.x * f;
-        acc.y += v.y * f;
-        acc.z += v.z * f;
-        acc.w += v.w * f;
+        const float* src = p.part_o + ((size_t)s_slot[k] * p.G + r) * D + e0;
+        const float2 v0 = load_coherent(src), v1 = load_coherent(src + 2);
+        acc.x += v0.x * f;
+        acc.y += v0.y * f;
+        acc.z += v1.x * f;
+        acc.w += v1.y * f;
       }
       const float inv = s_inv[rr];
       const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
@@ -657,23 +447,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_slots_kernel(AttnPara
     const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
     const int r = qr0 + rr;
     float M = -INFINITY;
-    for (int k = w0; k <= w1; ++k)
-      if ((long long)k * T / nw < (long long)(k + 1) * T / nw)
-        M = fmaxf(M, p.part_ml[((size_t)(k + seg) * p.G + r) * 2]);
+    for (int k = 0; k < ns; ++k) M = fmaxf(M, load_coherent(p.part_ml + ((size_t)(x0 + k) * p.G + r) * 2).x);
     float Lsum = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = w0; k <= w1; ++k) {
-      if (!((long long)k * T / nw < (long long)(k + 1) * T / nw)) continue;
-      const size_t base = (size_t)(k + seg) * p.G + r;
-      const float ms = p.part_ml[base * 2];
-      if (ms == -INFINITY) continue;
-      const float f = exp2f(ms - M);
-      Lsum += p.part_ml[base * 2 + 1] * f;
-      const float4 v = *reinterpret_cast<const float4*>(p.part_o + base * D + e0);
-      acc.x += v.x * f;
-      acc.y += v.y * f;
-      acc.z += v.z * f;
-      acc.w += v.w * f;
+    for (int k = 0; k < ns; ++k) {
+      const size_t base = (size_t)(x0 + k) * p.G + r;
+      const float2 ml = load_coherent(p.part_ml + base * 2);
+      if (ml.x == -INFINITY) continue;
+      const float f = exp2f(ml.x - M);
+      Lsum += ml.y * f;
+      const float2 v0 = load_coherent(p.part_o + base * D + e0), v1 = load_coherent(p.part_o + base * D + e0 + 2);
+      acc.x += v0.x * f;
+      acc.y += v0.y * f;
+      acc.z += v1.x * f;
+      acc.w += v1.y * f;
     }
     const float inv = 1.f / Lsum;
     const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
@@ -682,6 +469,313 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_slots_kernel(AttnPara
     store_out<QT>(p, ob + 1, acc.y * inv);
     store_out<QT>(p, ob + 2, acc.z * inv);
     store_out<QT>(p, ob + 3, acc.w * inv);
+  }
+}
+
+template <int NT, int D, int QT>
+__global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p) {
+  constexpr int KS = D / 32;  // 32-dim k-steps of S^T
+  constexpr int MT = D / 16;  // 16-dim tiles of O^T
+  constexpr int BS = 16;
+  constexpr int RPG = 16 * NT;
+  constexpr int NWV = kMfmaThreads / 64;
+  constexpr int QSTR = D + 8;  // bf16 row stride of the staged queries
+  extern __shared__ int s_pref[];
+  __shared__ __align__(16) uint16_t sQ[RPG * QSTR];
+  // Block ids of the pages being walked. Reading them from LDS keeps the page
+  // loads in flight: a vector load of a table entry would need vmcnt(0), which
+  // also waits for every prefetched page.
+  __shared__ int sTab[kTabChunk];
+  __shared__ float sm_m[NWV][RPG];
+  __shared__ float sm_l[NWV][RPG];
+  __shared__ __align__(16) float sm_x[NWV * RPG * 16];  // combine slots: [wave][row][16 dims]
+  __shared__ float s_inv[RPG];
+  __shared__ int s_slot[kMergeSlots];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63, w = uni(threadIdx.x >> 6);
+  const int i16 = lane & 15, g = lane >> 4;
+  const int nw = gridDim.x;
+  const int wg = share_of_block(blockIdx.x, nw);
+  int* s_kpref = s_pref + p.B + 1;
+  const long long HR = (long long)p.Hkv * p.nrg;
+  build_plan(p, s_pref, s_kpref, HR, nw);
+  if (s_pref[p.B] == 0) return;
+  const long long N = HR * s_kpref[p.B];  // pieces in the batch
+  const long long x_begin = (long long)wg * N / nw, x_end = (long long)(wg + 1) * N / nw;
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
+  const uint16_t* qbase = static_cast<const uint16_t*>(p.q);
+  const float sl2 = p.scale_log2;
+
+  for (long long x = x_begin; x < x_end; ++x) {
+    const int b = uni(seq_of(s_kpref, p.B, HR, x));
+    const int kb = uni(s_kpref[b + 1] - s_kpref[b]);  // pieces per segment of sequence b
+    const int rem = (int)(x - HR * s_kpref[b]);
+    const int hr = rem / kb, piece = rem - hr * kb;
+    const int np = uni(s_pref[b + 1] - s_pref[b]);
+    const int lp0 = (int)((long long)piece * np / kb), lp1 = (int)((long long)(piece + 1) * np / kb);
+    const int h = hr / p.nrg, rg = hr - h * p.nrg;
+    const int seg = b * (int)HR + hr;
+    const int x0 = (int)(x - piece);  // the segment's first piece
+    const int start = uni(p.start[b]);
+    const int L = start + p.C;
+    const int qr0 = rg * RPG;
+    const int nr = min(RPG, p.G - qr0);
+    const int32_t* table = p.tables + (size_t)uni(p.seq_ids[b]) * p.maxb;
+
+    int jrow[NT];  // chunk row j of query column 16 nt + i16 (rows past nr repeat the last)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + i16, nr - 1)) / p.ratio;
+
+    // The previous segment's LDS readers are done: stage the segment's query
+    // rows (zero past nr) and the first block ids.
+    __syncthreads();
+    for (int t = threadIdx.x; t < min(kTabChunk, lp1 - lp0); t += blockDim.x)
+      sTab[t] = safe_block(p, table[lp0 + t]);
+    for (int idx = threadIdx.x; idx < RPG * (D / 8); idx += blockDim.x) {
+      const int rr = idx / (D / 8), c = idx - rr * (D / 8);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (rr < nr) {
+        const int r = qr0 + rr, j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
+        v = *reinterpret_cast<const uint4*>(qbase + (((size_t)b * p.C + j) * p.Hq + hq) * D + 8 * c);
+      }
+      *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = v;
+    }
+    __syncthreads();
+
+    f32x4_t o[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m[NT], l[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      m[nt] = -INFINITY;
+      l[nt] = 0.f;
+    }
+
+    int tab0 = lp0;  // first page whose block id is sTab[0]
+    auto load_page = [&](PageRegs<D>& f, int page) {
+      const int phys = uni(sTab[page - tab0]);
+      const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
+      const uint16_t* kp = kbase + slot;
+      const uint16_t* vp = vbase + slot;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) f.k[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) f.v[mt] = *reinterpret_cast<const uint2*>(vp + (16 * mt + i16) * BS + 4 * g);
+    };
+
+    auto compute_page = [&](PageRegs<D>& f, int page) {
+      const int kpos0 = page * BS + 4 * g;  // key position of accumulator element 0
+      if (page * BS + BS > L) {
+        // Keys at or beyond L are stale pool contents: zero their V.
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          uint32_t lo = f.v[mt].x, hi = f.v[mt].y;
+          if (kpos0 + 0 >= L) lo &= 0xffff0000u;
+          if (kpos0 + 1 >= L) lo &= 0x0000ffffu;
+          if (kpos0 + 2 >= L) hi &= 0xffff0000u;
+          if (kpos0 + 3 >= L) hi &= 0x0000ffffu;
+          f.v[mt] = make_uint2(lo, hi);
+        }
+      }
+      // The query fragments (B operand: row 16 nt + i16, dims 32 ks + 8 g .. + 7)
+      // are re-read from LDS for every page instead of being hoisted into
+      // registers for the whole walk.
+      asm volatile("" ::: "memory");
+      f32x4_t sc[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) sc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const uint4 qv = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
+          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, f.k[ks]),
+                                                           __builtin_bit_cast(bf16x8_t, qv), sc[nt], 0, 0, 0);
+        }
+      const bool need_mask = page * BS + BS - 1 > start;
+      float x[NT][4];
+      bool grow = false;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          x[nt][jj] = sc[nt][jj] * sl2;
+          if (need_mask && kpos0 + jj > start + jrow[nt]) x[nt][jj] = -INFINITY;
+          grow |= x[nt][jj] > m[nt] + kSlack;
+        }
+      }
+      // m[nt] is a reference, not the running max: scores may exceed it by up
+      // to kSlack (P <= 2^kSlack), so the column max -- two cross-lane steps --
+      // and the rescale of O are needed only when a score goes beyond that,
+      // i.e. on the first page and rarely after it.
+      if (__any(grow)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float mx = fmaxf(fmaxf(x[nt][0], x[nt][1]), fmaxf(x[nt][2], x[nt][3]));
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          const float m_new = fmaxf(m[nt], mx);
+          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[nt] - m_new);
+          l[nt] *= alpha;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) o[mt][nt] *= alpha;
+          m[nt] = m_new;
+        }
+      }
+      bf16x8_t pf[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const float* x4 = x[nt];
+        const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
+        float e[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(x4[jj] - mu);
+        l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
+        // P = hi + lo, both bf16: slots 0..3 carry hi, 4..7 lo of the same keys,
+        // so one 16x16x32 MFMA against {V, V} accumulates P V to ~16 bits.
+        const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
+        const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
+        const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
+        const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
+        pf[nt] = __builtin_bit_cast(
+            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
+                                 pack2_bf16(r01[0], r01[1]), pack2_bf16(r23[0], r23[1])));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        // {V^T, V^T}: the same keys in both halves of the k-slots.
+        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(f.v[mt].x, f.v[mt].y, f.v[mt].x, f.v[mt].y));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[nt], o[mt][nt], 0, 0, 0);
+      }
+    };
+
+    // Wave w takes pages tab0 + w, tab0 + w + NWV, ...; kRing rotating
+    // register buffers keep kRing - 1 pages in flight while one is computed.
+    constexpr int kRing = ring_depth(NT, D);
+    PageRegs<D> buf[kRing];
+    for (; tab0 < lp1; tab0 += kTabChunk) {
+      const int wend = min(lp1, tab0 + kTabChunk);
+      if (tab0 != lp0) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < wend - tab0; t += blockDim.x) sTab[t] = safe_block(p, table[tab0 + t]);
+        __syncthreads();
+      }
+      const int pg0 = tab0 + w, last = wend - 1;
+      const int n = pg0 < wend ? (last - pg0) / NWV + 1 : 0;  // this wave's pages in the window
+      // Every load is issued unconditionally (past the end it re-reads the
+      // window's last page): the number of loads in flight is then the same on
+      // every path, so each page waits only for its own loads (vmcnt(N)), not
+      // for the pages prefetched after it (vmcnt(0)).
+#pragma unroll
+      for (int u = 0; u < kRing - 1; ++u) load_page(buf[u], min(pg0 + NWV * u, last));
+      for (int it = 0; it < n; it += kRing) {
+#pragma unroll
+        for (int u = 0; u < kRing; ++u) {
+          const int s = it + u;
+          if (s >= n) break;
+          load_page(buf[(u + kRing - 1) % kRing], min(pg0 + NWV * (s + kRing - 1), last));
+          compute_page(buf[u], pg0 + NWV * s);
+        }
+      }
+    }
+
+    // Row sums: the four lane groups hold disjoint keys of the same query column.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      l[nt] += __shfl_xor(l[nt], 16, 64);
+      l[nt] += __shfl_xor(l[nt], 32, 64);
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        sm_m[w][16 * nt + i16] = m[nt];
+        sm_l[w][16 * nt + i16] = l[nt];
+      }
+    }
+    __syncthreads();
+
+    // Combine the waves tile by tile: in round mt every wave stores its O^T tile
+    // mt (16 dims x RPG rows) into its own LDS slot, then the workgroup's
+    // threads each take (row, 4 dims) of the tile, add the NWV slots with the
+    // row's factors 2^(m_w - M) (fixed order) and write the output -- or the
+    // partial -- directly.
+    const bool final_out = kb == 1;
+    const int slot = (int)x;
+    const int crow = threadIdx.x >> 2, cd4 = threadIdx.x & 3;  // combining thread: row, dims 4*cd4..+3
+    const bool combiner = crow < nr;
+    float cfac[NWV], cinv = 0.f, cM = 0.f, cL = 0.f;
+    if (combiner) {
+      cM = sm_m[0][crow];
+#pragma unroll
+      for (int ww = 1; ww < NWV; ++ww) cM = fmaxf(cM, sm_m[ww][crow]);
+#pragma unroll
+      for (int ww = 0; ww < NWV; ++ww) {
+        const float mw = sm_m[ww][crow];
+        cfac[ww] = mw == -INFINITY ? 0.f : exp2f(mw - cM);
+        cL += sm_l[ww][crow] * cfac[ww];
+      }
+      cinv = 1.f / cL;
+    }
+    const int cr = qr0 + crow;
+    size_t cbase;
+    if (final_out) {
+      const int j = cr / p.ratio, hq = h * p.ratio + (cr - j * p.ratio);
+      cbase = (((size_t)b * p.C + j) * p.Hq + hq) * D;
+    } else {
+      cbase = ((size_t)slot * p.G + cr) * D;
+      if (combiner && cd4 == 0) store_coherent(p.part_ml + ((size_t)slot * p.G + cr) * 2, cM, cL);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt > 0) __syncthreads();  // the previous round's readers are done
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        *reinterpret_cast<f32x4_t*>(&sm_x[((w * RPG) + 16 * nt + i16) * 16 + 4 * g]) = o[mt][nt];
+      __syncthreads();
+      if (combiner) {
+        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ww = 0; ww < NWV; ++ww)
+          acc += *reinterpret_cast<const f32x4_t*>(&sm_x[((ww * RPG) + crow) * 16 + 4 * cd4]) * cfac[ww];
+        const int e0 = 16 * mt + 4 * cd4;
+        if (final_out) {
+          if constexpr (QT == SPV_BF16) {
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + cbase + e0) =
+                make_uint2(pack2_bf16(acc[0] * cinv, acc[1] * cinv), pack2_bf16(acc[2] * cinv, acc[3] * cinv));
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) store_out<QT>(p, cbase + e0 + k, acc[k] * cinv);
+          }
+        } else {
+          store_coherent(p.part_o + cbase + e0, acc[0], acc[1]);
+          store_coherent(p.part_o + cbase + e0 + 2, acc[2], acc[3]);
+        }
+      }
+    }
+
+    if (!final_out) {
+      // Every wave waits until its coherent partial stores have completed; after
+      // the barrier thread 0 counts this share's pages in. The workgroup that
+      // completes the count reads the partials with coherent loads.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(p.counters + seg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == kb;
+      __syncthreads();
+      if (s_last) {
+        // The merge weights reuse the query rows' LDS, dead after the page walk.
+        static_assert(sizeof(float) * RPG * kMergeSlots <= sizeof(sQ), "merge weights exceed sQ");
+        merge_segment<QT, RPG, D>(p, x0, kb, b, h, qr0, nr, reinterpret_cast<float(*)[kMergeSlots]>(sQ),
+                                  s_inv, s_slot);
+        if (threadIdx.x == 0) p.counters[seg] = 0;
+      }
+    }
   }
 }
 
@@ -721,35 +815,55 @@ struct Plan {
 Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv_dtype, int q_dtype) {
   Plan pl{};
   const int G = C * (Hq / Hkv);
-  pl.mfma = kv_dtype == SPV_BF16 && q_dtype == SPV_BF16 && bs == 16 && (d == 128 || d == 64) && G >= 16;
+  pl.mfma = kv_dtype == SPV_BF16 && q_dtype == SPV_BF16 && bs == 16 && (d == 128 || d == 64) && G >= 16 &&
+            B <= kMfmaMaxB;
   const int max_pages = (max_ctx + bs - 1) / bs;
   if (pl.mfma) {
     pl.nt = G >= 64 ? 4 : (G + 15) / 16;
     pl.rows_per_group = 16 * pl.nt;
-    pl.pages_per_split = 0;
-    pl.max_splits = 0;
-  } else {
+    pl.nrg = (G + pl.rows_per_group - 1) / pl.rows_per_group;
+    // One arrival counter per segment.
+    if ((long long)B * Hkv * pl.nrg > kCounterWords) pl.mfma = false;
+  }
+  if (!pl.mfma) {
     pl.nt = 0;
     pl.rows_per_group = 64;
     pl.pages_per_split = bs >= 16 ? 8 : 128 / bs;
     pl.max_splits = (max_pages + pl.pages_per_split - 1) / pl.pages_per_split;
+    pl.nrg = (G + pl.rows_per_group - 1) / pl.rows_per_group;
   }
-  pl.nrg = (G + pl.rows_per_group - 1) / pl.rows_per_group;
-  (void)B;
   return pl;
 }
 
-size_t workspace_for(const Plan& pl, int B, int C, int Hq, int Hkv, int d) {
+// Partial rows the plan may write (0: the call needs no partials).
+size_t partial_rows(const Plan& pl, int B, int C, int Hq, int Hkv) {
   const size_t G = (size_t)C * (Hq / Hkv);
-  size_t slots;
-  if (pl.mfma) {
-    slots = (size_t)kMfmaWGsMax + (size_t)B * Hkv * pl.nrg;
-  } else {
-    if (pl.max_splits <= 1) return 0;
-    slots = (size_t)B * Hkv * pl.max_splits;
+  if (pl.mfma) return (size_t)kMfmaWGsMax * G;  // one slot per piece, at most one piece per workgroup
+  if (pl.max_splits <= 1) return 0;
+  return (size_t)B * Hkv * pl.max_splits * G;
+}
+
+// Bytes of the (m, l) rows, padded so the O rows that follow are 256-byte aligned.
+size_t ml_bytes(size_t rows) { return (rows * 2 * sizeof(float) + 255) & ~(size_t)255; }
+
+size_t workspace_for(const Plan& pl, int B, int C, int Hq, int Hkv, int d) {
+  if (!pl.mfma && pl.max_splits <= 1) return 0;
+  const size_t rows = partial_rows(pl, B, C, Hq, Hkv);
+  return (size_t)SPV_ATTN_COUNTER_BYTES + ml_bytes(rows) + rows * d * sizeof(float);
+}
+
+// Workgroups of the persistent MFMA grid: one per compute unit.
+int persistent_wgs() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  const int slot = dev & 63;
+  if (cached[slot] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    cached[slot] = cus < kMfmaWGsMax ? cus : kMfmaWGsMax;
   }
-  const size_t rows = slots * G;
-  return rows * d * sizeof(float) + rows * 2 * sizeof(float) + 256;
+  return cached[slot];
 }
 
 template <int QT, int KT>
@@ -775,8 +889,8 @@ int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s) {
 
 template <int D>
 void launch_mfma(const AttnParams& p, int nt, hipStream_t s) {
-  const size_t smem = (size_t)(p.B + 1) * sizeof(int);
-  const dim3 grid(mfma_wgs(nt)), blk(kAttnThreads);
+  const size_t smem = (size_t)2 * (p.B + 1) * sizeof(int);  // page and piece prefixes
+  const dim3 grid(persistent_wgs()), blk(kMfmaThreads);
   switch (nt) {
     case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16>), grid, blk, smem, s, p); break;
     case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16>), grid, blk, smem, s, p); break;
@@ -846,30 +960,16 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
   p.max_pages = (max_ctx + block_size - 1) / block_size;
   p.scale_log2 = scale * kLog2e;
   if (need > 0) {
-    const size_t rows = (need - 256) / (sizeof(float) * (head_dim + 2));
-    p.part_o = static_cast<float*>(workspace);
-    p.part_ml = p.part_o + rows * head_dim;
+    const size_t rows = partial_rows(pl, B, C, num_q_heads, num_kv_heads);
+    char* ws = static_cast<char*>(workspace);
+    p.counters = reinterpret_cast<int*>(ws);
+    p.part_ml = reinterpret_cast<float*>(ws + SPV_ATTN_COUNTER_BYTES);
+    p.part_o = reinterpret_cast<float*>(ws + SPV_ATTN_COUNTER_BYTES + ml_bytes(rows));
   }
   hipStream_t s = (hipStream_t)stream;
   if (pl.mfma) {
     if (head_dim == 128) launch_mfma<128>(p, pl.nt, s);
     else launch_mfma<64>(p, pl.nt, s);
-    SPV_CHECK_LAUNCH();
-    const int nseg = B * num_kv_heads * pl.nrg;
-    const int nwg = mfma_wgs(pl.nt);
-    const size_t smem = (size_t)(B + 1) * sizeof(int);
-    const dim3 mgrid(nseg, (pl.rows_per_group + kMergeRows - 1) / kMergeRows);
-    switch (q_dtype) {
-      case SPV_F32:
-        hipLaunchKernelGGL(attn_merge_slots_kernel<SPV_F32>, mgrid, dim3(kAttnThreads), smem, s, p, nwg);
-        break;
-      case SPV_BF16:
-        hipLaunchKernelGGL(attn_merge_slots_kernel<SPV_BF16>, mgrid, dim3(kAttnThreads), smem, s, p, nwg);
-        break;
-      default:
-        hipLaunchKernelGGL(attn_merge_slots_kernel<SPV_F16>, mgrid, dim3(kAttnThreads), smem, s, p, nwg);
-        break;
-    }
     SPV_CHECK_LAUNCH();
     return SPV_OK;
   }

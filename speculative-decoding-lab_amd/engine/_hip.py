@@ -126,12 +126,15 @@ def i32(values, device: torch.device) -> torch.Tensor:
 
 
 class Workspace:
-    """Grow-only device scratch buffer owned by the caller of the library."""
+    """Grow-only device scratch buffer owned by the caller of the library.
+
+    Allocated zero-filled: the attention entry point keeps arrival counters at
+    its head that must start at zero (and are zero again after every call)."""
 
     def __init__(self) -> None:
         self._buf: Optional[torch.Tensor] = None
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
         if self._buf is None or self._buf.numel() < nbytes or self._buf.device != device:
-            self._buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            self._buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         return self._buf

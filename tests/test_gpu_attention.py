@@ -199,6 +199,24 @@ def test_output_writes_stay_inside_the_batch(cuda, C, Hq):
     _bf16_check(out, ref_attn.extend_attention_dense(q, keys, values, lens, Hq))
 
 
+def test_repeated_calls_are_identical_and_leave_counters_zero(cuda):
+    # Sequences cut between workgroups are merged by the last one to arrive;
+    # its arrival counters live at the head of the workspace and must be zero
+    # again after every call, and the fixed-order merges make reruns bitwise equal.
+    import engine.attention as A
+
+    g = torch.Generator().manual_seed(21)
+    lens = torch.randint(256, 4097, (32,), generator=g).tolist()
+    gpu, keys, values = _dense_pool(cuda, lens, 6, 2, 128, 16, torch.bfloat16, seed=21, cap=20000)
+    q = torch.randn(32, 6, 12, 128, generator=g).to(torch.bfloat16).to(cuda)
+    outs = [verify_attention(q, gpu, 0, list(range(32)), lens, max(lens) + 6).clone() for _ in range(3)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    counters = A._workspace._buf[: 1 << 18]
+    assert int(counters.count_nonzero()) == 0
+    _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, 12))
+
+
 def test_split_count_does_not_change_result(cuda):
     # The same batch with max_ctx raised (more, partly empty splits) gives the same output.
     lens, C, Hq, Hkv, d = [700, 33], 6, 12, 2, 128
