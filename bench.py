@@ -12,8 +12,11 @@ the free list. One step =
      (target logits N(0, 2^2), draft = target + N(0, 1), T = 1, caller noise),
   4. rewind of the pool to start + n_commit with the sampled lengths.
 
-All inputs are resident in HBM before timing; the step runs as one captured HIP
-graph. The headline ``value`` is the verify-attention HBM bandwidth (algorithmic
+All inputs are resident in HBM before timing; steps run as captured HIP graphs.
+The batch exists in 8 replicas on disjoint random pages of the pool (and the
+logits in 2 sets); consecutive calls use different replicas, so none finds its
+K/V in the 256 MB last-level cache -- each call reads HBM as one layer of a
+deep model would. The headline ``value`` is the verify-attention HBM bandwidth (algorithmic
 bytes / measured time of the attention call); ``spec_step_us_per_seq`` is the
 whole step per sequence. ``cpu_baseline`` times the CPU oracle (the reference's
 gather + repeat_interleave + masked SDPA per sequence) on the host.
@@ -41,6 +44,11 @@ METRIC = "verify-attn HBM GB/s (% of peak) + spec-step us/seq, gamma=5, 1 GPU"
 
 B, HQ, HKV, D, BS, GAMMA, CAP, VOCAB = 32, 12, 2, 128, 16, 5, 65536, 151936
 C = GAMMA + 1
+# Timed calls cycle over REPLICAS copies of the batch on disjoint pages of the
+# pool (~700 MB of K/V in all) and over two sets of logits, so that no call
+# finds its data in the 256 MB last-level cache left by the previous one:
+# every call reads HBM, as one layer of a deep model does.
+REPLICAS, LOGIT_SETS = 8, 2
 
 
 def attention_bytes(lens):
@@ -103,22 +111,25 @@ def build_workload(dev, seed=0):
     lens, g = workload_lens(seed)
     perm = torch.randperm(CAP, generator=g).tolist()
     tables, pos = [], 0
-    for L in lens:
-        n = -(-L // BS)
-        tables.append(perm[pos: pos + n])
-        pos += n
+    for _ in range(REPLICAS):
+        for L in lens:
+            n = -(-L // BS)
+            tables.append(perm[pos: pos + n])
+            pos += n
     free = perm[pos:]
-    kv = PagedKVCache(1, HKV, D, CAP, BS, dev, torch.bfloat16, max_seqs=B,
+    kv = PagedKVCache(1, HKV, D, CAP, BS, dev, torch.bfloat16, max_seqs=B * REPLICAS,
                       max_blocks_per_seq=-(-(4096 + C) // BS) + 1)
-    kv.load_state(tables, lens, free)
+    kv.load_state(tables, lens * REPLICAS, free)
     gd = torch.Generator(device=dev).manual_seed(seed)
     keys, values = [], []
-    for s, L in enumerate(lens):
-        k = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
-        v = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
-        kv.write_block(0, [s], [0], k, v)
-        keys.append(k[0])
-        values.append(v[0])
+    for r in range(REPLICAS):
+        for s, L in enumerate(lens):
+            k = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
+            v = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
+            kv.write_block(0, [r * B + s], [0], k, v)
+            if r == 0:
+                keys.append(k[0])
+                values.append(v[0])
     w = {
         "lens": lens,
         "kv": kv,
@@ -127,15 +138,17 @@ def build_workload(dev, seed=0):
         "q": torch.randn(B, C, HQ, D, generator=gd, device=dev).to(torch.bfloat16),
         "k_new": torch.randn(B, C, HKV, D, generator=gd, device=dev).to(torch.bfloat16),
         "v_new": torch.randn(B, C, HKV, D, generator=gd, device=dev).to(torch.bfloat16),
-        "sid": torch.arange(B, dtype=torch.int32, device=dev),
+        "sids": [torch.arange(r * B, (r + 1) * B, dtype=torch.int32, device=dev) for r in range(REPLICAS)],
         "start": torch.tensor(lens, dtype=torch.int32, device=dev),
+        "logits": [],
     }
-    target = torch.randn(B, C, VOCAB, generator=gd, device=dev) * 2.0
-    draft = target[:, :GAMMA] + torch.randn(B, GAMMA, VOCAB, generator=gd, device=dev)
-    probs_q = torch.softmax(draft, dim=-1)
-    w["target"] = target.contiguous()
-    w["draft"] = draft.contiguous()
-    w["proposals"] = torch.multinomial(probs_q.reshape(-1, VOCAB), 1, generator=gd).reshape(B, GAMMA).to(torch.int32)
+    for _ in range(LOGIT_SETS):
+        target = torch.randn(B, C, VOCAB, generator=gd, device=dev) * 2.0
+        draft = target[:, :GAMMA] + torch.randn(B, GAMMA, VOCAB, generator=gd, device=dev)
+        probs_q = torch.softmax(draft, dim=-1)
+        proposals = torch.multinomial(probs_q.reshape(-1, VOCAB), 1, generator=gd).reshape(B, GAMMA)
+        w["logits"].append((target.contiguous(), draft.contiguous(), proposals.to(torch.int32)))
+        del probs_q
     w["u"] = torch.rand(B, GAMMA, generator=gd, device=dev)
     w["noise"] = torch.empty(B, VOCAB, device=dev).exponential_(1, generator=gd)
     w["attn_out"] = torch.empty_like(w["q"])
@@ -143,6 +156,8 @@ def build_workload(dev, seed=0):
 
 
 def make_step(w):
+    """Closures of one verify step for replica r / logits set t: append the
+    verify tokens, attention, fused sampling, rewind."""
     from engine.attention import verify_attention
     from engine.spec_scheduler import _new_result, verify_sample
 
@@ -150,24 +165,28 @@ def make_step(w):
     max_ctx = max(w["lens"]) + C
     res = _new_result(B, GAMMA, kv.device)
 
-    def append():
-        kv.write_block_device(0, w["sid"], w["start"], w["k_new"], w["v_new"])
+    def append(r):
+        kv.write_block_device(0, w["sids"][r], w["start"], w["k_new"], w["v_new"])
 
-    def attend():
-        verify_attention(w["q"], kv, 0, w["sid"], w["start"], max_ctx, out=w["attn_out"])
+    def attend(r):
+        verify_attention(w["q"], kv, 0, w["sids"][r], w["start"], max_ctx, out=w["attn_out"])
 
-    def sample():
-        verify_sample(w["target"], w["draft"], w["proposals"], w["u"], w["noise"], 1.0,
+    def sample(t):
+        target, draft, proposals = w["logits"][t]
+        verify_sample(target, draft, proposals, w["u"], w["noise"], 1.0,
                       start_pos=w["start"], result=res, validate=False)
 
-    def rewind():
-        kv.rewind_device(w["sid"], res.new_len, res.finished)
+    def rewind(r):
+        # All replicas share the context lengths, so the sampled new lengths
+        # apply to any of them.
+        kv.rewind_device(w["sids"][r], res.new_len, res.finished)
 
-    def step():
-        append()
-        attend()
-        sample()
-        rewind()
+    def step(i):
+        r, t = i % REPLICAS, i % LOGIT_SETS
+        append(r)
+        attend(r)
+        sample(t)
+        rewind(r)
 
     return step, {"append": append, "attend": attend, "sample": sample, "rewind": rewind}, res
 
@@ -277,25 +296,31 @@ def main() -> int:
     print("bench: building workload", file=sys.stderr, flush=True)
     w = build_workload(dev, args.seed)
     step, parts, res = make_step(w)
-    for _ in range(max(1, args.warmup)):
-        step()
+    for i in range(max(1, args.warmup) * REPLICAS):
+        step(i)
     torch.cuda.synchronize()
     print("bench: warm-up done, capturing", file=sys.stderr, flush=True)
 
-    # Timed region: K whole steps, one graph replay each.
-    g_step = graph_of(step, 1, torch)
+    # Timed region: K whole steps; one graph replay runs REPLICAS steps (each
+    # on its own replica of the batch), so the K steps are ceil(K / REPLICAS)
+    # replays.
+    g_step = graph_of(lambda: [step(i) for i in range(REPLICAS)], 1, torch)
     for _ in range(args.warmup):
         g_step.replay()
     torch.cuda.synchronize()
-    ms_per_step = time_graph(g_step, args.steps, torch)
+    replays = max(1, -(-args.steps // REPLICAS))
+    ms_per_step = time_graph(g_step, replays, torch) / REPLICAS
 
-    # Per-part timings (graphs of 20 back-to-back calls, outside the timed region).
-    reps = 20
+    # Per-part timings outside the timed region: graphs of back-to-back calls
+    # cycling over the replicas / logits sets.
+    reps = 3 * REPLICAS
     part_us = {}
-    for name in ("attend", "sample"):
-        gpart = graph_of(parts[name], reps, torch)
-        part_us[name] = time_graph(gpart, 5, torch) * 1000.0 / reps
-    g_ar = graph_of(lambda: (parts["append"](), parts["rewind"]()), reps, torch)
+    g_att = graph_of(lambda: [parts["attend"](i % REPLICAS) for i in range(reps)], 1, torch)
+    part_us["attend"] = time_graph(g_att, 5, torch) * 1000.0 / reps
+    g_smp = graph_of(lambda: [parts["sample"](i % LOGIT_SETS) for i in range(reps)], 1, torch)
+    part_us["sample"] = time_graph(g_smp, 5, torch) * 1000.0 / reps
+    g_ar = graph_of(lambda: [(parts["append"](i % REPLICAS), parts["rewind"](i % REPLICAS)) for i in range(reps)],
+                    1, torch)
     part_us["append_rewind"] = time_graph(g_ar, 5, torch) * 1000.0 / reps
     torch.cuda.synchronize()
     print("bench: timings done", file=sys.stderr, flush=True)
@@ -312,7 +337,7 @@ def main() -> int:
         "value": round(attn_gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": replays * REPLICAS,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
@@ -323,7 +348,8 @@ def main() -> int:
         "config": {
             "workload": "Qwen2.5-1.5B-shaped paged verify step: batch 32, gamma 5 (6 rows), "
                         "12q/2kv heads, head_dim 128, block 16, ctx U[256,4096], 65536-block pool, "
-                        "1 layer; fused sampling over V=151936 fp32 at T=1",
+                        "1 layer; fused sampling over V=151936 fp32 at T=1; calls cycle over 8 "
+                        "replicas of the batch on disjoint pages (no last-level-cache reuse)",
             "global_batch": B,
             "seq_len": int(sum(lens) / len(lens)),
             "parallelism": "single-gpu",

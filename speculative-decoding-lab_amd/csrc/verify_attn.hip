@@ -235,8 +235,13 @@ constexpr int kMfmaMaxB = 512;    // the page and piece prefixes of the batch li
 // every operand stays in VGPRs) keeps eight pages in flight per CU.
 __host__ __device__ constexpr int ring_depth(int, int) { return 2; }
 constexpr int kMfmaThreads = 512;
+// O^T tiles combined per LDS round: as many as fit beside the other buffers
+// (the slots take 8 waves x 16 * nt rows x 64 B per tile).
+__host__ __device__ constexpr int combine_tiles(int nt, int mt) {
+  return (nt == 1 ? 4 : nt <= 3 ? 2 : 1) < mt ? (nt == 1 ? 4 : nt <= 3 ? 2 : 1) : mt;
+}
 constexpr int kTabChunk = 512;    // block ids staged in LDS per window
-constexpr int kMergeSlots = 32;   // partial slots staged in LDS by the merging workgroup
+constexpr int kMergeChunk = 4;    // partial slots the merging workgroup loads at once
 // log2 units a score may exceed its column's reference before O is rescaled.
 constexpr float kSlack = 8.f;
 
@@ -246,16 +251,30 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
 }
 
 // Partials cross workgroups (and XCDs, whose L2s are not coherent with each
-// other): they are written and read with device-scope atomic accesses, which
-// go to the device coherence point (sc1), so publishing them needs only their
-// completion, not a write-back of the whole L2.
-__device__ __forceinline__ void store_coherent(float* dst, float a, float b) {
-  const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// other): they are written and read through buffer accesses with the sc1
+// cache policy, which go to the device coherence point, so publishing them
+// needs only their completion (s_waitcnt), not a write-back of the whole L2.
+// Plain (non-atomic) accesses leave the compiler free to keep many in flight.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int kCoherent = 16;                 // cache-policy operand: sc1
+constexpr int kBufferWord3 = 0x00020000;      // raw 32-bit buffer descriptor, gfx9 family
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, kBufferWord3);
 }
-__device__ __forceinline__ float2 load_coherent(const float* src) {
-  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+__device__ __forceinline__ void store4_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off, f32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)byte_off, 0, kCoherent);
+}
+__device__ __forceinline__ void store2_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off, float a, float b) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{__float_as_uint(a), __float_as_uint(b)}, r, (int)byte_off, 0,
+                                        kCoherent);
+}
+__device__ __forceinline__ f32x4_t load4_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCoherent));
+}
+__device__ __forceinline__ float2 load2_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off) {
+  const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, kCoherent);
+  return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
 }
 
 // Values that are the same in every lane of a wave, moved to scalar registers
@@ -356,119 +375,70 @@ struct PageRegs {
   uint2 v[D / 16];  // dim 16 mt + i16, keys 4 g .. 4 g + 3
 };
 
-// Merge of one segment's partial slots (rows qr0 .. qr0 + nr - 1) into the
-// output. The O
-// rows of the first kPre slots are requested before the (m, l) phase so both
-// uncached round trips overlap.
+// Merge of one segment's partial slots x0 .. x0 + ns - 1 (rows qr0 .. qr0 + nr
+// - 1) into the output. Each thread takes (row, 4 dims) items and issues every
+// load of a chunk of kMergeChunk slots -- the slots' (m, l) of its rows and its
+// O slices -- before using any, so a merge of up to kMergeChunk slots costs one
+// uncached round trip and no barrier; more slots are folded in with the
+// usual online rescale.
 template <int QT, int RPG, int D>
-__device__ void merge_segment(const AttnParams& p, int x0, int ns, int b, int h, int qr0, int nr,
-                              float (*s_f)[kMergeSlots], float* s_inv, int* s_slot) {
-  constexpr int kPre = 4;
+__device__ void merge_segment(const AttnParams& p, int x0, int ns, int b, int h, int qr0, int nr) {
   constexpr int kItems = (RPG * (D / 4) + kMfmaThreads - 1) / kMfmaThreads;  // float4 outputs per thread
-  // The segment's partial slots are its piece indices x0 .. x0 + ns - 1.
-  for (int k = threadIdx.x; k < kMergeSlots && k < ns; k += blockDim.x) s_slot[k] = x0 + k;
-  __syncthreads();
-  if (ns <= kMergeSlots) {
-    const int npre = min(ns, kPre);
-    float2 pre[kItems][kPre][2];
+  float M[kItems], Ls[kItems];
+  f32x4_t acc[kItems];
 #pragma unroll
-    for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kMfmaThreads;
-      const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
-#pragma unroll
-      for (int k = 0; k < kPre; ++k)
-        if (rr < nr && k < npre) {
-          const float* src = p.part_o + ((size_t)s_slot[k] * p.G + qr0 + rr) * D + e0;
-          pre[it][k][0] = load_coherent(src);
-          pre[it][k][1] = load_coherent(src + 2);
-        }
-    }
-    // One lane per (row, slot); the kMergeSlots lanes of a row are half a wave.
-    const int lane = threadIdx.x & 63;
-    for (int base = 0; base < nr * kMergeSlots; base += blockDim.x) {
-      const int idx = base + threadIdx.x;
-      const int rr = idx / kMergeSlots, k = idx - rr * kMergeSlots;
-      float mk = -INFINITY, lk = 0.f;
-      if (rr < nr && k < ns) {
-        const float2 ml = load_coherent(p.part_ml + ((size_t)s_slot[k] * p.G + qr0 + rr) * 2);
-        mk = ml.x;
-        lk = ml.y;
-      }
-      float M = mk;
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-      const float f = mk == -INFINITY ? 0.f : exp2f(mk - M);
-      float Ls = lk * f;
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) Ls += __shfl_xor(Ls, o, 64);
-      if (rr < nr) {
-        s_f[rr][k] = f;
-        if ((lane & 31) == 0) s_inv[rr] = 1.f / Ls;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kMfmaThreads;
-      const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
-      if (rr >= nr) continue;
-      const int r = qr0 + rr;
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int k = 0; k < kPre; ++k)
-        if (k < npre) {
-          const float f = s_f[rr][k];
-          acc.x += pre[it][k][0].x * f;
-          acc.y += pre[it][k][0].y * f;
-          acc.z += pre[it][k][1].x * f;
-          acc.w += pre[it][k][1].y * f;
-        }
-      for (int k = kPre; k < ns; ++k) {
-        const float f = s_f[rr][k];
-        const float* src = p.part_o + ((size_t)s_slot[k] * p.G + r) * D + e0;
-        const float2 v0 = load_coherent(src), v1 = load_coherent(src + 2);
-        acc.x += v0.x * f;
-        acc.y += v0.y * f;
-        acc.z += v1.x * f;
-        acc.w += v1.y * f;
-      }
-      const float inv = s_inv[rr];
-      const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
-      const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
-      store_out<QT>(p, ob + 0, acc.x * inv);
-      store_out<QT>(p, ob + 1, acc.y * inv);
-      store_out<QT>(p, ob + 2, acc.z * inv);
-      store_out<QT>(p, ob + 3, acc.w * inv);
-    }
-    return;
+  for (int it = 0; it < kItems; ++it) {
+    M[it] = -INFINITY;
+    Ls[it] = 0.f;
+    acc[it] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  // Many slots (a tiny workload spread over many workgroups): direct loops.
-  for (int idx = threadIdx.x; idx < nr * (D / 4); idx += blockDim.x) {
-    const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
-    const int r = qr0 + rr;
-    float M = -INFINITY;
-    for (int k = 0; k < ns; ++k) M = fmaxf(M, load_coherent(p.part_ml + ((size_t)(x0 + k) * p.G + r) * 2).x);
-    float Lsum = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = 0; k < ns; ++k) {
-      const size_t base = (size_t)(x0 + k) * p.G + r;
-      const float2 ml = load_coherent(p.part_ml + base * 2);
-      if (ml.x == -INFINITY) continue;
-      const float f = exp2f(ml.x - M);
-      Lsum += ml.y * f;
-      const float2 v0 = load_coherent(p.part_o + base * D + e0), v1 = load_coherent(p.part_o + base * D + e0 + 2);
-      acc.x += v0.x * f;
-      acc.y += v0.y * f;
-      acc.z += v1.x * f;
-      acc.w += v1.y * f;
+  const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml), ro = coherent_rsrc(p.part_o);
+  for (int c0 = 0; c0 < ns; c0 += kMergeChunk) {
+    float2 ml[kItems][kMergeChunk];
+    f32x4_t ov[kItems][kMergeChunk];
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kMfmaThreads;
+      const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
+#pragma unroll
+      for (int k = 0; k < kMergeChunk; ++k) {
+        ml[it][k] = make_float2(-INFINITY, 0.f);
+        if (rr < nr && c0 + k < ns) {
+          const size_t row = (size_t)(x0 + c0 + k) * p.G + qr0 + rr;
+          ml[it][k] = load2_coherent(rml, row * 2 * sizeof(float));
+          ov[it][k] = load4_coherent(ro, (row * D + e0) * sizeof(float));
+        }
+      }
     }
-    const float inv = 1.f / Lsum;
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      float mc = M[it];
+#pragma unroll
+      for (int k = 0; k < kMergeChunk; ++k) mc = fmaxf(mc, ml[it][k].x);
+      const float sc = M[it] == -INFINITY ? 0.f : exp2f(M[it] - mc);
+      acc[it] *= sc;
+      Ls[it] *= sc;
+#pragma unroll
+      for (int k = 0; k < kMergeChunk; ++k) {
+        if (ml[it][k].x == -INFINITY) continue;
+        const float f = exp2f(ml[it][k].x - mc);
+        Ls[it] += ml[it][k].y * f;
+        acc[it] += ov[it][k] * f;
+      }
+      M[it] = mc;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int idx = threadIdx.x + it * kMfmaThreads;
+    const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
+    if (rr >= nr) continue;
+    const int r = qr0 + rr;
+    const float inv = 1.f / Ls[it];
     const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
     const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
-    store_out<QT>(p, ob + 0, acc.x * inv);
-    store_out<QT>(p, ob + 1, acc.y * inv);
-    store_out<QT>(p, ob + 2, acc.z * inv);
-    store_out<QT>(p, ob + 3, acc.w * inv);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) store_out<QT>(p, ob + k, acc[it][k] * inv);
   }
 }
 
@@ -481,16 +451,18 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   constexpr int NWV = kMfmaThreads / 64;
   constexpr int QSTR = D + 8;  // bf16 row stride of the staged queries
   extern __shared__ int s_pref[];
-  __shared__ __align__(16) uint16_t sQ[RPG * QSTR];
+  // The staged query rows (page walk) and the combine slots (after it) share LDS.
+  constexpr int TPR = combine_tiles(NT, MT);  // O^T tiles combined per round
+  constexpr int kQBytes = RPG * QSTR * 2, kXBytes = NWV * RPG * 16 * TPR * 4;
+  __shared__ __align__(16) char s_union[kQBytes > kXBytes ? kQBytes : kXBytes];
+  uint16_t* sQ = reinterpret_cast<uint16_t*>(s_union);
+  float* sm_x = reinterpret_cast<float*>(s_union);  // [wave][tile of the round][row][16 dims]
   // Block ids of the pages being walked. Reading them from LDS keeps the page
   // loads in flight: a vector load of a table entry would need vmcnt(0), which
   // also waits for every prefetched page.
   __shared__ int sTab[kTabChunk];
   __shared__ float sm_m[NWV][RPG];
   __shared__ float sm_l[NWV][RPG];
-  __shared__ __align__(16) float sm_x[NWV * RPG * 16];  // combine slots: [wave][row][16 dims]
-  __shared__ float s_inv[RPG];
-  __shared__ int s_slot[kMergeSlots];
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63, w = uni(threadIdx.x >> 6);
@@ -700,15 +672,21 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     }
     __syncthreads();
 
-    // Combine the waves tile by tile: in round mt every wave stores its O^T tile
-    // mt (16 dims x RPG rows) into its own LDS slot, then the workgroup's
-    // threads each take (row, 4 dims) of the tile, add the NWV slots with the
-    // row's factors 2^(m_w - M) (fixed order) and write the output -- or the
+    // Combine the waves TPR tiles per round: every wave stores its O^T tiles of
+    // the round (16 dims x RPG rows each) into its own LDS slot, then each
+    // thread takes (row, tile, 4 dims), adds the NWV slots with the row's
+    // factors 2^(m_w - M) (fixed order) and writes the output -- or the
     // partial -- directly.
     const bool final_out = kb == 1;
     const int slot = (int)x;
-    const int crow = threadIdx.x >> 2, cd4 = threadIdx.x & 3;  // combining thread: row, dims 4*cd4..+3
-    const bool combiner = crow < nr;
+    // Combining thread: tile of the round (slowest, so a wave reads 16
+    // consecutive rows of one tile: conflict-free), row, dims 4 * cd4 .. + 3.
+    // The thread index is made opaque here so that the combine's addresses are
+    // computed now, not hoisted over the page walk (where they would spill).
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int ct = tid / (4 * RPG), crow = (tid >> 2) % RPG, cd4 = tid & 3;
+    const bool combiner = ct < TPR && crow < nr;
     float cfac[NWV], cinv = 0.f, cM = 0.f, cL = 0.f;
     if (combiner) {
       cM = sm_m[0][crow];
@@ -723,27 +701,38 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       cinv = 1.f / cL;
     }
     const int cr = qr0 + crow;
-    size_t cbase;
+    const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml), ro = coherent_rsrc(p.part_o);
+    // Element offset of the thread's row in the output or in the partial slot
+    // (32-bit: both tensors are far below 2^31 elements here).
+    uint32_t cbase;
     if (final_out) {
       const int j = cr / p.ratio, hq = h * p.ratio + (cr - j * p.ratio);
-      cbase = (((size_t)b * p.C + j) * p.Hq + hq) * D;
+      cbase = (uint32_t)(((b * p.C + j) * p.Hq + hq) * D);
     } else {
-      cbase = ((size_t)slot * p.G + cr) * D;
-      if (combiner && cd4 == 0) store_coherent(p.part_ml + ((size_t)slot * p.G + cr) * 2, cM, cL);
+      cbase = (uint32_t)((slot * p.G + cr) * D);
+      if (combiner && ct == 0 && cd4 == 0) store2_coherent(rml, ((size_t)slot * p.G + cr) * 2 * sizeof(float), cM, cL);
     }
+    static_assert(MT % TPR == 0, "tiles per round must divide the tile count");
+    static_assert(4 * RPG * TPR <= kMfmaThreads, "one combining thread per (tile, row, 4 dims)");
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (mt > 0) __syncthreads();  // the previous round's readers are done
+    for (int mt0 = 0; mt0 < MT; mt0 += TPR) {
+      if (mt0 > 0) __syncthreads();  // the previous round's readers are done
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        *reinterpret_cast<f32x4_t*>(&sm_x[((w * RPG) + 16 * nt + i16) * 16 + 4 * g]) = o[mt][nt];
+      for (int t = 0; t < TPR; ++t)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          if (16 * nt + i16 < nr)  // rows past nr are padding
+            *reinterpret_cast<f32x4_t*>(&sm_x[(((w * TPR) + t) * RPG + 16 * nt + i16) * 16 + 4 * g]) = o[mt0 + t][nt];
       __syncthreads();
       if (combiner) {
-        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        f32x4_t v[NWV];
 #pragma unroll
         for (int ww = 0; ww < NWV; ++ww)
-          acc += *reinterpret_cast<const f32x4_t*>(&sm_x[((ww * RPG) + crow) * 16 + 4 * cd4]) * cfac[ww];
-        const int e0 = 16 * mt + 4 * cd4;
+          v[ww] = *reinterpret_cast<const f32x4_t*>(&sm_x[(((ww * TPR) + ct) * RPG + crow) * 16 + 4 * cd4]);
+        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ww = 0; ww < NWV; ++ww) acc += v[ww] * cfac[ww];
+        const int e0 = 16 * (mt0 + ct) + 4 * cd4;
         if (final_out) {
           if constexpr (QT == SPV_BF16) {
             *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + cbase + e0) =
@@ -753,8 +742,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
             for (int k = 0; k < 4; ++k) store_out<QT>(p, cbase + e0 + k, acc[k] * cinv);
           }
         } else {
-          store_coherent(p.part_o + cbase + e0, acc[0], acc[1]);
-          store_coherent(p.part_o + cbase + e0 + 2, acc[2], acc[3]);
+          store4_coherent(ro, (size_t)(cbase + e0) * sizeof(float), acc);
         }
       }
     }
@@ -769,10 +757,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         s_last = __hip_atomic_fetch_add(p.counters + seg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == kb;
       __syncthreads();
       if (s_last) {
-        // The merge weights reuse the query rows' LDS, dead after the page walk.
-        static_assert(sizeof(float) * RPG * kMergeSlots <= sizeof(sQ), "merge weights exceed sQ");
-        merge_segment<QT, RPG, D>(p, x0, kb, b, h, qr0, nr, reinterpret_cast<float(*)[kMergeSlots]>(sQ),
-                                  s_inv, s_slot);
+        merge_segment<QT, RPG, D>(p, x0, kb, b, h, qr0, nr);
         if (threadIdx.x == 0) p.counters[seg] = 0;
       }
     }
@@ -815,8 +800,12 @@ struct Plan {
 Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv_dtype, int q_dtype) {
   Plan pl{};
   const int G = C * (Hq / Hkv);
+  // The MFMA kernel addresses the output and the partial slots with 32-bit
+  // offsets (bytes for the partials).
+  const bool fits32 = (long long)B * C * Hq * d < (1LL << 31) &&
+                      (long long)kMfmaWGsMax * G * d * (long long)sizeof(float) < (1LL << 31);
   pl.mfma = kv_dtype == SPV_BF16 && q_dtype == SPV_BF16 && bs == 16 && (d == 128 || d == 64) && G >= 16 &&
-            B <= kMfmaMaxB;
+            B <= kMfmaMaxB && fits32;
   const int max_pages = (max_ctx + bs - 1) / bs;
   if (pl.mfma) {
     pl.nt = G >= 64 ? 4 : (G + 15) / 16;
