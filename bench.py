@@ -79,15 +79,24 @@ def workload_lens(seed=0):
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_attn_qwen15_b32_traffic.md")
 
 
+def attn_source_hash():
+    """Identifies the verify-attention source revision a profile was taken on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in ("verify_attn.hip", "spv_common.h"):
+        with open(os.path.join(PKG, "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
     """HBM bytes per verify-attention call from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel factor), or None
-    when the summary was taken on a different verify_attn.hip."""
-    import hashlib
-
+    when the summary was taken on a different verify-attention source."""
     try:
         text = open(TRAFFIC_PROFILE).read()
-        src = open(os.path.join(PKG, "csrc", "verify_attn.hip"), "rb").read()
+        src_hash = attn_source_hash()
     except OSError:
         return None
     fields = {}
@@ -95,7 +104,7 @@ def measured_traffic():
         if ":" in line:
             k, v = line.split(":", 1)
             fields[k.strip()] = v.strip().strip("`")
-    if fields.get("verify_attn.hip source hash") != hashlib.sha256(src).hexdigest()[:16]:
+    if fields.get("verify-attention source hash") != src_hash:
         return None
     try:
         return int(float(fields["traffic_bytes_per_call"]))

@@ -158,7 +158,13 @@ int spv_verify_attn(void* out, const void* q, int q_dtype,
 
 /* -------------------------------------------------------------- sampling */
 
-/* Workspace needed by spv_verify_sample. */
+/* Workspace needed by spv_verify_sample. Its first SPV_SAMPLE_COUNTER_BYTES
+ * hold per-sequence arrival counters (two per sequence, B <= 65535): they must
+ * be zero when a workspace is first used (allocate it zero-filled); every call
+ * leaves them zero again, whatever its B. Calls that share one workspace must
+ * be ordered (one stream); the attention and sampling entry points each need
+ * a workspace of their own. */
+#define SPV_SAMPLE_COUNTER_BYTES (1 << 19)
 size_t spv_verify_sample_workspace_bytes(int32_t B, int32_t gamma, int32_t V);
 
 /* One fused verify-sampling step: logits_to_probs (specdec/sampler.py:19-36)

@@ -100,60 +100,106 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
   }
 }
 
-// Copy of one token's K row (Hkv x d, contiguous per head) and V column
-// (transposed page: element (h, e) at ((h * d) + e) * bs + offset).
+// The K/V copy of an append: one workgroup per (batch entry b, kv head h,
+// block touched by the chunk) copies the chunk's tokens that fall in that block.
+//  * K rows of consecutive positions in one block are contiguous, so K moves in
+//    16-byte pieces.
+//  * The V page is transposed (element (h, e, o) at ((h * d) + e) * bs + o), so
+//    one dimension's keys of one block form a row of bs elements. Each
+//    dimension's row is written whole: the old row is read when the chunk
+//    covers it only in part, the new keys are placed, and the full row is
+//    stored. Element-sized stores at the row stride would leave partial memory
+//    bursts, which the memory controller completes by read-modify-write.
+constexpr int kWriteThreads = 256;
+
 template <int ES>
-__global__ __launch_bounds__(64) void kv_write_kernel(
+struct Elem;
+template <>
+struct Elem<4> {
+  using T = uint32_t;
+};
+template <>
+struct Elem<2> {
+  using T = uint16_t;
+};
+template <>
+struct Elem<1> {
+  using T = uint8_t;
+};
+
+template <int ES>
+__global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(
     uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool, const uint8_t* __restrict__ knew,
     const uint8_t* __restrict__ vnew, const int32_t* __restrict__ tables, int32_t maxb,
     const int32_t* __restrict__ nblocks, int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, const int32_t* __restrict__ ctr,
     int32_t C, int32_t layer, int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t limit_b) {
-  const int b = blockIdx.x / C, j = blockIdx.x % C;
+  using T = typename Elem<ES>::T;
+  const int b = blockIdx.x / hkv, h = blockIdx.x - b * hkv;
   // limit_b < 0: the allocation of this call recorded the failing sequence in ctr.
   if (limit_b < 0) {
     const int ex = ctr[CTR_EXHAUSTED];
-    limit_b = ex ? ex - 1 : C * gridDim.x;
+    limit_b = ex ? ex - 1 : 0x7fffffff;
   }
   if (b > limit_b) return;
   const int sid = seq_ids[b];
   const int s0 = start[b];
-  const int pos = s0 + j;
-  const int blk = pos / bs, off = pos - blk * bs;
-  const int nb = nblocks[sid];
-  if (blk >= nb) return;  // only possible for the failing sequence of an exhausted pool
+  // Positions s0 .. s0 + n - 1 have blocks; n < C only for the failing sequence
+  // of an exhausted pool.
+  const int n = min(C, nblocks[sid] * bs - s0);
+  if (n <= 0 || s0 < 0) return;
+  // The chunk extends the sequence's length to s0 + n.
+  if (h == 0 && blockIdx.y == 0 && threadIdx.x == 0 && seq_lens[sid] < s0 + n) seq_lens[sid] = s0 + n;
+  const int blk = s0 / bs + (int)blockIdx.y;
+  if (blk > (s0 + n - 1) / bs) return;
   const int phys = tables[(size_t)sid * maxb + blk];
   if ((unsigned)phys >= (unsigned)cap) return;  // never write outside the pool
-  const size_t page = ((size_t)layer * cap + phys) * hkv;  // first (block, head) slot
-  const size_t row_elems = (size_t)hkv * d;
-  const uint8_t* ksrc = knew + ((size_t)b * C + j) * row_elems * ES;
-  const uint8_t* vsrc = vnew + ((size_t)b * C + j) * row_elems * ES;
-  const int row_bytes = d * ES;
-  if ((row_bytes & 15) == 0) {
-    const int vec_per_head = row_bytes >> 4;
-    for (int t = threadIdx.x; t < hkv * vec_per_head; t += blockDim.x) {
-      const int h = t / vec_per_head, c = t - h * vec_per_head;
-      uint8_t* dst = kpool + ((page + h) * bs + off) * (size_t)row_bytes;
-      reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(ksrc + (size_t)h * row_bytes)[c];
+  // New keys of this block occupy row offsets [lo, hi); offset o holds chunk token o + jbase.
+  const int lo = max(s0, blk * bs) - blk * bs;
+  const int hi = min(s0 + n, (blk + 1) * bs) - blk * bs;
+  const int jbase = blk * bs - s0;
+  const size_t row_elems = (size_t)hkv * d;  // elements of one token's K (or V) over all heads
+  const size_t slot = (((size_t)layer * cap + phys) * hkv + h);  // the (block, head) page
+
+  const int kbytes = d * ES;
+  if ((kbytes & 15) == 0) {
+    const int vec = kbytes >> 4;
+    for (int t = threadIdx.x; t < (hi - lo) * vec; t += blockDim.x) {
+      const int o = lo + t / vec, c = t % vec;
+      uint8_t* dst = kpool + (slot * bs + o) * (size_t)kbytes;
+      const uint8_t* src = knew + (((size_t)b * C + jbase + o) * row_elems + (size_t)h * d) * ES;
+      reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(src)[c];
     }
   } else {
-    for (int t = threadIdx.x; t < hkv * row_bytes; t += blockDim.x) {
-      const int h = t / row_bytes, c = t - h * row_bytes;
-      kpool[((page + h) * bs + off) * (size_t)row_bytes + c] = ksrc[(size_t)h * row_bytes + c];
+    for (int t = threadIdx.x; t < (hi - lo) * kbytes; t += blockDim.x) {
+      const int o = lo + t / kbytes, c = t % kbytes;
+      kpool[(slot * bs + o) * (size_t)kbytes + c] =
+          knew[(((size_t)b * C + jbase + o) * row_elems + (size_t)h * d) * ES + c];
     }
   }
-  for (int t = threadIdx.x; t < hkv * d; t += blockDim.x) {
-    const int h = t / d, e = t - h * d;
-    uint8_t* dst = vpool + (((page + h) * d + e) * bs + off) * ES;
-    const uint8_t* src = vsrc + (size_t)t * ES;
-    if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
-    else if constexpr (ES == 2) *reinterpret_cast<uint16_t*>(dst) = *reinterpret_cast<const uint16_t*>(src);
-    else *dst = *src;
-  }
-  // The last token this call writes for the sequence extends its length.
-  if (threadIdx.x == 0) {
-    const int last_j = min(C - 1, nb * bs - 1 - s0);
-    if (j == last_j && seq_lens[sid] < pos + 1) seq_lens[sid] = pos + 1;
+
+  const bool whole = lo == 0 && hi == bs;
+  for (int e = threadIdx.x; e < d; e += blockDim.x) {
+    T* dst = reinterpret_cast<T*>(vpool) + (slot * d + e) * bs;
+    const T* src = reinterpret_cast<const T*>(vnew) + (size_t)b * C * row_elems + (size_t)h * d + e;
+    if (((bs * ES) & 15) == 0) {
+      constexpr int kPer = 16 / ES;
+      for (int c = 0; c < bs / kPer; ++c) {
+        union {
+          uint4 q;
+          T x[kPer];
+        } u;
+        if (!whole) u.q = reinterpret_cast<const uint4*>(dst)[c];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int o = c * kPer + k;
+          if (o >= lo && o < hi) u.x[k] = src[(size_t)(jbase + o) * row_elems];
+        }
+        reinterpret_cast<uint4*>(dst)[c] = u.q;
+      }
+    } else {
+      for (int o = lo; o < hi; ++o) dst[o] = src[(size_t)(jbase + o) * row_elems];
+    }
   }
 }
 
@@ -403,6 +449,7 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
       max_blocks_per_seq < 1 || write_limit_b < -1 || write_limit_b > B)
     return SPV_ERR_ARG;
   if (write_limit_b < 0 && (!may_alloc || !ctr)) return SPV_ERR_ARG;
+  if ((C + block_size - 1) / block_size + 1 > 65535) return SPV_ERR_ARG;  // blocks one chunk can touch
   if (B == 0) return SPV_OK;
   hipStream_t s = (hipStream_t)stream;
   if (may_alloc) {
@@ -412,7 +459,8 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
     SPV_CHECK_LAUNCH();
   }
   if (alloc_only) return SPV_OK;
-  const dim3 grid(B * C), blk(64);
+  // One workgroup per (entry, kv head, block the chunk can touch).
+  const dim3 grid(B * num_kv_heads, (C + block_size - 1) / block_size + 1), blk(kWriteThreads);
   auto* kp = static_cast<uint8_t*>(k_pool);
   auto* vp = static_cast<uint8_t*>(v_pool);
   auto* kn = static_cast<const uint8_t*>(k_new);

@@ -104,6 +104,57 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total)
   return wave_off + incl - v;
 }
 
+// Accesses for data handed between workgroups of one launch (partial results
+// merged by the last workgroup to arrive). The L2 caches of the XCDs are not
+// coherent with each other, so these go through raw buffer accesses with the
+// sc1 cache policy, which reach the device coherence point: a producer waits
+// for its stores to complete (s_waitcnt vmcnt(0)) before it counts itself in
+// with a device-scope atomic, and the consumer reads with the same policy.
+// Plain (non-atomic) accesses leave the compiler free to keep many in flight.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int kCoherent = 16;             // cache-policy operand: sc1
+constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit buffer descriptor, gfx9 family
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, kBufferWord3);
+}
+__device__ __forceinline__ void store_coherent_b128(__amdgpu_buffer_rsrc_t r, size_t byte_off, u32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)byte_off, 0, kCoherent);
+}
+__device__ __forceinline__ void store_coherent_b64(__amdgpu_buffer_rsrc_t r, size_t byte_off, u32x2_t v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)byte_off, 0, kCoherent);
+}
+__device__ __forceinline__ u32x4_t load_coherent_b128(__amdgpu_buffer_rsrc_t r, size_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCoherent);
+}
+__device__ __forceinline__ u32x2_t load_coherent_b64(__amdgpu_buffer_rsrc_t r, size_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, kCoherent);
+}
+
+// A raw buffer over `bytes` bytes for ordinary (cached) loads: loads past the
+// end return zero instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferWord3);
+}
+__device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
+}
+
+// Count one producer of `counter` in after all of this workgroup's coherent
+// stores have completed; true in every thread of the workgroup that completes
+// the count of `total`. That workgroup sets the counter back to zero.
+__device__ __forceinline__ bool arrive_last(int* counter, int total, int* s_flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == total;
+    if (last) *counter = 0;
+    *s_flag = last;
+  }
+  __syncthreads();
+  return *s_flag;
+}
+
 }  // namespace spv
 
 #define SPV_CHECK_LAUNCH()                                        \

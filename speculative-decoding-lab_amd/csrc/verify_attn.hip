@@ -251,29 +251,20 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
 }
 
 // Partials cross workgroups (and XCDs, whose L2s are not coherent with each
-// other): they are written and read through buffer accesses with the sc1
-// cache policy, which go to the device coherence point, so publishing them
-// needs only their completion (s_waitcnt), not a write-back of the whole L2.
-// Plain (non-atomic) accesses leave the compiler free to keep many in flight.
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-constexpr int kCoherent = 16;                 // cache-policy operand: sc1
-constexpr int kBufferWord3 = 0x00020000;      // raw 32-bit buffer descriptor, gfx9 family
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, kBufferWord3);
-}
+// other): they are written and read through the coherent buffer accesses of
+// spv_common.h, so publishing them needs only their completion (s_waitcnt),
+// not a write-back of the whole L2.
 __device__ __forceinline__ void store4_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off, f32x4_t v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)byte_off, 0, kCoherent);
+  store_coherent_b128(r, byte_off, __builtin_bit_cast(u32x4_t, v));
 }
 __device__ __forceinline__ void store2_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off, float a, float b) {
-  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{__float_as_uint(a), __float_as_uint(b)}, r, (int)byte_off, 0,
-                                        kCoherent);
+  store_coherent_b64(r, byte_off, u32x2_t{__float_as_uint(a), __float_as_uint(b)});
 }
 __device__ __forceinline__ f32x4_t load4_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off) {
-  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCoherent));
+  return __builtin_bit_cast(f32x4_t, load_coherent_b128(r, byte_off));
 }
 __device__ __forceinline__ float2 load2_coherent(__amdgpu_buffer_rsrc_t r, size_t byte_off) {
-  const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, kCoherent);
+  const u32x2_t v = load_coherent_b64(r, byte_off);
   return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
 }
 

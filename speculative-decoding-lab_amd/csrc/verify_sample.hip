@@ -13,14 +13,19 @@
 //
 // Kernels (HBM-bound; every logits row is read once by the stats pass, the one
 // raced row pair and its noise row once more by the race pass):
-//   1. row_stats  grid (chunks, rows): per 8192-entry chunk max & sum exp (or argmax)
-//   2. decide     grid (B): combine the chunks, gather p[x], q[x], decide k
-//   3. race       grid (chunks, B): residual sum and the top-2 of r/E per chunk
-//   4. finalize   grid (B): the draw, the accepted list, budget/eos cut, new_len
+//   1. row_stats  grid (chunks, B * rows): per 8192-entry chunk max & sum exp (or
+//                 argmax); the last workgroup of each sequence combines the
+//                 chunks, gathers p[x], q[x] and decides k (greedy: also commits)
+//   1'. decide    grid (B): the decision alone, for probability inputs
+//   2. race       grid (chunks, B): residual sum and the top-2 of r/E per chunk;
+//                 the last workgroup of each sequence makes the draw and the
+//                 accepted list, budget/eos cut and new_len
+// Workgroups hand their per-chunk results to the last one of a sequence through
+// coherent stores and an arrival counter per sequence (spv_common.h).
 // The race compares r/E instead of (r/t)/E (t, the residual sum, is only known
 // after the pass). Both orders agree whenever the two best r/E differ by more
 // than 1e-6 relative (rounding moves a key by at most 2^-23); a closer pair, or
-// an empty residual (t <= 1e-12), is re-raced exactly by the finalize kernel.
+// an empty residual (t <= 1e-12), is re-raced exactly by the finalizing workgroup.
 #include <math.h>
 
 #include "spv_common.h"
@@ -50,16 +55,23 @@ struct RacePart {
   float v1, v2;  // best and second-best r / E of the chunk
   int i1, i2;
   double rsum, psum;
-};
+};  // 32 bytes: two coherent 16-byte stores
 
 struct SampleWs {
-  float* stat_m;   // [rows][nch]
-  float* stat_s;   // [rows][nch] (sum exp, or argmax index bits in greedy mode)
+  int* cnt_stats;  // [B] row-stats workgroups of each sequence that have finished
+  int* cnt_race;   // [B] race workgroups of each sequence that have finished
+  float2* stat;    // [B][2 gamma + 1]: (max, sum exp), or (max, argmax index bits) when greedy
   RaceInfo* info;  // [B]
   RacePart* race;  // [B][nch]
 };
 
 __host__ __device__ inline int num_chunks(int V) { return (V + kChunk - 1) / kChunk; }
+
+// The arrival counters sit at fixed offsets at the head of the workspace (the
+// same for every B): they must be zero when a workspace is first used, and
+// every call leaves them zero.
+constexpr int kCounterSeqs = SPV_SAMPLE_COUNTER_BYTES / (2 * sizeof(int));
+static_assert(kCounterSeqs >= 65535, "one counter pair per sequence of the largest batch");
 
 size_t ws_layout(int B, int gamma, int V, SampleWs* ws, void* base) {
   const int nch = num_chunks(V);
@@ -70,14 +82,15 @@ size_t ws_layout(int B, int gamma, int V, SampleWs* ws, void* base) {
     off += (bytes + 255) & ~(size_t)255;
     return o;
   };
-  const size_t o_m = take(rows * nch * sizeof(float));
-  const size_t o_s = take(rows * nch * sizeof(float));
+  const size_t o_cnt = take(SPV_SAMPLE_COUNTER_BYTES);
+  const size_t o_stat = take(rows * sizeof(float2));
   const size_t o_info = take((size_t)B * sizeof(RaceInfo));
   const size_t o_race = take((size_t)B * nch * sizeof(RacePart));
   if (ws && base) {
     char* c = static_cast<char*>(base);
-    ws->stat_m = reinterpret_cast<float*>(c + o_m);
-    ws->stat_s = reinterpret_cast<float*>(c + o_s);
+    ws->cnt_stats = reinterpret_cast<int*>(c + o_cnt);
+    ws->cnt_race = ws->cnt_stats + kCounterSeqs;
+    ws->stat = reinterpret_cast<float2*>(c + o_stat);
     ws->info = reinterpret_cast<RaceInfo*>(c + o_info);
     ws->race = reinterpret_cast<RacePart*>(c + o_race);
   }
@@ -207,103 +220,13 @@ __device__ __forceinline__ double block_sum_f64(double x) {
   return t;
 }
 
-__device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int row, int B,
-                                                int gamma, int V) {
-  const int C = gamma + 1;
-  return row < B * C ? target + (size_t)row * V : draft + (size_t)(row - B * C) * V;
-}
-
 // x = z / T in float32 (torch divides the fp32 tensor by the scalar in fp32).
 __device__ __forceinline__ float scaled(float z, float tf, bool unit) { return unit ? z : z / tf; }
 
 // Element i of this thread's slice of a chunk: 8 float4 per thread.
 __device__ __forceinline__ int vec_index(int c, int k) { return c * (kChunk / 4) + threadIdx.x + k * kThreads; }
 
-// ------------------------------------------------------------- 1. row stats
-template <bool GREEDY>
-__global__ __launch_bounds__(kThreads) void row_stats_kernel(const float* __restrict__ target,
-                                                             const float* __restrict__ draft, int B,
-                                                             int gamma, int V, float tf, SampleWs ws) {
-  const int c = blockIdx.x, row = blockIdx.y, nch = gridDim.x;
-  const float* z = row_ptr(target, draft, row, B, gamma, V);
-  const bool unit = tf == 1.0f;
-  float bv = -INFINITY, m = -INFINITY, s = 0.f;
-  int bi = 0x7fffffff;
-  if ((V & 3) == 0) {
-    // All loads of the slice are issued before any is used.
-    const int n4 = V >> 2;
-    float4 v[kVecPerThread];
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i4 = vec_index(c, k);
-      v[k] = i4 < n4 ? reinterpret_cast<const float4*>(z)[i4]
-                     : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-    }
-    if (GREEDY) {
-#pragma unroll
-      for (int k = 0; k < kVecPerThread; ++k) {
-        const int i = 4 * vec_index(c, k);
-        if (i >= V) continue;
-        if (better(v[k].x, i, bv, bi)) bv = v[k].x, bi = i;
-        if (better(v[k].y, i + 1, bv, bi)) bv = v[k].y, bi = i + 1;
-        if (better(v[k].z, i + 2, bv, bi)) bv = v[k].z, bi = i + 2;
-        if (better(v[k].w, i + 3, bv, bi)) bv = v[k].w, bi = i + 3;
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < kVecPerThread; ++k) {
-        v[k].x = scaled(v[k].x, tf, unit);
-        v[k].y = scaled(v[k].y, tf, unit);
-        v[k].z = scaled(v[k].z, tf, unit);
-        v[k].w = scaled(v[k].w, tf, unit);
-        m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
-      }
-      if (m != -INFINITY) {
-#pragma unroll
-        for (int k = 0; k < kVecPerThread; ++k)
-          s += exp2f((v[k].x - m) * kLog2e) + exp2f((v[k].y - m) * kLog2e) + exp2f((v[k].z - m) * kLog2e) +
-               exp2f((v[k].w - m) * kLog2e);
-      }
-    }
-  } else {
-    const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
-    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
-      const float zi = z[i];
-      if (GREEDY) {
-        if (better(zi, i, bv, bi)) bv = zi, bi = i;
-      } else {
-        const float x = scaled(zi, tf, unit);
-        if (x > m) {
-          s = (m == -INFINITY) ? 0.f : s * exp2f((m - x) * kLog2e);
-          m = x;
-        }
-        s += exp2f((x - m) * kLog2e);
-      }
-    }
-  }
-  if (GREEDY) {
-    block_argmax(bv, bi);
-    if (threadIdx.x == 0) {
-      ws.stat_m[(size_t)row * nch + c] = bv;
-      ws.stat_s[(size_t)row * nch + c] = __int_as_float(bi);
-    }
-  } else {
-    __shared__ float sm[kThreads / 64], ss[kThreads / 64];
-    wave_lse(m, s);
-    if ((threadIdx.x & 63) == 0) {
-      sm[threadIdx.x >> 6] = m;
-      ss[threadIdx.x >> 6] = s;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int k = 1; k < kThreads / 64; ++k) lse_combine(m, s, sm[k], ss[k]);
-      ws.stat_m[(size_t)row * nch + c] = m;
-      ws.stat_s[(size_t)row * nch + c] = s;
-    }
-  }
-}
-
-// -------------------------------------------------------------- 2. decide
+// ------------------------------------------------------------ arguments
 struct DecideArgs {
   const float* target;
   const float* draft;
@@ -316,211 +239,6 @@ struct DecideArgs {
   float tf;
 };
 
-// p[x] of a softmax row, float32 as torch.softmax forms it: exp(x - max) / sum.
-__device__ __forceinline__ float softmax_at(float z, float m, float s, float tf) {
-  const float x = tf == 1.0f ? z : z / tf;
-  return expf(x - m) / s;
-}
-
-__global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a, SampleWs ws) {
-  const int b = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int C = a.gamma + 1, nch = num_chunks(a.V), nrows = 2 * a.gamma + 1;
-  const bool greedy = a.greedy && !a.is_probs;
-  // Row r < C: target row r; row C + j: draft row j.
-  __shared__ float s_m[65], s_s[65];
-  __shared__ int s_am[65];
-  __shared__ float s_zp[32], s_zq[32];
-  if (!a.is_probs) {
-    for (int r = w; r < nrows; r += blockDim.x >> 6) {
-      const int grow = r < C ? b * C + r : a.B * C + b * a.gamma + (r - C);
-      if (greedy) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int c = lane; c < nch; c += 64) {
-          const float v = ws.stat_m[(size_t)grow * nch + c];
-          const int i = __float_as_int(ws.stat_s[(size_t)grow * nch + c]);
-          if (better(v, i, bv, bi)) bv = v, bi = i;
-        }
-        wave_argmax(bv, bi);
-        if (lane == 0) s_am[r] = bi;
-      } else {
-        float mm = -INFINITY, ss = 0.f;
-        for (int c = lane; c < nch; c += 64)
-          lse_combine(mm, ss, ws.stat_m[(size_t)grow * nch + c], ws.stat_s[(size_t)grow * nch + c]);
-        wave_lse(mm, ss);
-        if (lane == 0) {
-          s_m[r] = mm;
-          s_s[r] = ss;
-        }
-      }
-    }
-  }
-  // Gather the target / draft entries at the proposals, one lane each.
-  if (threadIdx.x < a.gamma) {
-    const int j = threadIdx.x;
-    const int x = a.proposals[(size_t)b * a.gamma + j];
-    float zp = 0.f, zq = 0.f;
-    if ((unsigned)x < (unsigned)a.V && !greedy) {  // an out-of-vocabulary proposal is never read
-      zp = a.target[((size_t)b * C + j) * a.V + x];
-      zq = a.draft[((size_t)b * a.gamma + j) * a.V + x];
-    }
-    s_zp[j] = zp;
-    s_zq[j] = zq;
-  }
-  __syncthreads();
-  if (threadIdx.x != 0) return;
-
-  int k = a.gamma;
-  for (int j = 0; j < a.gamma; ++j) {
-    const int x = a.proposals[(size_t)b * a.gamma + j];
-    float pp, qq;
-    if ((unsigned)x >= (unsigned)a.V) {
-      pp = qq = 0.f;
-    } else if (a.is_probs) {
-      pp = s_zp[j];
-      qq = s_zq[j];
-    } else if (greedy) {
-      pp = s_am[j] == x ? 1.f : 0.f;
-      qq = s_am[C + j] == x ? 1.f : 0.f;
-    } else {
-      pp = softmax_at(s_zp[j], s_m[j], s_s[j], a.tf);
-      qq = softmax_at(s_zq[j], s_m[C + j], s_s[C + j], a.tf);
-    }
-    const double qd = (double)qq, pd = (double)pp;
-    const double acc = qd <= kEps ? (pd > kEps ? 1.0 : 0.0) : fmin(1.0, pd / qd);
-    if (a.accept_prob) a.accept_prob[(size_t)b * a.gamma + j] = acc;
-    if (k == a.gamma && !((double)a.u[(size_t)b * a.gamma + j] < acc)) {
-      k = j;
-      if (!a.accept_prob) break;
-    }
-  }
-  if (a.decide_only) return;
-  RaceInfo info{};
-  info.k = k;
-  info.mode = k < a.gamma ? RACE_RESIDUAL : RACE_BONUS;
-  info.token = -1;
-  if (greedy) {
-    // One-hot rows: the residual is one-hot at the target argmax (or equals p,
-    // when both rows agree), and the bonus row is one-hot: the draw is the
-    // target row's argmax for any positive finite E.
-    info.token = s_am[k];
-    info.mode = RACE_NONE;
-  } else if (!a.is_probs) {
-    info.mp = s_m[k];
-    info.sp = s_s[k];
-    if (k < a.gamma) {
-      info.mq = s_m[C + k];
-      info.sq = s_s[C + k];
-    }
-  }
-  ws.info[b] = info;
-  a.accept_len[b] = k;
-  for (int j = 0; j < C; ++j)
-    a.out_tokens[(size_t)b * C + j] = j < k ? a.proposals[(size_t)b * a.gamma + j] : -1;
-}
-
-// Probability of element i of the raced target (p) / draft (q) row.
-struct RaceRows {
-  const float* p;
-  const float* q;
-  float mp, isp, mq, isq, tf;
-  bool probs, unit;
-  __device__ __forceinline__ float prob(float z, float m, float is) const {
-    return probs ? z : exp2f((scaled(z, tf, unit) - m) * kLog2e) * is;
-  }
-  __device__ __forceinline__ float pval(float z) const { return prob(z, mp, isp); }
-  __device__ __forceinline__ float qval(float z) const { return prob(z, mq, isq); }
-};
-
-__device__ __forceinline__ RaceRows race_rows(const DecideArgs& a, const RaceInfo& info, int b) {
-  const int C = a.gamma + 1;
-  RaceRows r;
-  r.p = a.target + ((size_t)b * C + info.k) * a.V;
-  r.q = info.k < a.gamma ? a.draft + ((size_t)b * a.gamma + info.k) * a.V : nullptr;
-  r.mp = info.mp;
-  r.isp = 1.f / info.sp;
-  r.mq = info.mq;
-  r.isq = info.k < a.gamma ? 1.f / info.sq : 0.f;
-  r.tf = a.tf;
-  r.probs = a.is_probs;
-  r.unit = a.tf == 1.0f;
-  return r;
-}
-
-// ---------------------------------------------------------------- 3. race
-__global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, const float* __restrict__ noise,
-                                                        SampleWs ws) {
-  const int c = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
-  const RaceInfo info = ws.info[b];
-  if (info.mode == RACE_NONE) return;
-  const RaceRows rr = race_rows(a, info, b);
-  const bool resid = info.mode == RACE_RESIDUAL;
-  const float* e = noise + (size_t)b * a.V;
-  Top2 t2;
-  t2.init();
-  float rs = 0.f, ps = 0.f;
-  auto visit = [&](int i, float zp, float zq, float ei) {
-    const float p = rr.pval(zp);
-    float r = p;
-    if (resid) {
-      const float d = p - rr.qval(zq);
-      r = d < 0.f ? 0.f : d;  // torch.clamp(p - q, min=0): NaN stays NaN
-      rs += r;
-      ps += p;
-    }
-    t2.push(r / ei, i);
-  };
-  if ((a.V & 3) == 0) {
-    const int n4 = a.V >> 2;
-    float4 zp[kVecPerThread], zq[kVecPerThread], ev[kVecPerThread];
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i4 = vec_index(c, k);
-      if (i4 < n4) {
-        zp[k] = reinterpret_cast<const float4*>(rr.p)[i4];
-        zq[k] = resid ? reinterpret_cast<const float4*>(rr.q)[i4] : zp[k];
-        ev[k] = reinterpret_cast<const float4*>(e)[i4];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i4 = vec_index(c, k);
-      if (i4 >= n4) continue;
-      visit(4 * i4 + 0, zp[k].x, zq[k].x, ev[k].x);
-      visit(4 * i4 + 1, zp[k].y, zq[k].y, ev[k].y);
-      visit(4 * i4 + 2, zp[k].z, zq[k].z, ev[k].z);
-      visit(4 * i4 + 3, zp[k].w, zq[k].w, ev[k].w);
-    }
-  } else {
-    const int i0 = c * kChunk, i1 = min(a.V, i0 + kChunk);
-    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) visit(i, rr.p[i], resid ? rr.q[i] : 0.f, e[i]);
-  }
-  t2.wave_reduce();
-  __shared__ float s_v1[kThreads / 64], s_v2[kThreads / 64];
-  __shared__ int s_i1[kThreads / 64], s_i2[kThreads / 64];
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    s_v1[w] = t2.v1;
-    s_v2[w] = t2.v2;
-    s_i1[w] = t2.i1;
-    s_i2[w] = t2.i2;
-  }
-  const double rsum = block_sum_f64((double)rs);
-  const double psum = block_sum_f64((double)ps);
-  if (threadIdx.x == 0) {
-    for (int k = 1; k < kThreads / 64; ++k) t2.merge(s_v1[k], s_i1[k], s_v2[k], s_i2[k]);
-    RacePart part;
-    part.v1 = t2.v1;
-    part.v2 = t2.v2;
-    part.i1 = t2.i1;
-    part.i2 = t2.i2;
-    part.rsum = rsum;
-    part.psum = psum;
-    ws.race[(size_t)b * nch + c] = part;
-  }
-}
-
-// ------------------------------------------------------------ 4. finalize
 struct CommitArgs {
   const int32_t* start;
   const int32_t* remaining;
@@ -531,83 +249,25 @@ struct CommitArgs {
   int32_t* new_len;
 };
 
-__global__ __launch_bounds__(kThreads) void finalize_kernel(DecideArgs a, CommitArgs cm, SampleWs ws) {
-  const int b = blockIdx.x;
-  const int C = a.gamma + 1, nch = num_chunks(a.V);
-  const RaceInfo info = ws.info[b];
-  int token = info.token;
-  if (info.mode != RACE_NONE) {
-    __shared__ int s_token, s_exact;
-    __shared__ float s_t, s_psum;
-    if (threadIdx.x < 64) {
-      Top2 t2;
-      t2.init();
-      double rs = 0.0, ps = 0.0;
-      for (int c = threadIdx.x; c < nch; c += 64) {
-        const RacePart part = ws.race[(size_t)b * nch + c];
-        t2.merge(part.v1, part.i1, part.v2, part.i2);
-        rs += part.rsum;
-        ps += part.psum;
-      }
-      t2.wave_reduce();
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        rs += __shfl_xor(rs, o, 64);
-        ps += __shfl_xor(ps, o, 64);
-      }
-      if (threadIdx.x == 0) {
-        int exact = 0;
-        if (info.mode == RACE_RESIDUAL) {
-          const float t = (float)rs;  // fp32 sum, accumulated in fp64 and rounded once
-          s_t = t;
-          s_psum = fmaxf((float)ps, 1e-12f);  // p.sum().clamp_min(1e-12)
-          if ((double)t <= kEps) exact = 2;                      // race p / sum(p) instead
-          else if (!isnan(t2.v1) && !(t2.v1 - t2.v2 > kTieRel * t2.v1)) exact = 1;  // near tie
-        }
-        s_exact = exact;
-        s_token = t2.i1;
-      }
-    }
-    __syncthreads();
-    if (s_exact) {
-      // Exact race over the whole row with the normaliser known (rare).
-      const RaceRows rr = race_rows(a, info, b);
-      const float* e = cm.noise + (size_t)b * a.V;
-      const float t = s_t, psum = s_psum;
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
-        const float p = rr.pval(rr.p[i]);
-        float rhat;
-        if (s_exact == 2) {
-          rhat = p / psum;
-        } else {
-          const float d = p - rr.qval(rr.q[i]);
-          rhat = (d < 0.f ? 0.f : d) / t;
-        }
-        const float key = rhat / e[i];
-        if (better(key, i, bv, bi)) bv = key, bi = i;
-      }
-      block_argmax(bv, bi);
-      token = bi;
-    } else {
-      token = s_token;
-    }
-  }
-  if (threadIdx.x != 0) return;
-  const int k = info.k;
-  a.out_tokens[(size_t)b * C + k] = token;
-  // Commit cut (spec_scheduler.py:274-303): budget with Python slice semantics,
-  // then the first eos (not kept).
+constexpr int kWaves = kThreads / 64;
+
+// p[x] of a softmax row, float32 as torch.softmax forms it: exp(x - max) / sum.
+__device__ __forceinline__ float softmax_at(float z, float m, float s, float tf) {
+  const float x = tf == 1.0f ? z : z / tf;
+  return expf(x - m) / s;
+}
+
+// Commit cut of one sequence (spec_scheduler.py:274-303): the budget with
+// Python slice semantics, then the first eos (not kept). `xs` holds the
+// proposals; `rem` and `st` are remaining[b] and start[b] (loaded early).
+__device__ __forceinline__ void commit_cut(const DecideArgs& a, const CommitArgs& cm, int b, int k, int token, const int* xs,
+                           int rem, int st) {
   int n = k + 1;
   bool fin = false;
-  if (cm.remaining) {
-    const int rem = cm.remaining[b];
-    if (n > rem) n = rem >= 0 ? rem : max(0, n + rem);
-  }
+  if (cm.remaining && n > rem) n = rem >= 0 ? rem : max(0, n + rem);
   if (cm.eos >= 0) {
     for (int i = 0; i < n; ++i) {
-      const int tok = i < k ? a.proposals[(size_t)b * a.gamma + i] : token;
+      const int tok = i < k ? xs[i] : token;
       if (tok == cm.eos) {
         n = i;
         fin = true;
@@ -616,10 +276,431 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(DecideArgs a, Commit
     }
   }
   if (n == 0) fin = true;
-  if (cm.remaining && n >= cm.remaining[b]) fin = true;
+  if (cm.remaining && n >= rem) fin = true;
   if (cm.n_commit) cm.n_commit[b] = n;
   if (cm.finished) cm.finished[b] = fin ? 1 : 0;
-  if (cm.new_len) cm.new_len[b] = n > 0 ? (cm.start ? cm.start[b] : 0) + n : -1;
+  if (cm.new_len) cm.new_len[b] = n > 0 ? st + n : -1;
+}
+
+// ------------------------------------------------------------- decision
+// Decision of sequence b (spec_scheduler.py:60-77): accept x_j while
+// (double)u_j < min(1, p_j[x_j] / q_j[x_j]), and record the draw to make.
+// Runs in one whole workgroup. In logits mode the row statistics of the
+// sequence were published by the row-stats workgroups with coherent stores and
+// are read the same way here. In greedy mode the draw is the target row's
+// argmax, so the commit is finished here as well.
+enum InputMode : int { IN_PROBS = 0, IN_LOGITS = 1, IN_GREEDY = 2 };
+
+template <int MODE>
+__device__ __forceinline__ void decide_seq(const DecideArgs& a, const CommitArgs& cm, const SampleWs& ws, int b) {
+  const int C = a.gamma + 1, nrows = 2 * a.gamma + 1;
+  constexpr bool greedy = MODE == IN_GREEDY;
+  __shared__ float s_m[2 * 32 + 1], s_s[2 * 32 + 1];
+  __shared__ int s_am[2 * 32 + 1];
+  __shared__ float s_zp[32], s_zq[32], s_u[32];
+  __shared__ int s_x[32];
+  __shared__ int s_k, s_tok;
+  // Loads in flight together: proposals and uniforms, the row statistics, and
+  // the start / budget of the commit; then the entries at the proposals.
+  const int t = threadIdx.x;
+  int x = -1;
+  if (t < a.gamma) {
+    x = a.proposals[(size_t)b * a.gamma + t];
+    s_u[t] = a.u[(size_t)b * a.gamma + t];
+  }
+  int rem = 0, st = 0;
+  if (t == 0 && greedy && !a.decide_only) {
+    if (cm.remaining) rem = cm.remaining[b];
+    if (cm.start) st = cm.start[b];
+  }
+  if (MODE != IN_PROBS && t < nrows) {
+    const u32x2_t v = load_coherent_b64(coherent_rsrc(ws.stat), ((size_t)b * nrows + t) * sizeof(float2));
+    if (greedy) {
+      s_am[t] = (int)v.y;
+    } else {
+      s_m[t] = __uint_as_float(v.x);
+      s_s[t] = __uint_as_float(v.y);
+    }
+  }
+  if (t < a.gamma) {
+    float zp = 0.f, zq = 0.f;
+    if ((unsigned)x < (unsigned)a.V && !greedy) {  // an out-of-vocabulary proposal is never read
+      zp = a.target[((size_t)b * C + t) * a.V + x];
+      zq = a.draft[((size_t)b * a.gamma + t) * a.V + x];
+    }
+    s_x[t] = x;
+    s_zp[t] = zp;
+    s_zq[t] = zq;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int k = a.gamma;
+    for (int j = 0; j < a.gamma; ++j) {
+      const int xj = s_x[j];
+      float pp, qq;
+      if ((unsigned)xj >= (unsigned)a.V) {
+        pp = qq = 0.f;
+      } else if (MODE == IN_PROBS) {
+        pp = s_zp[j];
+        qq = s_zq[j];
+      } else if (greedy) {
+        pp = s_am[j] == xj ? 1.f : 0.f;
+        qq = s_am[C + j] == xj ? 1.f : 0.f;
+      } else {
+        pp = softmax_at(s_zp[j], s_m[j], s_s[j], a.tf);
+        qq = softmax_at(s_zq[j], s_m[C + j], s_s[C + j], a.tf);
+      }
+      const double qd = (double)qq, pd = (double)pp;
+      const double acc = qd <= kEps ? (pd > kEps ? 1.0 : 0.0) : fmin(1.0, pd / qd);
+      if (a.accept_prob) a.accept_prob[(size_t)b * a.gamma + j] = acc;
+      if (k == a.gamma && !((double)s_u[j] < acc)) {
+        k = j;
+        if (!a.accept_prob) break;
+      }
+    }
+    s_k = k;
+    // One-hot rows: the residual is one-hot at the target argmax (or equals p,
+    // when both rows agree), and the bonus row is one-hot: the draw is the
+    // target row's argmax for any positive finite E.
+    s_tok = greedy ? s_am[k] : -1;
+    if (!a.decide_only) {
+      RaceInfo info{};
+      info.k = k;
+      info.mode = greedy ? RACE_NONE : k < a.gamma ? RACE_RESIDUAL : RACE_BONUS;
+      info.token = s_tok;
+      if (MODE == IN_LOGITS) {
+        info.mp = s_m[k];
+        info.sp = s_s[k];
+        if (k < a.gamma) {
+          info.mq = s_m[C + k];
+          info.sq = s_s[C + k];
+        }
+      }
+      ws.info[b] = info;
+      a.accept_len[b] = k;
+      if (greedy) commit_cut(a, cm, b, k, s_tok, s_x, rem, st);
+    }
+  }
+  __syncthreads();
+  if (a.decide_only) return;
+  const int k = s_k;
+  if (t < C) a.out_tokens[(size_t)b * C + t] = t < k ? s_x[t] : (t == k && greedy ? s_tok : -1);
+}
+
+// ------------------------------------------------------------- 1. row stats
+// One workgroup per row: grid (B * (2 gamma + 1)), sequence b's rows
+// consecutive (row r < gamma + 1 is target row r, row gamma + 1 + j is draft
+// row j). The row streams through the workgroup in steps of kStepVec float4
+// per thread, the next step's loads in flight while one is reduced. The last
+// row of a sequence to finish makes its decision.
+constexpr int kStepVec = 8;
+
+template <int MODE, bool UNIT>
+__global__ __launch_bounds__(kThreads) void row_stats_kernel(DecideArgs a, CommitArgs cm, SampleWs ws) {
+  constexpr bool GREEDY = MODE == IN_GREEDY;
+  const int nrows = 2 * a.gamma + 1, C = a.gamma + 1;
+  const int b = blockIdx.x / nrows, r = blockIdx.x - b * nrows;
+  const float* z = r < C ? a.target + ((size_t)b * C + r) * a.V : a.draft + ((size_t)b * a.gamma + (r - C)) * a.V;
+  const int V = a.V;
+  const float tf = a.tf;
+  float bv = -INFINITY, m = -INFINITY, s = 0.f;
+  int bi = 0x7fffffff;
+  // Softmax statistics of a run of values (already scaled), all of index order.
+  auto absorb = [&](const float* xs, int n) {
+    float mx = m;
+    for (int q = 0; q < n; ++q) mx = fmaxf(mx, xs[q]);
+    if (mx == -INFINITY) return;
+    if (mx > m) {
+      s = m == -INFINITY ? 0.f : s * exp2f((m - mx) * kLog2e);
+      m = mx;
+    }
+    for (int q = 0; q < n; ++q) s += exp2f((xs[q] - m) * kLog2e);
+  };
+  auto greedy_visit = [&](float v, int i) {
+    // Indices rise within a thread, so an equal later value never wins.
+    if (!(v <= bv) && better(v, i, bv, bi)) bv = v, bi = i;
+  };
+  if ((V & 3) == 0) {
+    const int n4 = V >> 2;
+    const __amdgpu_buffer_rsrc_t rz = span_rsrc(z, (uint32_t)V * 4u);
+    constexpr int kStep = kStepVec * kThreads;
+    const int nstep = (n4 + kStep - 1) / kStep;
+    u32x4_t cur[kStepVec], nxt[kStepVec];
+#pragma unroll
+    for (int k = 0; k < kStepVec; ++k) cur[k] = load_b128(rz, (uint32_t)(threadIdx.x + k * kThreads) * 16u);
+    for (int stp = 0; stp < nstep; ++stp) {
+      const int base = stp * kStep;
+      // Past the row end the buffer loads return zero; those entries are skipped.
+#pragma unroll
+      for (int k = 0; k < kStepVec; ++k)
+        nxt[k] = load_b128(rz, (uint32_t)(base + kStep + threadIdx.x + k * kThreads) * 16u);
+      float xs[4 * kStepVec];
+#pragma unroll
+      for (int k = 0; k < kStepVec; ++k) {
+        const int i4 = base + threadIdx.x + k * kThreads;
+        const bool ok = i4 < n4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = __uint_as_float(cur[k][e]);
+          if (GREEDY) {
+            if (ok) greedy_visit(v, 4 * i4 + e);
+          } else {
+            xs[4 * k + e] = ok ? (UNIT ? v : v / tf) : -INFINITY;
+          }
+        }
+      }
+      if (!GREEDY) absorb(xs, 4 * kStepVec);
+#pragma unroll
+      for (int k = 0; k < kStepVec; ++k) cur[k] = nxt[k];
+    }
+  } else {
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+      const float zi = z[i];
+      if (GREEDY) {
+        greedy_visit(zi, i);
+      } else {
+        const float x = UNIT ? zi : zi / tf;
+        absorb(&x, 1);
+      }
+    }
+  }
+  const size_t slot = ((size_t)b * nrows + r) * sizeof(float2);
+  if (GREEDY) {
+    block_argmax(bv, bi);
+    if (threadIdx.x == 0) store_coherent_b64(coherent_rsrc(ws.stat), slot, u32x2_t{__float_as_uint(bv), (unsigned)bi});
+  } else {
+    __shared__ float sm[kWaves], ss[kWaves];
+    wave_lse(m, s);
+    if ((threadIdx.x & 63) == 0) {
+      sm[threadIdx.x >> 6] = m;
+      ss[threadIdx.x >> 6] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int k = 1; k < kWaves; ++k) lse_combine(m, s, sm[k], ss[k]);
+      store_coherent_b64(coherent_rsrc(ws.stat), slot, u32x2_t{__float_as_uint(m), __float_as_uint(s)});
+    }
+  }
+  __shared__ int s_last;
+  if (arrive_last(ws.cnt_stats + b, nrows, &s_last)) decide_seq<MODE>(a, cm, ws, b);
+}
+
+// Decision without row statistics (probability inputs): grid (B).
+__global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a, CommitArgs cm, SampleWs ws) {
+  decide_seq<IN_PROBS>(a, cm, ws, blockIdx.x);
+}
+
+// ------------------------------------------------------------ finalize
+// Probability of element i of the raced target (p) / draft (q) row, as torch
+// forms it: exp(x - max) / sum with x = z / T (exact re-race only).
+__device__ __forceinline__ float exact_prob(float z, float m, float s, float tf, bool probs) {
+  return probs ? z : softmax_at(z, m, s, tf);
+}
+
+// The draw and the commit of sequence b, in the workgroup that completed its
+// race: combine the per-chunk top-2 (coherent loads), re-race exactly when the
+// best two keys are within kTieRel or the residual is empty, then cut.
+__device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitArgs& cm, const SampleWs& ws, int b,
+                                             const RaceInfo& info) {
+  const int C = a.gamma + 1, nch = num_chunks(a.V);
+  __shared__ int s_token, s_exact;
+  __shared__ float s_t, s_psum;
+  __shared__ int s_x[32];
+  if ((int)threadIdx.x < info.k) s_x[threadIdx.x] = a.proposals[(size_t)b * a.gamma + threadIdx.x];
+  int rem = 0, st = 0;
+  if (threadIdx.x == 0) {
+    if (cm.remaining) rem = cm.remaining[b];
+    if (cm.start) st = cm.start[b];
+  }
+  if (info.mode == RACE_NONE) {
+    if (threadIdx.x == 0) s_token = info.token, s_exact = 0;
+  } else if (threadIdx.x < 64) {
+    const __amdgpu_buffer_rsrc_t rr = coherent_rsrc(ws.race);
+    Top2 t2;
+    t2.init();
+    double rs = 0.0, ps = 0.0;
+    for (int c = threadIdx.x; c < nch; c += 64) {
+      const size_t o = ((size_t)b * nch + c) * sizeof(RacePart);
+      const u32x4_t lo = load_coherent_b128(rr, o), hi = load_coherent_b128(rr, o + 16);
+      t2.merge(__uint_as_float(lo.x), (int)lo.z, __uint_as_float(lo.y), (int)lo.w);
+      rs += __hiloint2double((int)hi.y, (int)hi.x);
+      ps += __hiloint2double((int)hi.w, (int)hi.z);
+    }
+    t2.wave_reduce();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      rs += __shfl_xor(rs, o, 64);
+      ps += __shfl_xor(ps, o, 64);
+    }
+    if (threadIdx.x == 0) {
+      int exact = 0;
+      const bool tie = !isnan(t2.v1) && !(t2.v1 - t2.v2 > kTieRel * t2.v1);
+      if (info.mode == RACE_RESIDUAL) {
+        const float t = (float)rs;  // fp32 sum, accumulated in fp64 and rounded once
+        s_t = t;
+        s_psum = fmaxf((float)ps, 1e-12f);  // p.sum().clamp_min(1e-12)
+        if ((double)t <= kEps) exact = 2;  // race p / sum(p) instead
+        else if (tie) exact = 1;
+      } else if (tie) {
+        exact = 3;  // bonus row
+      }
+      s_exact = exact;
+      s_token = t2.i1;
+    }
+  }
+  __syncthreads();
+  int token = s_token;
+  if (s_exact) {
+    // Exact race over the whole row with torch's arithmetic (rare).
+    const int k = info.k;
+    const float* pr = a.target + ((size_t)b * C + k) * a.V;
+    const float* qr = k < a.gamma ? a.draft + ((size_t)b * a.gamma + k) * a.V : nullptr;
+    const float* e = cm.noise + (size_t)b * a.V;
+    const bool probs = a.is_probs;
+    const float t = s_t, psum = s_psum;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
+      const float p = exact_prob(pr[i], info.mp, info.sp, a.tf, probs);
+      float rhat;
+      if (s_exact == 3) {
+        rhat = p;
+      } else if (s_exact == 2) {
+        rhat = p / psum;
+      } else {
+        const float d = p - exact_prob(qr[i], info.mq, info.sq, a.tf, probs);
+        rhat = (d < 0.f ? 0.f : d) / t;
+      }
+      const float key = rhat / e[i];
+      if (better(key, i, bv, bi)) bv = key, bi = i;
+    }
+    block_argmax(bv, bi);
+    token = bi;
+  }
+  if (threadIdx.x != 0) return;
+  a.out_tokens[(size_t)b * C + info.k] = token;
+  commit_cut(a, cm, b, info.k, token, s_x, rem, st);
+}
+
+// ---------------------------------------------------------------- 2. race
+// Residual (or bonus) race of one chunk: p (and q) from the row statistics,
+// the residual (p - q)+ formed on the fly, keys r / E kept as their top two.
+// Keys use x * (1 / T) and a hardware reciprocal of E: they differ from the
+// exact keys by a few ulp, and best pairs closer than kTieRel are re-raced
+// exactly. All loads of the chunk are issued before the first is used (buffer
+// loads past the row end return zero and count as absent).
+template <bool RESID, bool UNIT, bool PROBS>
+__device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& info, int b, int c, Top2& t2,
+                                           float& rs, float& ps, const float* __restrict__ e) {
+  const int C = a.gamma + 1, V = a.V;
+  const float* pr = a.target + ((size_t)b * C + info.k) * V;
+  const float* qr = RESID ? a.draft + ((size_t)b * a.gamma + info.k) * V : pr;
+  const float rtf = 1.f / a.tf;
+  const float mp = info.mp * kLog2e, isp = 1.f / info.sp;
+  const float mq = info.mq * kLog2e, isq = RESID ? 1.f / info.sq : 0.f;
+  // p and q are each rounded before p - q is formed, as torch forms them as
+  // tensors first (a contracted fma would leave a residual of ~1 ulp where
+  // p == q).
+  auto prob = [&](float zv, float ml, float is) {
+    if (PROBS) return zv;
+    const float x = UNIT ? zv : zv * rtf;
+    float pv = __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -ml)) * is;
+    asm("" : "+v"(pv));  // opaque: the product is not fused into p - q
+    return pv;
+  };
+  // Branch-free visit in rising index order: a strictly larger key takes a
+  // place (an equal later key never wins), NaN keys are tracked apart (the
+  // first NaN wins, as torch.argmax), and entries past the row end
+  // (ok == false) add nothing and carry key -1, below every real key.
+  int nan_i = 0x7fffffff;
+  auto visit = [&](int i, bool ok, float zp, float zq, float ei) {
+    float p = prob(zp, mp, isp);
+    float r = p;
+    if (RESID) {
+      const float d = p - prob(zq, mq, isq);
+      r = d < 0.f ? 0.f : d;  // torch.clamp(p - q, min=0): NaN stays NaN
+    }
+    r = ok ? r : 0.f;
+    if (RESID) {
+      rs += r;
+      ps += ok ? p : 0.f;
+    }
+    const float key = ok ? r * __builtin_amdgcn_rcpf(ei) : -1.f;
+    const bool c1 = key > t2.v1, c2 = key > t2.v2;
+    t2.v2 = c1 ? t2.v1 : (c2 ? key : t2.v2);
+    t2.i2 = c1 ? t2.i1 : (c2 ? i : t2.i2);
+    t2.v1 = c1 ? key : t2.v1;
+    t2.i1 = c1 ? i : t2.i1;
+    nan_i = (key != key && nan_i == 0x7fffffff) ? i : nan_i;
+  };
+  if ((V & 3) == 0) {
+    const int n4 = V >> 2;
+    const uint32_t row_bytes = (uint32_t)V * 4u;
+    const __amdgpu_buffer_rsrc_t bp = span_rsrc(pr, row_bytes), bq = span_rsrc(qr, row_bytes),
+                                 be = span_rsrc(e, row_bytes);
+    u32x4_t zp[kVecPerThread], zq[kVecPerThread], ev[kVecPerThread];
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const uint32_t off = (uint32_t)vec_index(c, k) * 16u;
+      zp[k] = load_b128(bp, off);
+      if (RESID) zq[k] = load_b128(bq, off);
+      ev[k] = load_b128(be, off);
+    }
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i4 = vec_index(c, k);
+      const u32x4_t q4 = RESID ? zq[k] : zp[k];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        visit(4 * i4 + t, i4 < n4, __uint_as_float(zp[k][t]), __uint_as_float(q4[t]), __uint_as_float(ev[k][t]));
+    }
+  } else {
+    const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
+    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) visit(i, true, pr[i], RESID ? qr[i] : 0.f, e[i]);
+  }
+  if (nan_i != 0x7fffffff) {  // a NaN key leads the thread's list
+    t2.v2 = t2.v1;
+    t2.i2 = t2.i1;
+    t2.v1 = __uint_as_float(0x7fc00000u);
+    t2.i1 = nan_i;
+  }
+}
+
+// grid (chunks, B). The last workgroup of a sequence to finish makes its draw
+// and commit.
+template <bool UNIT, bool PROBS>
+__global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs cm, SampleWs ws) {
+  const int c = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
+  const RaceInfo info = ws.info[b];
+  const float* e = cm.noise + (size_t)b * a.V;
+  Top2 t2;
+  t2.init();
+  float rs = 0.f, ps = 0.f;
+  if (info.mode == RACE_RESIDUAL) race_chunk<true, UNIT, PROBS>(a, info, b, c, t2, rs, ps, e);
+  else if (info.mode == RACE_BONUS) race_chunk<false, UNIT, PROBS>(a, info, b, c, t2, rs, ps, e);
+  t2.wave_reduce();
+  __shared__ float s_v1[kWaves], s_v2[kWaves];
+  __shared__ int s_i1[kWaves], s_i2[kWaves];
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_v1[w] = t2.v1;
+    s_v2[w] = t2.v2;
+    s_i1[w] = t2.i1;
+    s_i2[w] = t2.i2;
+  }
+  const double rsum = block_sum_f64((double)rs);
+  const double psum = block_sum_f64((double)ps);
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kWaves; ++k) t2.merge(s_v1[k], s_i1[k], s_v2[k], s_i2[k]);
+    const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(ws.race);
+    const size_t o = ((size_t)b * nch + c) * sizeof(RacePart);
+    store_coherent_b128(rp, o, u32x4_t{__float_as_uint(t2.v1), __float_as_uint(t2.v2), (unsigned)t2.i1,
+                                       (unsigned)t2.i2});
+    store_coherent_b128(rp, o + 16, u32x4_t{(unsigned)__double2loint(rsum), (unsigned)__double2hiint(rsum),
+                                            (unsigned)__double2loint(psum), (unsigned)__double2hiint(psum)});
+  }
+  __shared__ int s_last;
+  if (arrive_last(ws.cnt_race + b, nch, &s_last)) finalize_seq(a, cm, ws, b, info);
 }
 
 // ------------------------------------------------------- single-row helpers
@@ -778,7 +859,8 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
   ws_layout(B, gamma, V, &ws, workspace);
   hipStream_t s = (hipStream_t)stream;
   const int nch = num_chunks(V);
-  if ((size_t)B * (2 * gamma + 1) > 65535) return SPV_ERR_ARG;
+  // Race partials and rows are addressed with 32-bit buffer offsets.
+  if ((size_t)B * nch * sizeof(RacePart) > 0x7fffffffu || (size_t)V * 4 > 0xffffffffu) return SPV_ERR_ARG;
   DecideArgs a{};
   a.target = target;
   a.draft = draft;
@@ -795,24 +877,31 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
   a.decide_only = decide_only ? 1 : 0;
   a.tf = temperature_divisor(temperature);
 
-  if (!is_probs) {
-    const dim3 grid(nch, B * (2 * gamma + 1));
-    if (greedy)
-      hipLaunchKernelGGL(row_stats_kernel<true>, grid, dim3(kThreads), 0, s, target, draft, B, gamma, V, a.tf, ws);
-    else
-      hipLaunchKernelGGL(row_stats_kernel<false>, grid, dim3(kThreads), 0, s, target, draft, B, gamma, V, a.tf,
-                         ws);
-    SPV_CHECK_LAUNCH();
-  }
-  hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kThreads), 0, s, a, ws);
-  SPV_CHECK_LAUNCH();
-  if (decide_only) return SPV_OK;
-  if (!greedy) {
-    hipLaunchKernelGGL(race_kernel, dim3(nch, B), dim3(kThreads), 0, s, a, exp_noise, ws);
-    SPV_CHECK_LAUNCH();
-  }
   CommitArgs cm{start_pos, remaining, exp_noise, eos_id, n_commit, finished, new_len};
-  hipLaunchKernelGGL(finalize_kernel, dim3(B), dim3(kThreads), 0, s, a, cm, ws);
+  // Logits: row statistics, whose last workgroup per sequence decides (and, in
+  // greedy mode, commits). Probabilities: the decision alone. Then, unless
+  // greedy or decide-only, the race, whose last workgroup per sequence commits.
+  const bool unit = a.tf == 1.0f;
+  if (!is_probs) {
+    const dim3 grid(B * (2 * gamma + 1));
+    if (greedy)
+      hipLaunchKernelGGL((row_stats_kernel<IN_GREEDY, true>), grid, dim3(kThreads), 0, s, a, cm, ws);
+    else if (unit)
+      hipLaunchKernelGGL((row_stats_kernel<IN_LOGITS, true>), grid, dim3(kThreads), 0, s, a, cm, ws);
+    else
+      hipLaunchKernelGGL((row_stats_kernel<IN_LOGITS, false>), grid, dim3(kThreads), 0, s, a, cm, ws);
+  } else {
+    hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kThreads), 0, s, a, cm, ws);
+  }
+  SPV_CHECK_LAUNCH();
+  if (decide_only || greedy) return SPV_OK;
+  const dim3 rgrid(nch, B);
+  if (is_probs)
+    hipLaunchKernelGGL((race_kernel<true, true>), rgrid, dim3(kThreads), 0, s, a, cm, ws);
+  else if (unit)
+    hipLaunchKernelGGL((race_kernel<true, false>), rgrid, dim3(kThreads), 0, s, a, cm, ws);
+  else
+    hipLaunchKernelGGL((race_kernel<false, false>), rgrid, dim3(kThreads), 0, s, a, cm, ws);
   SPV_CHECK_LAUNCH();
   return SPV_OK;
 }

@@ -128,8 +128,9 @@ def i32(values, device: torch.device) -> torch.Tensor:
 class Workspace:
     """Grow-only device scratch buffer owned by the caller of the library.
 
-    Allocated zero-filled: the attention entry point keeps arrival counters at
-    its head that must start at zero (and are zero again after every call)."""
+    Allocated zero-filled: the attention and sampling entry points keep arrival
+    counters at its head that must start at zero (and are zero again after
+    every call)."""
 
     def __init__(self) -> None:
         self._buf: Optional[torch.Tensor] = None

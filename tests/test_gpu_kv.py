@@ -353,3 +353,40 @@ def test_rewind_device_inputs_refresh_mirrors(cuda):
     cpu.truncate(1, 5)
     cpu.clear(1)
     _same_state(gpu, cpu)
+
+
+@pytest.mark.parametrize("dtype,chunk", [(torch.bfloat16, 6), (torch.bfloat16, 20), (torch.float32, 7)])
+def test_append_into_filled_pool_touches_only_the_chunk(cuda, dtype, chunk):
+    """Block 16, d 128: V rows are rebuilt whole (old keys read back); every
+    pool element outside the appended positions must be left as it was."""
+    B, cap, bs, H, d = 12, 256, 16, 2, 128
+    g = torch.Generator().manual_seed(11)
+    lens = torch.randint(0, 70, (B,), generator=g).tolist()
+    perm = torch.randperm(cap, generator=g).tolist()
+    tables, pos = [], 0
+    for L in lens:
+        n = -(-L // bs)
+        tables.append(perm[pos: pos + n])
+        pos += n
+    gpu = PagedKVCache(2, H, d, cap, bs, cuda, dtype, max_seqs=B)
+    gpu.load_state(tables, lens, perm[pos:])
+    cpu = ref.PagedKVCache(2, H, d, cap, bs, store=False)
+    cpu.load_state(tables, lens, perm[pos:])
+    # Every element of both layers holds a distinct-looking value beforehand.
+    gpu.k_pool.copy_(torch.randn(gpu.k_pool.shape, generator=g).to(dtype))
+    gpu.v_pool.copy_(torch.randn(gpu.v_pool.shape, generator=g).to(dtype))
+    k0, v0 = gpu.k_pool.cpu().clone(), gpu.v_pool.cpu().clone()
+    kn = torch.randn(B, chunk, H, d, generator=g).to(dtype)
+    vn = torch.randn(B, chunk, H, d, generator=g).to(dtype)
+    gpu.write_block(1, list(range(B)), lens, kn.to(cuda), vn.to(cuda))
+    cpu.write_block(1, list(range(B)), lens, None, None, chunk=chunk)
+    _same_state(gpu, cpu)
+    # Expected pools: the initial contents with the chunk placed (V transposed per block).
+    for b, L in enumerate(lens):
+        for j in range(chunk):
+            p = L + j
+            blk = cpu.block_tables[b][p // bs]
+            k0[1, blk, :, p % bs, :] = kn[b, j]
+            v0[1, blk, :, :, p % bs] = vn[b, j]
+    assert torch.equal(gpu.k_pool.cpu(), k0)
+    assert torch.equal(gpu.v_pool.cpu(), v0)

@@ -167,3 +167,36 @@ def test_commit_cut_matches_oracle(cuda, eos):
         assert n_commit[b] == k
         assert fin[b] == int(eos_hit or k == 0 or k >= int(remaining[b]))
         assert new_len[b] == (int(start[b]) + k if k > 0 else -1)
+
+
+SAMPLE_COUNTER_BYTES = 1 << 19  # SPV_SAMPLE_COUNTER_BYTES
+
+
+@pytest.mark.parametrize("T", [1.0, 0.0])
+def test_repeated_calls_are_identical_and_leave_counters_zero(cuda, T):
+    g, target, draft, u, noise = _workload(21, B=16, gamma=5, V=20000)
+    x = _proposals(draft, T, g)
+    want = S.verify_from_logits(target, draft, x, u, noise, T)
+    args = (target.to(cuda), draft.to(cuda), x.to(cuda), u.to(cuda), noise.to(cuda) if T > 0 else None, T)
+    outs = []
+    for _ in range(3):
+        res = es.verify_sample(*args)
+        assert res.accepted_lists() == want
+        outs.append((res.accept_len.clone(), res.out_tokens.clone()))
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(es._workspace._buf[:SAMPLE_COUNTER_BYTES])) == 0
+    for a, o in outs[1:]:
+        assert torch.equal(a, outs[0][0]) and torch.equal(o, outs[0][1])
+
+
+def test_workspace_reused_across_batch_sizes(cuda):
+    # One workspace serves calls of growing and shrinking B; the counters sit
+    # at fixed offsets, so no call reads another call's partials as counters.
+    es._workspace.get(4 << 20, cuda)
+    for i, B in enumerate([4, 24, 8, 40]):
+        # odd vocabularies take the element-wise paths
+        g, target, draft, u, noise = _workload(30 + i, B=B, gamma=4, V=12000 + i % 2)
+        x = _proposals(draft, 1.0, g)
+        want = S.verify_from_logits(target, draft, x, u, noise, 1.0)
+        res = es.verify_sample(target.to(cuda), draft.to(cuda), x.to(cuda), u.to(cuda), noise.to(cuda), 1.0)
+        assert res.accepted_lists() == want, B
