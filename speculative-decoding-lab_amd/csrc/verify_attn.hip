@@ -238,7 +238,7 @@ constexpr int kMfmaThreads = 512;
 // O^T tiles combined per LDS round: as many as fit beside the other buffers
 // (the slots take 8 waves x 16 * nt rows x 64 B per tile).
 __host__ __device__ constexpr int combine_tiles(int nt, int mt) {
-  return (nt == 1 ? 4 : nt <= 3 ? 2 : 1) < mt ? (nt == 1 ? 4 : nt <= 3 ? 2 : 1) : mt;
+  return (nt == 1 ? 8 : nt <= 3 ? 4 : 2) < mt ? (nt == 1 ? 8 : nt <= 3 ? 4 : 2) : mt;
 }
 constexpr int kTabChunk = 512;    // block ids staged in LDS per window
 constexpr int kMergeChunk = 4;    // partial slots the merging workgroup loads at once
@@ -283,15 +283,43 @@ __device__ __forceinline__ int seq_of(const int* pref, int B, long long hr_count
   return lo;
 }
 
-// Wave-wide inclusive sum of v (64 lanes).
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
-  return v;
+// Wave-wide inclusive sum / maximum (x >= 0) of one int per lane through DPP
+// row shifts and row broadcasts: lane l gets the result over lanes 0..l, with
+// no LDS round trip.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+__device__ __forceinline__ int wave_incl_max(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false));
+  return x;
+}
+__device__ __forceinline__ int lane63(int x) { return __builtin_amdgcn_readlane(x, 63); }
+
+// floor(a / b) for 0 <= a < 2^53, b >= 1: the correctly rounded double
+// quotient truncates to the exact one (64-bit integer division would expand
+// to a long instruction sequence).
+__device__ __forceinline__ long long div_floor(long long a, long long b) {
+  return (long long)((double)a / (double)b);
+}
+
+// ceil(a / P) for a >= 0, P >= 1: a reciprocal estimate corrected to the
+// exact quotient.
+__device__ __forceinline__ int ceil_div(int a, int P, float rP) {
+  int q = (int)((float)a * rP);
+  while (q > 0 && q * P > a) --q;
+  while ((q + 1) * P <= a) ++q;
+  return q + (q * P < a ? 1 : 0);
 }
 
 // Pieces: every segment of np pages (one per (sequence b, kv head, row group))
@@ -301,51 +329,57 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 // P starts at ceil(total / nw) and grows in proportion to the overshoot;
 // when the segments alone outnumber the workgroups, P is the longest context
 // and every piece is a whole segment. Wave 0 computes the whole plan with
-// wave-wide scans (no barrier until the end):
+// wave-wide scans (no barrier until the end), and keeps each sequence's id
+// and start position in LDS for the piece set-up:
 //   s_pref[b]  = pages of the sequences before b (per segment), s_pref[B] = total;
-//   s_kpref[b] = pieces of one segment of each sequence before b, s_kpref[B] = total.
-__device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, long long HR, int nw) {
+//   s_kpref[b] = pieces of one segment of each sequence before b, s_kpref[B] = total;
+//   s_sid[b], s_start[b] = seq_ids[b], start_pos[b].
+template <int BS>
+__device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, int* s_sid, int* s_start, long long HR,
+                           int nw) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const bool one = p.B <= 64;  // the common case keeps every count in a register
     int np1 = 0, carry = 0, maxnp = 0;
     for (int base = 0; base < p.B; base += 64) {
       const int b = base + lane;
-      const int np = b < p.B ? context_pages(p, p.start[b] + p.C) : 0;
-      const int incl = wave_incl_scan(np);
+      int np = 0;
+      if (b < p.B) {
+        const int st = p.start[b];
+        s_start[b] = st;
+        s_sid[b] = p.seq_ids[b];
+        np = min((st + p.C + BS - 1) / BS, p.max_pages);
+      }
+      const int incl = wave_incl_sum(np);
       if (b < p.B) s_pref[b] = carry + incl - np;
-      carry += __shfl(incl, 63, 64);
-      int mx = np;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
-      maxnp = max(maxnp, mx);
+      carry += lane63(incl);
+      maxnp = max(maxnp, lane63(wave_incl_max(np)));
       np1 = np;
     }
     if (lane == 0) s_pref[p.B] = carry;
     auto pages_of = [&](int b) { return one ? np1 : s_pref[b + 1] - s_pref[b]; };
     const long long T = HR * carry;
-    int P = HR * p.B >= nw ? maxnp : (int)min((long long)maxnp, max(1LL, (T + nw - 1) / nw));
+    int P = HR * p.B >= nw ? maxnp : (int)min((long long)maxnp, max(1LL, div_floor(T + nw - 1, nw)));
     int npieces;
     for (;;) {
+      const float rP = __builtin_amdgcn_rcpf((float)P);
       npieces = 0;
       for (int base = 0; base < p.B; base += 64) {
         const int b = base + lane;
-        int k = b < p.B ? (pages_of(b) + P - 1) / P : 0;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
-        npieces += k;
+        npieces += lane63(wave_incl_sum(b < p.B ? ceil_div(pages_of(b), P, rP) : 0));
       }
       const long long n = HR * npieces;
       if (n <= nw || P >= maxnp) break;  // P = maxnp gives n = HR * B <= nw here
-      P = (int)min((long long)maxnp, max((long long)P + 1, (P * n + nw - 1) / nw));
+      P = (int)min((long long)maxnp, max((long long)P + 1, div_floor(P * n + nw - 1, nw)));
     }
+    const float rP = __builtin_amdgcn_rcpf((float)P);
     carry = 0;
     for (int base = 0; base < p.B; base += 64) {
       const int b = base + lane;
-      const int k = b < p.B ? (pages_of(b) + P - 1) / P : 0;
-      const int incl = wave_incl_scan(k);
+      const int k = b < p.B ? ceil_div(pages_of(b), P, rP) : 0;
+      const int incl = wave_incl_sum(k);
       if (b < p.B) s_kpref[b] = carry + incl - k;
-      carry += __shfl(incl, 63, 64);
+      carry += lane63(incl);
     }
     if (lane == 0) s_kpref[p.B] = carry;
   }
@@ -461,11 +495,13 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   const int nw = gridDim.x;
   const int wg = share_of_block(blockIdx.x, nw);
   int* s_kpref = s_pref + p.B + 1;
+  int* s_sid = s_kpref + p.B + 1;
+  int* s_start = s_sid + p.B + 1;
   const long long HR = (long long)p.Hkv * p.nrg;
-  build_plan(p, s_pref, s_kpref, HR, nw);
+  build_plan<BS>(p, s_pref, s_kpref, s_sid, s_start, HR, nw);
   if (s_pref[p.B] == 0) return;
   const long long N = HR * s_kpref[p.B];  // pieces in the batch
-  const long long x_begin = (long long)wg * N / nw, x_end = (long long)(wg + 1) * N / nw;
+  const long long x_begin = div_floor((long long)wg * N, nw), x_end = div_floor((long long)(wg + 1) * N, nw);
   const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
   const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
   const uint16_t* qbase = static_cast<const uint16_t*>(p.q);
@@ -477,15 +513,15 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     const int rem = (int)(x - HR * s_kpref[b]);
     const int hr = rem / kb, piece = rem - hr * kb;
     const int np = uni(s_pref[b + 1] - s_pref[b]);
-    const int lp0 = (int)((long long)piece * np / kb), lp1 = (int)((long long)(piece + 1) * np / kb);
+    const int lp0 = (int)div_floor((long long)piece * np, kb), lp1 = (int)div_floor((long long)(piece + 1) * np, kb);
     const int h = hr / p.nrg, rg = hr - h * p.nrg;
     const int seg = b * (int)HR + hr;
     const int x0 = (int)(x - piece);  // the segment's first piece
-    const int start = uni(p.start[b]);
+    const int start = uni(s_start[b]);
     const int L = start + p.C;
     const int qr0 = rg * RPG;
     const int nr = min(RPG, p.G - qr0);
-    const int32_t* table = p.tables + (size_t)uni(p.seq_ids[b]) * p.maxb;
+    const int32_t* table = p.tables + (size_t)uni(s_sid[b]) * p.maxb;
 
     int jrow[NT];  // chunk row j of query column 16 nt + i16 (rows past nr repeat the last)
 #pragma unroll
@@ -670,41 +706,56 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // partial -- directly.
     const bool final_out = kb == 1;
     const int slot = (int)x;
-    // Combining thread: tile of the round (slowest, so a wave reads 16
-    // consecutive rows of one tile: conflict-free), row, dims 4 * cd4 .. + 3.
-    // The thread index is made opaque here so that the combine's addresses are
-    // computed now, not hoisted over the page walk (where they would spill).
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    const int ct = tid / (4 * RPG), crow = (tid >> 2) % RPG, cd4 = tid & 3;
-    const bool combiner = ct < TPR && crow < nr;
-    float cfac[NWV], cinv = 0.f, cM = 0.f, cL = 0.f;
-    if (combiner) {
-      cM = sm_m[0][crow];
+    // Row factors: thread r < nr turns its row's wave maxima into the factors
+    // 2^(m_w - M) in place (sm_m[w][r]) and the row's 1 / L into sm_l[0][r],
+    // and writes the row's (M, L) partial; the first round's barrier publishes
+    // them to the combiners.
+    if ((int)threadIdx.x < nr) {
+      const int r = threadIdx.x;
+      float cM = sm_m[0][r];
 #pragma unroll
-      for (int ww = 1; ww < NWV; ++ww) cM = fmaxf(cM, sm_m[ww][crow]);
+      for (int ww = 1; ww < NWV; ++ww) cM = fmaxf(cM, sm_m[ww][r]);
+      float cL = 0.f;
 #pragma unroll
       for (int ww = 0; ww < NWV; ++ww) {
-        const float mw = sm_m[ww][crow];
-        cfac[ww] = mw == -INFINITY ? 0.f : exp2f(mw - cM);
-        cL += sm_l[ww][crow] * cfac[ww];
+        const float mw = sm_m[ww][r];
+        const float f = mw == -INFINITY ? 0.f : exp2f(mw - cM);
+        sm_m[ww][r] = f;
+        cL += sm_l[ww][r] * f;
       }
-      cinv = 1.f / cL;
+      sm_l[0][r] = 1.f / cL;
+      if (!final_out) store2_coherent(coherent_rsrc(p.part_ml), ((size_t)slot * p.G + qr0 + r) * 2 * sizeof(float), cM, cL);
     }
-    const int cr = qr0 + crow;
-    const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml), ro = coherent_rsrc(p.part_o);
-    // Element offset of the thread's row in the output or in the partial slot
-    // (32-bit: both tensors are far below 2^31 elements here).
-    uint32_t cbase;
-    if (final_out) {
-      const int j = cr / p.ratio, hq = h * p.ratio + (cr - j * p.ratio);
-      cbase = (uint32_t)(((b * p.C + j) * p.Hq + hq) * D);
-    } else {
-      cbase = (uint32_t)((slot * p.G + cr) * D);
-      if (combiner && ct == 0 && cd4 == 0) store2_coherent(rml, ((size_t)slot * p.G + cr) * 2 * sizeof(float), cM, cL);
+    // Combining items: (tile of the round, row, dims 4 * cd4 .. + 3), the tile
+    // slowest so that a wave reads 16 consecutive rows of one tile (conflict
+    // free); a thread takes items tid and tid + kMfmaThreads. The thread index
+    // is made opaque here so that the combine's addresses are computed now,
+    // not hoisted over the page walk (where they would spill).
+    constexpr int kCItems = (TPR * RPG * 4 + kMfmaThreads - 1) / kMfmaThreads;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    int ct[kCItems], crow[kCItems], cd4[kCItems];
+    bool combiner[kCItems];
+    uint32_t cbase[kCItems];
+    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(p.part_o);
+#pragma unroll
+    for (int ci = 0; ci < kCItems; ++ci) {
+      const int idx = tid + ci * kMfmaThreads;
+      ct[ci] = idx / (4 * RPG);
+      crow[ci] = (idx >> 2) % RPG;
+      cd4[ci] = idx & 3;
+      combiner[ci] = ct[ci] < TPR && crow[ci] < nr;
+      const int cr = qr0 + crow[ci];
+      // Element offset of the item's row in the output or in the partial slot
+      // (32-bit: both tensors are far below 2^31 elements here).
+      if (final_out) {
+        const int j = cr / p.ratio, hq = h * p.ratio + (cr - j * p.ratio);
+        cbase[ci] = (uint32_t)(((b * p.C + j) * p.Hq + hq) * D);
+      } else {
+        cbase[ci] = (uint32_t)((slot * p.G + cr) * D);
+      }
     }
     static_assert(MT % TPR == 0, "tiles per round must divide the tile count");
-    static_assert(4 * RPG * TPR <= kMfmaThreads, "one combining thread per (tile, row, 4 dims)");
 #pragma unroll
     for (int mt0 = 0; mt0 < MT; mt0 += TPR) {
       if (mt0 > 0) __syncthreads();  // the previous round's readers are done
@@ -715,25 +766,28 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
           if (16 * nt + i16 < nr)  // rows past nr are padding
             *reinterpret_cast<f32x4_t*>(&sm_x[(((w * TPR) + t) * RPG + 16 * nt + i16) * 16 + 4 * g]) = o[mt0 + t][nt];
       __syncthreads();
-      if (combiner) {
+#pragma unroll
+      for (int ci = 0; ci < kCItems; ++ci) {
+        if (!combiner[ci]) continue;
         f32x4_t v[NWV];
 #pragma unroll
         for (int ww = 0; ww < NWV; ++ww)
-          v[ww] = *reinterpret_cast<const f32x4_t*>(&sm_x[(((ww * TPR) + ct) * RPG + crow) * 16 + 4 * cd4]);
+          v[ww] = *reinterpret_cast<const f32x4_t*>(&sm_x[(((ww * TPR) + ct[ci]) * RPG + crow[ci]) * 16 + 4 * cd4[ci]]);
         f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ww = 0; ww < NWV; ++ww) acc += v[ww] * cfac[ww];
-        const int e0 = 16 * (mt0 + ct) + 4 * cd4;
+        for (int ww = 0; ww < NWV; ++ww) acc += v[ww] * sm_m[ww][crow[ci]];
+        const int e0 = 16 * (mt0 + ct[ci]) + 4 * cd4[ci];
         if (final_out) {
+          const float cinv = sm_l[0][crow[ci]];
           if constexpr (QT == SPV_BF16) {
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + cbase + e0) =
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + cbase[ci] + e0) =
                 make_uint2(pack2_bf16(acc[0] * cinv, acc[1] * cinv), pack2_bf16(acc[2] * cinv, acc[3] * cinv));
           } else {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) store_out<QT>(p, cbase + e0 + k, acc[k] * cinv);
+            for (int k = 0; k < 4; ++k) store_out<QT>(p, cbase[ci] + e0 + k, acc[k] * cinv);
           }
         } else {
-          store4_coherent(ro, (size_t)(cbase + e0) * sizeof(float), acc);
+          store4_coherent(ro, (size_t)(cbase[ci] + e0) * sizeof(float), acc);
         }
       }
     }
@@ -869,7 +923,7 @@ int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s) {
 
 template <int D>
 void launch_mfma(const AttnParams& p, int nt, hipStream_t s) {
-  const size_t smem = (size_t)2 * (p.B + 1) * sizeof(int);  // page and piece prefixes
+  const size_t smem = (size_t)4 * (p.B + 1) * sizeof(int);  // page / piece prefixes, ids, starts
   const dim3 grid(persistent_wgs()), blk(kMfmaThreads);
   switch (nt) {
     case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16>), grid, blk, smem, s, p); break;
