@@ -56,37 +56,46 @@ __global__ void free_one_kernel(int32_t* __restrict__ free_stack, int32_t* __res
 // Lazy allocation for one extend block (kv.py:119-122 applied to every write of
 // model.py:184-187). Sequence b needs blocks up to (start_b + C - 1) / bs; the
 // missing ones are popped from the stack top, sequence by sequence in batch
-// order and in logical order within a sequence.
+// order and in logical order within a sequence. Two dependent round trips:
+// the stack height and the entries' ids and starts, then their block counts
+// and the stack's top entries (as many as this call can pop, staged in LDS).
+constexpr int kAllocStage = 4096;
+
 __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
     int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
     const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
     const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, int32_t B, int32_t C,
     int32_t bs) {
   __shared__ int s_scan[kPoolThreads / 64];
-  __shared__ int s_top, s_fail;
-  if (threadIdx.x == 0) {
-    s_top = ctr[CTR_TOP];
-    s_fail = B;
-  }
+  __shared__ int s_fail;
+  __shared__ int s_free[kAllocStage];  // s_free[i] = free_stack[top - 1 - i]
+  const int top = ctr[CTR_TOP];
+  // The first chunk of entries (one chunk for B <= blockDim.x), clamped loads.
+  const int bc = min((int)threadIdx.x, B - 1);
+  int sid = seq_ids[bc], st = start[bc];
+  int nb = nblocks[sid];
+  const int maxneed = (int)min((long long)B * ((C + bs - 1) / bs + 1), (long long)kAllocStage);
+  const int nstage = min(top, maxneed);
+  for (int i = threadIdx.x; i < nstage; i += blockDim.x) s_free[i] = free_stack[top - 1 - i];
+  if (threadIdx.x == 0) s_fail = B;
   __syncthreads();
-  const int top = s_top;
   int consumed = 0;
   for (int base = 0; base < B; base += blockDim.x) {
     const int b = base + threadIdx.x;
-    int need = 0, sid = 0, nb = 0;
-    if (b < B) {
+    if (base > 0 && b < B) {
       sid = seq_ids[b];
+      st = start[b];
       nb = nblocks[sid];
-      const int last_blk = (start[b] + C - 1) / bs;
-      need = max(0, last_blk + 1 - nb);
     }
+    const int need = b < B ? max(0, (st + C - 1) / bs + 1 - nb) : 0;
     int total;
     const int off = block_exclusive_scan(need, s_scan, &total);
     const int avail = top - consumed;
     const int got = min(need, max(0, avail - off));
     if (b < B && got < need) atomicMin(&s_fail, b);
     for (int i = 0; i < got; ++i) {
-      const int id = free_stack[top - 1 - (consumed + off + i)];
+      const int pos = consumed + off + i;
+      const int id = pos < nstage ? s_free[pos] : free_stack[top - 1 - pos];
       tables[(size_t)sid * maxb + nb + i] = id;
       free_flag[id] = 0;
     }
@@ -102,15 +111,16 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
 
 // The K/V copy of an append: one workgroup per (batch entry b, kv head h,
 // block touched by the chunk) copies the chunk's tokens that fall in that block.
-//  * K rows of consecutive positions in one block are contiguous, so K moves in
-//    16-byte pieces.
-//  * The V page is transposed (element (h, e, o) at ((h * d) + e) * bs + o), so
-//    one dimension's keys of one block form a row of bs elements. Each
-//    dimension's row is written whole: the old row is read when the chunk
-//    covers it only in part, the new keys are placed, and the full row is
-//    stored. Element-sized stores at the row stride would leave partial memory
-//    bursts, which the memory controller completes by read-modify-write.
+// Two dependent round trips: the entry's sequence id and start, then its block
+// count, the block's id and the chunk's new keys and values, all issued before
+// any is used (tokens an exhausted pool cut off are loaded but not stored).
+//  * K rows of consecutive positions in one block are contiguous: 16-byte pieces.
+//  * The V page is transposed (element (h, e, o) at ((h * d) + e) * bs + o): a
+//    block's new keys of one dimension are consecutive elements of that
+//    dimension's row. All stores to a block come from one workgroup, so the
+//    L2 merges them into whole lines before they reach memory.
 constexpr int kWriteThreads = 256;
+constexpr int kWriteItems = 4;  // loads per thread issued together
 
 template <int ES>
 struct Elem;
@@ -136,70 +146,105 @@ __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(
     int32_t C, int32_t layer, int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t limit_b) {
   using T = typename Elem<ES>::T;
   const int b = blockIdx.x / hkv, h = blockIdx.x - b * hkv;
-  // limit_b < 0: the allocation of this call recorded the failing sequence in ctr.
+  const int sid = seq_ids[b];
+  const int s0 = start[b];
+  const int ex = limit_b < 0 ? ctr[CTR_EXHAUSTED] : 0;
+  const int blk = max(s0, 0) / bs + (int)blockIdx.y;
+  const int nb = nblocks[sid];
+  const int phys = tables[(size_t)sid * maxb + min(blk, maxb - 1)];
+  // The chunk's keys in this block occupy row offsets [lo, hi_c); offset o is
+  // chunk token o + jbase (before the cut of an exhausted pool).
+  const int lo = max(s0, blk * bs) - blk * bs;
+  const int hi_c = min(s0 + C, (blk + 1) * bs) - blk * bs;
+  const int jbase = blk * bs - s0;
+  const size_t row_elems = (size_t)hkv * d;  // elements of one token's K (or V) over all heads
+  auto token = [&](int o) { return min(max(jbase + o, 0), C - 1); };
+  const int vec = (d * ES) >> 4;  // 16-byte pieces of one K row (d * ES % 16 == 0 on this path)
+  const int nk = hi_c > lo ? (hi_c - lo) * vec : 0;
+  const int nv = hi_c > lo ? (hi_c - lo) * d : 0;
+  uint4 kreg[kWriteItems];
+  T vreg[kWriteItems];
+#pragma unroll
+  for (int k = 0; k < kWriteItems; ++k) {
+    const int ik = min((int)threadIdx.x + k * kWriteThreads, max(nk - 1, 0));
+    const int ok_ = lo + ik / vec, c = ik % vec;
+    kreg[k] = reinterpret_cast<const uint4*>(knew + (((size_t)b * C + token(ok_)) * row_elems + (size_t)h * d) * ES)[c];
+    const int iv = min((int)threadIdx.x + k * kWriteThreads, max(nv - 1, 0));
+    const int ov = lo + iv / d, e = iv % d;
+    vreg[k] = reinterpret_cast<const T*>(vnew)[((size_t)b * C + token(ov)) * row_elems + (size_t)h * d + e];
+  }
+  if (limit_b < 0) limit_b = ex ? ex - 1 : 0x7fffffff;
+  if (b > limit_b || s0 < 0) return;
+  const int n = min(C, nb * bs - s0);
+  if (n <= 0) return;
+  if (h == 0 && blockIdx.y == 0 && threadIdx.x == 0 && seq_lens[sid] < s0 + n) seq_lens[sid] = s0 + n;
+  if (blk > (s0 + n - 1) / bs || (unsigned)phys >= (unsigned)cap) return;  // never write outside the pool
+  const int hi = min(s0 + n, (blk + 1) * bs) - blk * bs;
+  const size_t slot = (((size_t)layer * cap + phys) * hkv + h);  // the (block, head) page
+  uint8_t* kdst = kpool + slot * bs * (size_t)(d * ES);
+  T* vdst = reinterpret_cast<T*>(vpool) + slot * (size_t)d * bs;
+  for (int base = 0; base < max(nk, nv); base += kWriteItems * kWriteThreads) {
+    if (base > 0) {  // chunks longer than one round (large blocks or head dims)
+#pragma unroll
+      for (int k = 0; k < kWriteItems; ++k) {
+        const int ik = min(base + (int)threadIdx.x + k * kWriteThreads, max(nk - 1, 0));
+        const int ok_ = lo + ik / vec, c = ik % vec;
+        kreg[k] = reinterpret_cast<const uint4*>(knew + (((size_t)b * C + token(ok_)) * row_elems + (size_t)h * d) * ES)[c];
+        const int iv = min(base + (int)threadIdx.x + k * kWriteThreads, max(nv - 1, 0));
+        const int ov = lo + iv / d, e = iv % d;
+        vreg[k] = reinterpret_cast<const T*>(vnew)[((size_t)b * C + token(ov)) * row_elems + (size_t)h * d + e];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kWriteItems; ++k) {
+      const int ik = base + (int)threadIdx.x + k * kWriteThreads;
+      if (ik < nk && lo + ik / vec < hi)
+        reinterpret_cast<uint4*>(kdst + (size_t)(lo + ik / vec) * (d * ES))[ik % vec] = kreg[k];
+      const int iv = base + (int)threadIdx.x + k * kWriteThreads;
+      if (iv < nv && lo + iv / d < hi) vdst[(size_t)(iv % d) * bs + lo + iv / d] = vreg[k];
+    }
+  }
+}
+
+// K rows whose byte length is not a multiple of 16: element-wise copy (rare
+// head dims), same round-trip structure.
+template <int ES>
+__global__ __launch_bounds__(kWriteThreads) void kv_write_small_kernel(
+    uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool, const uint8_t* __restrict__ knew,
+    const uint8_t* __restrict__ vnew, const int32_t* __restrict__ tables, int32_t maxb,
+    const int32_t* __restrict__ nblocks, int32_t* __restrict__ seq_lens,
+    const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, const int32_t* __restrict__ ctr,
+    int32_t C, int32_t layer, int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t limit_b) {
+  using T = typename Elem<ES>::T;
+  const int b = blockIdx.x / hkv, h = blockIdx.x - b * hkv;
+  const int sid = seq_ids[b];
+  const int s0 = start[b];
   if (limit_b < 0) {
     const int ex = ctr[CTR_EXHAUSTED];
     limit_b = ex ? ex - 1 : 0x7fffffff;
   }
-  if (b > limit_b) return;
-  const int sid = seq_ids[b];
-  const int s0 = start[b];
-  // Positions s0 .. s0 + n - 1 have blocks; n < C only for the failing sequence
-  // of an exhausted pool.
+  if (b > limit_b || s0 < 0) return;
   const int n = min(C, nblocks[sid] * bs - s0);
-  if (n <= 0 || s0 < 0) return;
-  // The chunk extends the sequence's length to s0 + n.
+  if (n <= 0) return;
   if (h == 0 && blockIdx.y == 0 && threadIdx.x == 0 && seq_lens[sid] < s0 + n) seq_lens[sid] = s0 + n;
   const int blk = s0 / bs + (int)blockIdx.y;
   if (blk > (s0 + n - 1) / bs) return;
   const int phys = tables[(size_t)sid * maxb + blk];
-  if ((unsigned)phys >= (unsigned)cap) return;  // never write outside the pool
-  // New keys of this block occupy row offsets [lo, hi); offset o holds chunk token o + jbase.
+  if ((unsigned)phys >= (unsigned)cap) return;
   const int lo = max(s0, blk * bs) - blk * bs;
   const int hi = min(s0 + n, (blk + 1) * bs) - blk * bs;
   const int jbase = blk * bs - s0;
-  const size_t row_elems = (size_t)hkv * d;  // elements of one token's K (or V) over all heads
-  const size_t slot = (((size_t)layer * cap + phys) * hkv + h);  // the (block, head) page
-
-  const int kbytes = d * ES;
-  if ((kbytes & 15) == 0) {
-    const int vec = kbytes >> 4;
-    for (int t = threadIdx.x; t < (hi - lo) * vec; t += blockDim.x) {
-      const int o = lo + t / vec, c = t % vec;
-      uint8_t* dst = kpool + (slot * bs + o) * (size_t)kbytes;
-      const uint8_t* src = knew + (((size_t)b * C + jbase + o) * row_elems + (size_t)h * d) * ES;
-      reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(src)[c];
-    }
-  } else {
-    for (int t = threadIdx.x; t < (hi - lo) * kbytes; t += blockDim.x) {
-      const int o = lo + t / kbytes, c = t % kbytes;
-      kpool[(slot * bs + o) * (size_t)kbytes + c] =
-          knew[(((size_t)b * C + jbase + o) * row_elems + (size_t)h * d) * ES + c];
-    }
-  }
-
-  const bool whole = lo == 0 && hi == bs;
-  for (int e = threadIdx.x; e < d; e += blockDim.x) {
-    T* dst = reinterpret_cast<T*>(vpool) + (slot * d + e) * bs;
-    const T* src = reinterpret_cast<const T*>(vnew) + (size_t)b * C * row_elems + (size_t)h * d + e;
-    if (((bs * ES) & 15) == 0) {
-      constexpr int kPer = 16 / ES;
-      for (int c = 0; c < bs / kPer; ++c) {
-        union {
-          uint4 q;
-          T x[kPer];
-        } u;
-        if (!whole) u.q = reinterpret_cast<const uint4*>(dst)[c];
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-          const int o = c * kPer + k;
-          if (o >= lo && o < hi) u.x[k] = src[(size_t)(jbase + o) * row_elems];
-        }
-        reinterpret_cast<uint4*>(dst)[c] = u.q;
-      }
-    } else {
-      for (int o = lo; o < hi; ++o) dst[o] = src[(size_t)(jbase + o) * row_elems];
-    }
+  const size_t row_elems = (size_t)hkv * d;
+  const size_t slot = (((size_t)layer * cap + phys) * hkv + h);
+  const T* ksrc = reinterpret_cast<const T*>(knew);
+  const T* vsrc = reinterpret_cast<const T*>(vnew);
+  T* kdst = reinterpret_cast<T*>(kpool) + slot * bs * (size_t)d;
+  T* vdst = reinterpret_cast<T*>(vpool) + slot * (size_t)d * bs;
+  for (int t = threadIdx.x; t < (hi - lo) * d; t += blockDim.x) {
+    const int o = lo + t / d, e = t % d;
+    const size_t src = ((size_t)b * C + jbase + o) * row_elems + (size_t)h * d + e;
+    kdst[(size_t)o * d + e] = ksrc[src];
+    vdst[(size_t)e * bs + o] = vsrc[src];
   }
 }
 
@@ -242,6 +287,16 @@ __device__ __forceinline__ int rewind_block(const RewindEntry& e, int k, const i
   return k < e.ft ? tables[row + e.nb - 1 - k] : tables[row + (k - e.ft)];
 }
 
+// Rewind of a batch (truncate, then clear when finished: kv.py:150-183 applied
+// as in spec_scheduler.py:302-322). With at most blockDim.x entries freeing at
+// most kRewindItems blocks in all, the freed blocks are spread over the
+// threads (an entry's count scan places block k of entry i at top + off_i + k,
+// the order of the sequential frees) and the call takes four dependent round
+// trips: ids and lengths, block counts, table entries, flag marks. A block
+// already free or listed twice sends the call to the exact sequential replay.
+constexpr int kRewindItems = 8192;
+constexpr int kRewindRounds = kRewindItems / kPoolThreads;
+
 __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
     const int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
     int32_t* __restrict__ seq_lens, int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
@@ -249,6 +304,93 @@ __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
     const int32_t* __restrict__ finished, int32_t n, int32_t bs, int32_t shrink_only, int32_t cap) {
   __shared__ int s_scan[kPoolThreads / 64];
   __shared__ int s_top, s_dup;
+  __shared__ int s_off[kPoolThreads], s_sid[kPoolThreads], s_nb[kPoolThreads], s_ft[kPoolThreads];
+  __shared__ short s_owner[kRewindItems];
+  if (n <= (int)blockDim.x) {
+    const int i = threadIdx.x;
+    const int top = ctr[CTR_TOP];
+    RewindEntry e = rewind_entry(min(i, n - 1), seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+    const int cnt = i < n ? e.ft + e.fc : 0;
+    int total;
+    const int off = block_exclusive_scan(cnt, s_scan, &total);
+    if (total <= kRewindItems) {
+      if (i < n) {
+        s_off[i] = off;
+        s_sid[i] = e.sid;
+        s_nb[i] = e.nb;
+        s_ft[i] = e.ft;
+        for (int k = 0; k < cnt; ++k) s_owner[off + k] = (short)i;
+      }
+      __syncthreads();
+      int ids[kRewindRounds], old[kRewindRounds];
+#pragma unroll
+      for (int j = 0; j < kRewindRounds; ++j) {
+        ids[j] = -1;
+        if (j * (int)blockDim.x < total) {
+          const int t = min(i + j * (int)blockDim.x, total - 1);
+          const int o = s_owner[t], k = t - s_off[o], nbo = s_nb[o], fto = s_ft[o];
+          const size_t row = (size_t)s_sid[o] * maxb;
+          ids[j] = tables[row + (k < fto ? nbo - 1 - k : k - fto)];
+        }
+      }
+      bool mydup = false;
+#pragma unroll
+      for (int j = 0; j < kRewindRounds; ++j) {
+        old[j] = 0;
+        if (i + j * (int)blockDim.x < total) {
+          if ((unsigned)ids[j] >= (unsigned)cap) mydup = true;
+          else old[j] = atomicAdd(&free_flag[ids[j]], 2);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kRewindRounds; ++j) mydup |= old[j] != 0;
+      if (!__syncthreads_or(mydup)) {
+#pragma unroll
+        for (int j = 0; j < kRewindRounds; ++j) {
+          const int t = i + j * (int)blockDim.x;
+          if (t < total) {
+            free_stack[top + t] = ids[j];
+            free_flag[ids[j]] = 1;
+          }
+        }
+        if (i < n) {
+          nblocks[e.sid] = e.nb_final;
+          seq_lens[e.sid] = e.len_final;
+        }
+        if (i == 0) {
+          ctr[CTR_TOP] = top + total;
+          ctr[CTR_PUSHED] = total;
+        }
+        return;
+      }
+      // Undo the marks, then replay sequentially with the reference's rule
+      // `if block in free_list: return` (kv.py:73-74).
+#pragma unroll
+      for (int j = 0; j < kRewindRounds; ++j)
+        if (i + j * (int)blockDim.x < total && (unsigned)ids[j] < (unsigned)cap) atomicSub(&free_flag[ids[j]], 2);
+      __syncthreads();
+      if (i != 0) return;
+      int t = top, pushed = 0;
+      for (int q = 0; q < n; ++q) {
+        const RewindEntry eq = rewind_entry(q, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+        for (int k = 0; k < eq.ft + eq.fc; ++k) {
+          const int id = rewind_block(eq, k, tables, maxb);
+          if ((unsigned)id < (unsigned)cap && t < cap && atomicOr(&free_flag[id], 0) == 0) {
+            free_stack[t++] = id;
+            atomicExch(&free_flag[id], 1);
+            ++pushed;
+          }
+        }
+        nblocks[eq.sid] = eq.nb_final;
+        seq_lens[eq.sid] = eq.len_final;
+      }
+      ctr[CTR_TOP] = t;
+      ctr[CTR_PUSHED] = pushed;
+      ctr[CTR_SLOWPATH] += 1;
+      return;
+    }
+    __syncthreads();
+  }
   if (threadIdx.x == 0) {
     s_top = ctr[CTR_TOP];
     s_dup = 0;
@@ -465,14 +607,19 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
   auto* vp = static_cast<uint8_t*>(v_pool);
   auto* kn = static_cast<const uint8_t*>(k_new);
   auto* vn = static_cast<const uint8_t*>(v_new);
-  if (es == 4)
-    hipLaunchKernelGGL(kv_write_kernel<4>, grid, blk, 0, s, kp, vp, kn, vn, block_tables, max_blocks_per_seq,
-                       num_blocks, seq_lens, seq_ids, start_pos, ctr, C, layer, capacity, block_size,
-                       num_kv_heads, head_dim, write_limit_b);
-  else
-    hipLaunchKernelGGL(kv_write_kernel<2>, grid, blk, 0, s, kp, vp, kn, vn, block_tables, max_blocks_per_seq,
-                       num_blocks, seq_lens, seq_ids, start_pos, ctr, C, layer, capacity, block_size,
-                       num_kv_heads, head_dim, write_limit_b);
+  const bool vec16 = (head_dim * es) % 16 == 0;
+#define SPV_WRITE(KER)                                                                                          \
+  hipLaunchKernelGGL(KER, grid, blk, 0, s, kp, vp, kn, vn, block_tables, max_blocks_per_seq, num_blocks,       \
+                     seq_lens, seq_ids, start_pos, ctr, C, layer, capacity, block_size, num_kv_heads, head_dim, \
+                     write_limit_b)
+  if (es == 4) {
+    if (vec16) SPV_WRITE(kv_write_kernel<4>);
+    else SPV_WRITE(kv_write_small_kernel<4>);
+  } else {
+    if (vec16) SPV_WRITE(kv_write_kernel<2>);
+    else SPV_WRITE(kv_write_small_kernel<2>);
+  }
+#undef SPV_WRITE
   SPV_CHECK_LAUNCH();
   return SPV_OK;
 }

@@ -390,3 +390,33 @@ def test_append_into_filled_pool_touches_only_the_chunk(cuda, dtype, chunk):
             v0[1, blk, :, :, p % bs] = vn[b, j]
     assert torch.equal(gpu.k_pool.cpu(), k0)
     assert torch.equal(gpu.v_pool.cpu(), v0)
+
+
+@pytest.mark.parametrize("n_seq,blocks,truncate_to", [(40, 300, None), (1100, 2, 17), (24, 90, 33)])
+def test_large_rewinds_match_oracle(cuda, n_seq, blocks, truncate_to):
+    """Rewinds beyond the flattened path's limits (more than 8192 freed blocks,
+    more than 1024 entries) and long clears mixed with truncates inside them."""
+    bs = 16
+    cap = n_seq * blocks + 64
+    g = torch.Generator().manual_seed(n_seq)
+    perm = torch.randperm(cap, generator=g).tolist()
+    tables = [perm[i * blocks:(i + 1) * blocks] for i in range(n_seq)]
+    lens = [blocks * bs - int(torch.randint(0, bs, (1,), generator=g)) for _ in range(n_seq)]
+    free = perm[n_seq * blocks:]
+    gpu = PagedKVCache(1, 1, 8, cap, bs, cuda, torch.float32, max_seqs=n_seq, max_blocks_per_seq=blocks)
+    cpu = ref.PagedKVCache(1, 1, 8, cap, bs, store=False)
+    gpu.load_state(tables, lens, free)
+    cpu.load_state(tables, lens, free)
+    sids = list(range(n_seq))
+    if truncate_to is None:
+        new, fin = [-1] * n_seq, [1] * n_seq
+    else:
+        new = [truncate_to + (s % 5) for s in sids]
+        fin = [1 if s % 3 == 0 else 0 for s in sids]
+    gpu.rewind(sids, new, fin)
+    for s, nl, f in zip(sids, new, fin):
+        if nl >= 0:
+            cpu.truncate(s, nl)
+        if f:
+            cpu.clear(s)
+    _same_state(gpu, cpu)
