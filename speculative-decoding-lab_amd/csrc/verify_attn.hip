@@ -334,7 +334,10 @@ __device__ __forceinline__ int ceil_div(int a, int P, float rP) {
 //   s_pref[b]  = pages of the sequences before b (per segment), s_pref[B] = total;
 //   s_kpref[b] = pieces of one segment of each sequence before b, s_kpref[B] = total;
 //   s_sid[b], s_start[b] = seq_ids[b], start_pos[b].
-template <int BS>
+// When the segments alone are at least as many as the workgroups, pieces are
+// not used: the kernel splits the concatenated pages evenly instead, and the
+// search and s_kpref are skipped.
+template <int BS, bool BAL>
 __device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, int* s_sid, int* s_start, long long HR,
                            int nw) {
   if (threadIdx.x < 64) {
@@ -357,6 +360,7 @@ __device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, int* 
       np1 = np;
     }
     if (lane == 0) s_pref[p.B] = carry;
+    if constexpr (!BAL) {
     auto pages_of = [&](int b) { return one ? np1 : s_pref[b + 1] - s_pref[b]; };
     const long long T = HR * carry;
     int P = HR * p.B >= nw ? maxnp : (int)min((long long)maxnp, max(1LL, div_floor(T + nw - 1, nw)));
@@ -382,6 +386,7 @@ __device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, int* 
       carry += lane63(incl);
     }
     if (lane == 0) s_kpref[p.B] = carry;
+    }
   }
   __syncthreads();
 }
@@ -400,14 +405,14 @@ struct PageRegs {
   uint2 v[D / 16];  // dim 16 mt + i16, keys 4 g .. 4 g + 3
 };
 
-// Merge of one segment's partial slots x0 .. x0 + ns - 1 (rows qr0 .. qr0 + nr
-// - 1) into the output. Each thread takes (row, 4 dims) items and issues every
+// Merge of one segment's partial slots slot_of(0 .. ns - 1) (rows qr0 .. qr0 +
+// nr - 1) into the output. Each thread takes (row, 4 dims) items and issues every
 // load of a chunk of kMergeChunk slots -- the slots' (m, l) of its rows and its
 // O slices -- before using any, so a merge of up to kMergeChunk slots costs one
 // uncached round trip and no barrier; more slots are folded in with the
 // usual online rescale.
-template <int QT, int RPG, int D>
-__device__ void merge_segment(const AttnParams& p, int x0, int ns, int b, int h, int qr0, int nr) {
+template <int QT, int RPG, int D, typename SlotOf>
+__device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b, int h, int qr0, int nr) {
   constexpr int kItems = (RPG * (D / 4) + kMfmaThreads - 1) / kMfmaThreads;  // float4 outputs per thread
   float M[kItems], Ls[kItems];
   f32x4_t acc[kItems];
@@ -419,6 +424,9 @@ __device__ void merge_segment(const AttnParams& p, int x0, int ns, int b, int h,
   }
   const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml), ro = coherent_rsrc(p.part_o);
   for (int c0 = 0; c0 < ns; c0 += kMergeChunk) {
+    int slot[kMergeChunk];  // the chunk's slots, uniform
+#pragma unroll
+    for (int k = 0; k < kMergeChunk; ++k) slot[k] = uni(slot_of(min(c0 + k, ns - 1)));
     float2 ml[kItems][kMergeChunk];
     f32x4_t ov[kItems][kMergeChunk];
 #pragma unroll
@@ -429,7 +437,7 @@ __device__ void merge_segment(const AttnParams& p, int x0, int ns, int b, int h,
       for (int k = 0; k < kMergeChunk; ++k) {
         ml[it][k] = make_float2(-INFINITY, 0.f);
         if (rr < nr && c0 + k < ns) {
-          const size_t row = (size_t)(x0 + c0 + k) * p.G + qr0 + rr;
+          const size_t row = (size_t)slot[k] * p.G + qr0 + rr;
           ml[it][k] = load2_coherent(rml, row * 2 * sizeof(float));
           ov[it][k] = load4_coherent(ro, (row * D + e0) * sizeof(float));
         }
@@ -467,7 +475,7 @@ __device__ void merge_segment(const AttnParams& p, int x0, int ns, int b, int h,
   }
 }
 
-template <int NT, int D, int QT>
+template <int NT, int D, int QT, bool BAL>
 __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p) {
   constexpr int KS = D / 32;  // 32-dim k-steps of S^T
   constexpr int MT = D / 16;  // 16-dim tiles of O^T
@@ -498,25 +506,59 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   int* s_sid = s_kpref + p.B + 1;
   int* s_start = s_sid + p.B + 1;
   const long long HR = (long long)p.Hkv * p.nrg;
-  build_plan<BS>(p, s_pref, s_kpref, s_sid, s_start, HR, nw);
+  build_plan<BS, BAL>(p, s_pref, s_kpref, s_sid, s_start, HR, nw);
   if (s_pref[p.B] == 0) return;
-  const long long N = HR * s_kpref[p.B];  // pieces in the batch
-  const long long x_begin = div_floor((long long)wg * N, nw), x_end = div_floor((long long)(wg + 1) * N, nw);
+  // Page-balanced mode (segments >= workgroups): workgroup wg takes pages
+  // [A(wg), A(wg + 1)) of the segments laid end to end (sequence-major, then
+  // (kv head, row group)), A(w) = floor(w * T / nw). Whole segments write the
+  // output; a segment cut by these bounds leaves a partial in slot 2 wg (the
+  // workgroup's first piece) or 2 wg + 1 (its last) for each workgroup
+  // w_a .. w_b that holds part of it. Otherwise: equal pieces, one slot each.
+  constexpr bool balanced = BAL;  // chosen by the host: HR * B >= nw
+  const long long T = HR * s_pref[p.B];  // pages of all segments
+  auto page_start = [&](long long w) { return div_floor(w * T, nw); };
+  auto owner = [&](long long g) { return (int)div_floor((g + 1) * nw - 1, T); };  // workgroup holding page g
+  const long long N = balanced ? 0 : HR * s_kpref[p.B];  // pieces in the batch
+  const long long x_begin = balanced ? page_start(wg) : div_floor((long long)wg * N, nw);
+  const long long x_end = balanced ? page_start(wg + 1) : div_floor((long long)(wg + 1) * N, nw);
   const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
   const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
   const uint16_t* qbase = static_cast<const uint16_t*>(p.q);
   const float sl2 = p.scale_log2;
 
-  for (long long x = x_begin; x < x_end; ++x) {
-    const int b = uni(seq_of(s_kpref, p.B, HR, x));
-    const int kb = uni(s_kpref[b + 1] - s_kpref[b]);  // pieces per segment of sequence b
-    const int rem = (int)(x - HR * s_kpref[b]);
-    const int hr = rem / kb, piece = rem - hr * kb;
-    const int np = uni(s_pref[b + 1] - s_pref[b]);
-    const int lp0 = (int)div_floor((long long)piece * np, kb), lp1 = (int)div_floor((long long)(piece + 1) * np, kb);
+  for (long long x = x_begin; x < x_end;) {
+    // This piece: pages [lp0, lp1) of segment (b, hr); its partial slot, and
+    // the number of pieces (arrivals) of its segment.
+    int b, hr, lp0, lp1, slot, narr, x0 = 0, w_a = 0;
+    long long Gs = 0;
+    if constexpr (BAL) {
+      b = uni(seq_of(s_pref, p.B, HR, x));
+      const int np = uni(s_pref[b + 1] - s_pref[b]);
+      const int local = (int)(x - HR * s_pref[b]);
+      hr = local / np;
+      lp0 = local - hr * np;
+      lp1 = (int)min((long long)np, lp0 + (x_end - x));
+      Gs = HR * s_pref[b] + (long long)hr * np;
+      w_a = owner(Gs);
+      narr = owner(Gs + np - 1) - w_a + 1;
+      slot = 2 * wg + (x == x_begin ? 0 : 1);
+      x += lp1 - lp0;
+    } else {
+      b = uni(seq_of(s_kpref, p.B, HR, x));
+      const int kb = uni(s_kpref[b + 1] - s_kpref[b]);  // pieces per segment of sequence b
+      const int rem = (int)(x - HR * s_kpref[b]);
+      hr = rem / kb;
+      const int piece = rem - hr * kb;
+      const int np = uni(s_pref[b + 1] - s_pref[b]);
+      lp0 = (int)div_floor((long long)piece * np, kb);
+      lp1 = (int)div_floor((long long)(piece + 1) * np, kb);
+      x0 = (int)(x - piece);  // the segment's first piece
+      narr = kb;
+      slot = (int)x;
+      x += 1;
+    }
     const int h = hr / p.nrg, rg = hr - h * p.nrg;
     const int seg = b * (int)HR + hr;
-    const int x0 = (int)(x - piece);  // the segment's first piece
     const int start = uni(s_start[b]);
     const int L = start + p.C;
     const int qr0 = rg * RPG;
@@ -556,15 +598,28 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     }
 
     int tab0 = lp0;  // first page whose block id is sTab[0]
+    // With four query tiles (no registers to spare) pages are read through raw
+    // buffers: the page's base is scalar and each lane keeps one 32-bit offset
+    // for K and one for V (the k-step and tile offsets are scalar operands), so
+    // no 64-bit lane address lives across the walk to be spilled and reloaded.
+    const uint32_t koff = (uint32_t)(i16 * D + 8 * g) * 2u, voff = (uint32_t)(i16 * BS + 4 * g) * 2u;
     auto load_page = [&](PageRegs<D>& f, int page) {
       const int phys = uni(sTab[page - tab0]);
       const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
-      const uint16_t* kp = kbase + slot;
-      const uint16_t* vp = vbase + slot;
+      const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase + slot, BS * D * 2), rv = span_rsrc(vbase + slot, BS * D * 2);
+      if constexpr (NT >= 4) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) f.k[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
+        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint4, load_b128(rk, koff, 64u * ks));
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) f.v[mt] = *reinterpret_cast<const uint2*>(vp + (16 * mt + i16) * BS + 4 * g);
+        for (int mt = 0; mt < MT; ++mt) f.v[mt] = __builtin_bit_cast(uint2, load_b64(rv, voff, 32u * BS * mt));
+      } else {
+        const uint16_t* kp = kbase + slot;
+        const uint16_t* vp = vbase + slot;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) f.k[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) f.v[mt] = *reinterpret_cast<const uint2*>(vp + (16 * mt + i16) * BS + 4 * g);
+      }
     };
 
     auto compute_page = [&](PageRegs<D>& f, int page) {
@@ -704,8 +759,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // thread takes (row, tile, 4 dims), adds the NWV slots with the row's
     // factors 2^(m_w - M) (fixed order) and writes the output -- or the
     // partial -- directly.
-    const bool final_out = kb == 1;
-    const int slot = (int)x;
+    const bool final_out = narr == 1;
     // Row factors: thread r < nr turns its row's wave maxima into the factors
     // 2^(m_w - M) in place (sm_m[w][r]) and the row's 1 / L into sm_l[0][r],
     // and writes the row's (M, L) partial; the first round's barrier publishes
@@ -799,10 +853,18 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(p.counters + seg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == kb;
+        s_last = __hip_atomic_fetch_add(p.counters + seg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == narr;
       __syncthreads();
       if (s_last) {
-        merge_segment<QT, RPG, D>(p, x0, kb, b, h, qr0, nr);
+        // The segment's slots: its pieces in order (equal pieces), or each of
+        // workgroups w_a .. w_b -- slot 2w when the segment holds the
+        // workgroup's first page, else 2w + 1.
+        if constexpr (BAL) {
+          merge_segment<QT, RPG, D>(
+              p, [&](int k) { return 2 * (w_a + k) + (page_start(w_a + k) >= Gs ? 0 : 1); }, narr, b, h, qr0, nr);
+        } else {
+          merge_segment<QT, RPG, D>(p, [&](int k) { return x0 + k; }, narr, b, h, qr0, nr);
+        }
         if (threadIdx.x == 0) p.counters[seg] = 0;
       }
     }
@@ -848,7 +910,7 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
   // The MFMA kernel addresses the output and the partial slots with 32-bit
   // offsets (bytes for the partials).
   const bool fits32 = (long long)B * C * Hq * d < (1LL << 31) &&
-                      (long long)kMfmaWGsMax * G * d * (long long)sizeof(float) < (1LL << 31);
+                      2LL * kMfmaWGsMax * G * d * (long long)sizeof(float) < (1LL << 31);
   pl.mfma = kv_dtype == SPV_BF16 && q_dtype == SPV_BF16 && bs == 16 && (d == 128 || d == 64) && G >= 16 &&
             B <= kMfmaMaxB && fits32;
   const int max_pages = (max_ctx + bs - 1) / bs;
@@ -872,7 +934,7 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
 // Partial rows the plan may write (0: the call needs no partials).
 size_t partial_rows(const Plan& pl, int B, int C, int Hq, int Hkv) {
   const size_t G = (size_t)C * (Hq / Hkv);
-  if (pl.mfma) return (size_t)kMfmaWGsMax * G;  // one slot per piece, at most one piece per workgroup
+  if (pl.mfma) return (size_t)2 * kMfmaWGsMax * G;  // two partial slots per workgroup
   if (pl.max_splits <= 1) return 0;
   return (size_t)B * Hkv * pl.max_splits * G;
 }
@@ -921,16 +983,26 @@ int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s) {
   return SPV_OK;
 }
 
+template <int D, bool BAL>
+void launch_mfma_mode(const AttnParams& p, int nt, hipStream_t s, dim3 grid, size_t smem) {
+  const dim3 blk(kMfmaThreads);
+  switch (nt) {
+    case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
+    case 3: hipLaunchKernelGGL((attn_mfma_kernel<3, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
+    default: hipLaunchKernelGGL((attn_mfma_kernel<4, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
+  }
+}
+
+// Equal pieces when the workgroups outnumber the (sequence, kv head, row
+// group) segments, else the page-balanced split.
 template <int D>
 void launch_mfma(const AttnParams& p, int nt, hipStream_t s) {
   const size_t smem = (size_t)4 * (p.B + 1) * sizeof(int);  // page / piece prefixes, ids, starts
-  const dim3 grid(persistent_wgs()), blk(kMfmaThreads);
-  switch (nt) {
-    case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16>), grid, blk, smem, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16>), grid, blk, smem, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_mfma_kernel<3, D, SPV_BF16>), grid, blk, smem, s, p); break;
-    default: hipLaunchKernelGGL((attn_mfma_kernel<4, D, SPV_BF16>), grid, blk, smem, s, p); break;
-  }
+  const int nw = persistent_wgs();
+  const bool balanced = (long long)p.Hkv * p.nrg * p.B >= nw;
+  if (balanced) launch_mfma_mode<D, true>(p, nt, s, dim3(nw), smem);
+  else launch_mfma_mode<D, false>(p, nt, s, dim3(nw), smem);
 }
 
 }  // namespace

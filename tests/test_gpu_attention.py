@@ -233,3 +233,26 @@ def test_gather_ctx_matches_written_values(cuda):
     for s, L in enumerate(lens):
         got = gather_ctx(gpu, 0, s, L + C).cpu()
         assert torch.equal(got[0], keys[s]) and torch.equal(got[1], values[s])
+
+
+@pytest.mark.parametrize("B,C,Hq", [(160, 7, 16), (130, 6, 12)])
+def test_page_balanced_split_when_segments_outnumber_workgroups(cuda, B, C, Hq):
+    # With at least as many (sequence, kv head) segments as workgroups the
+    # pages are split evenly across workgroups: long segments are cut over
+    # several of them (partials merged by the last to arrive), short ones are
+    # whole inside one. Log-uniform lengths make both happen.
+    import math
+
+    import engine.attention as A
+
+    Hkv, d = 2, 128
+    g = torch.Generator().manual_seed(B + C)
+    lens = [int(math.exp(math.log(16) + (math.log(3000) - math.log(16)) * float(u)))
+            for u in torch.rand(B, generator=g)]
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.bfloat16, seed=B)
+    q = torch.randn(B, C, Hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    outs = [verify_attention(q, gpu, 0, list(range(B)), lens, max(lens) + C).clone() for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert int(torch.count_nonzero(A._workspace._buf[: 1 << 18])) == 0
+    _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, Hq))
