@@ -51,14 +51,17 @@ C = GAMMA + 1
 REPLICAS, LOGIT_SETS = 8, 2
 
 
-def attention_bytes(lens):
-    """Algorithmic HBM bytes of one verify-attention call (one layer)."""
+def attention_bytes(lens, chunk=C, hq=HQ, hkv=HKV, d=D, bs=BS):
+    """Algorithmic HBM bytes of one verify-attention call (one layer, bf16):
+    per sequence of context ``L`` the K and V rows of the ``L + chunk``
+    attended keys, the query read and output write, the block-table entries and
+    the start / id words."""
     total = 0
     for L in lens:
-        n = L + C
-        total += n * 2 * HKV * D * 2          # K and V of every attended key (bf16)
-        total += 2 * C * HQ * D * 2           # q read + out write (bf16)
-        total += 4 * math.ceil(n / BS) + 8    # block-table entries + start / id
+        n = L + chunk
+        total += n * 2 * hkv * d * 2
+        total += 2 * chunk * hq * d * 2
+        total += 4 * math.ceil(n / bs) + 8
     return total
 
 
@@ -283,6 +286,98 @@ def cpu_baseline(w, budget_s=10.0):
     }
 
 
+# Full-depth continuous batching: Qwen2.5-3B-shaped model, gamma 6.
+FD_LAYERS, FD_HQ, FD_HKV, FD_D, FD_BS, FD_GAMMA, FD_BATCH = 36, 16, 2, 128, 16, 6, 128
+FD_CTX = (512, 8192)          # prompt lengths, log-uniform
+FD_BUDGET = (32, 160)         # new tokens per request, uniform
+FD_RATE = 4.0                 # Poisson arrivals per step once the first batch is in
+FD_SIGMA = 1.05               # draft = target + N(0, sigma^2): acceptance ~0.6 per draft
+
+
+def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
+    """Continuous batching at full depth on one GPU.
+
+    A pool sized to most of the device's free HBM (its free list shuffled, as
+    after a long run), 128 requests at step 0 and a Poisson stream behind them
+    keep the batch at its cap of 128 sequences; every round appends the 7 verify
+    tokens in each of 36 layers, runs 36 verify attentions, the fused sampling
+    and the rewind (``engine.continuous``). Rounds are timed on the host
+    (device drained before each, one synchronisation at its end) and on the
+    device with events around every layer's append and attention.
+    """
+    import statistics
+
+    import torch
+
+    from engine.continuous import SpecContinuousDriver, SyntheticVerifyModel, poisson_requests
+    from engine.kv import PagedKVCache
+
+    chunk = FD_GAMMA + 1
+    model = SyntheticVerifyModel(FD_LAYERS, FD_HQ, FD_HKV, FD_D, VOCAB, FD_GAMMA, FD_BATCH, dev,
+                                 torch.bfloat16, seed=seed, draft_sigma=FD_SIGMA, prompt_cap=FD_CTX[1])
+    block_bytes = FD_LAYERS * 2 * FD_HKV * FD_BS * FD_D * 2
+    free, total = torch.cuda.mem_get_info(dev)
+    cap = int(pool_frac * free) // block_bytes
+    maxb = -(-(FD_CTX[1] + FD_BUDGET[1] + chunk) // FD_BS) + 1
+    n_req = FD_BATCH + int(FD_RATE * (rounds + warmup)) + 16
+    kv = PagedKVCache(FD_LAYERS, FD_HKV, FD_D, cap, FD_BS, dev, torch.bfloat16, max_seqs=n_req,
+                      max_blocks_per_seq=maxb)
+    g = torch.Generator().manual_seed(seed + 1)
+    kv.allocator.load_free_list(torch.randperm(cap, generator=g).to(torch.int32))
+    first = poisson_requests(FD_BATCH, 0.0, FD_CTX[0], FD_CTX[1], *FD_BUDGET, seed=seed + 2)
+    stream = poisson_requests(n_req - FD_BATCH, FD_RATE, FD_CTX[0], FD_CTX[1], *FD_BUDGET, seed=seed + 3,
+                              first_sid=FD_BATCH)
+    drv = SpecContinuousDriver(kv, model, FD_GAMMA, FD_BATCH, temperature=1.0)
+    per_round = []
+
+    def on_round(info):
+        n = len(info.sids)
+        per_round.append({"batch": n, "host_s": info.seconds, "gpu": info.gpu_ms,
+                          "attn_bytes": attention_bytes(info.starts, chunk, FD_HQ, FD_HKV, FD_D, FD_BS),
+                          "ctx": sum(info.starts) / n, "k": info.result.n_commit.tolist()})
+
+    res = drv.run(first + stream, max_steps=rounds + warmup, on_round=on_round, sync_timing=True,
+                  gpu_timing=True)
+    torch.cuda.synchronize()
+    timed = per_round[warmup:]
+    med = statistics.median
+    host_us = med(r["host_s"] for r in timed) * 1e6
+    gpu_us = med(r["gpu"]["round"] for r in timed) * 1e3
+    attend_ms = sum(r["gpu"]["attend"] for r in timed)
+    attn_gbs = sum(r["attn_bytes"] for r in timed) * FD_LAYERS / (attend_ms * 1e-3) / 1e9
+    ks = [k for r in timed for k in r["k"]]
+    batch = sum(r["batch"] for r in timed) / len(timed)
+    out = {
+        "workload": "Qwen2.5-3B-shaped continuous batching: {} layers, {}q/{}kv heads, head_dim {}, "
+                    "block {}, bf16 KV, gamma {}, batch cap {}, prompts log-U[{},{}], budgets U[{},{}], "
+                    "Poisson arrivals {}/step, draft = target + N(0,{}^2) over V={}, T=1; pool of {} blocks "
+                    "({:.1f} GB of {:.1f} GB HBM) with a shuffled free list".format(
+                        FD_LAYERS, FD_HQ, FD_HKV, FD_D, FD_BS, FD_GAMMA, FD_BATCH, FD_CTX[0], FD_CTX[1],
+                        FD_BUDGET[0], FD_BUDGET[1], FD_RATE, FD_SIGMA, VOCAB, cap, cap * block_bytes / 1e9,
+                        total / 1e9),
+        "rounds": len(timed),
+        "mean_batch": round(batch, 1),
+        "mean_ctx": round(sum(r["ctx"] for r in timed) / len(timed), 1),
+        "us_per_round": round(host_us, 1),
+        "us_per_seq": round(host_us / batch, 3),
+        "gpu_us_per_round": round(gpu_us, 1),
+        "gpu_us_per_seq": round(gpu_us / batch, 3),
+        "attend_us_per_layer": round(med(r["gpu"]["attend"] for r in timed) * 1e3 / FD_LAYERS, 2),
+        "append_us_per_layer": round(med(r["gpu"]["append"] for r in timed) * 1e3 / FD_LAYERS, 2),
+        "sample_rewind_us": round(med(r["gpu"]["sample"] for r in timed) * 1e3, 1),
+        "attn_gbs": round(attn_gbs, 1),
+        "mean_commit_per_seq_round": round(sum(ks) / len(ks), 3),
+        "mean_acceptance": round(sum(ks) / len(ks) / chunk, 4),
+        "admitted": res.admitted,
+        "finished": res.finished,
+        "pool_blocks": cap,
+        "peak_blocks": res.kv_peak_blocks,
+    }
+    del kv, model, drv
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -290,6 +385,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--full-depth-rounds", type=int, default=24,
+                    help="rounds of the 36-layer continuous-batching measurement (0 skips it)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -383,6 +480,12 @@ def main() -> int:
     if not args.no_cpu_baseline:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(w)
+    if args.full_depth_rounds > 0:
+        del g_step, g_att, g_smp, g_ar, step, parts, res, w
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        print("bench: full-depth continuous batching", file=sys.stderr, flush=True)
+        line["full_depth"] = full_depth(dev, args.full_depth_rounds, 4, args.seed)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -76,8 +76,11 @@ int spv_pool_free_one(int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
  * set to 1 + its batch index. `write_limit_b` (the failing batch index, or B)
  * restricts the token writes exactly as the reference's raise would: sequences
  * after it write nothing, and it writes only tokens whose block exists.
- * write_limit_b = -1 (with may_alloc) takes that index from ctr[1] as set by
- * this call's allocation, so a caller need not know it in advance.
+ * write_limit_b = -1 takes that index from ctr[1] as the last allocation on
+ * this pool set it: with may_alloc, this call's own; with may_alloc = 0, the
+ * allocation of an earlier call for the same chunk (the later layers of one
+ * verify round, whose blocks the first layer's call allocated), so a caller
+ * need not know the index in advance.
  * seq_lens[sid] = max(seq_lens[sid], last written position + 1). seq_ids must
  * be distinct within one call. k_new = v_new = NULL allocates only
  * (PagedKVCache._ensure_blocks_up_to, kv.py:119-122): no copy, no length change. */

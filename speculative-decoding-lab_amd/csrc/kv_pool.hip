@@ -590,7 +590,7 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
   if (B < 0 || C < 1 || layer < 0 || capacity < 1 || block_size < 1 || num_kv_heads < 1 || head_dim < 1 ||
       max_blocks_per_seq < 1 || write_limit_b < -1 || write_limit_b > B)
     return SPV_ERR_ARG;
-  if (write_limit_b < 0 && (!may_alloc || !ctr)) return SPV_ERR_ARG;
+  if (write_limit_b < 0 && !ctr) return SPV_ERR_ARG;
   if ((C + block_size - 1) / block_size + 1 > 65535) return SPV_ERR_ARG;  // blocks one chunk can touch
   if (B == 0) return SPV_OK;
   hipStream_t s = (hipStream_t)stream;

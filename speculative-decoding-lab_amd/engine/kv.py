@@ -309,14 +309,16 @@ class PagedKVCache:
             raise _exhausted(self.allocator.capacity)
 
     def write_block_device(self, layer: int, seq_ids: torch.Tensor, start_positions: torch.Tensor,
-                           k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+                           k_new: torch.Tensor, v_new: torch.Tensor, alloc: bool = True) -> None:
         """``write_block`` with int32 device ``seq_ids``/``start_positions`` and no host sync.
 
         The allocation decides on the device which sequence (if any) exhausts
         the pool and limits the writes exactly as ``write_block`` does; the host
         learns of it -- ``BlockExhaustedError`` -- at the next metadata query. The
         caller guarantees distinct, added sequence ids and that every table fits
-        ``max_blocks_per_seq`` blocks.
+        ``max_blocks_per_seq`` blocks. ``alloc=False`` skips the allocation for
+        a chunk whose blocks an earlier call allocated (the same ids and starts
+        in an earlier layer) and applies that call's exhaustion verdict.
         """
         B, chunk = int(k_new.shape[0]), int(k_new.shape[1])
         if B == 0:
@@ -325,7 +327,7 @@ class PagedKVCache:
              ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
              ptr(self.allocator.free_stack), ptr(self.allocator.free_flag), ptr(self.allocator.ctr),
              ptr(seq_ids), ptr(start_positions), B, chunk, int(layer), self.allocator.capacity,
-             self.block_size, self.num_kv_heads, self.head_dim, 1, -1, self._stream())
+             self.block_size, self.num_kv_heads, self.head_dim, 1 if alloc else 0, -1, self._stream())
         self._stale = True
         self.allocator._stale = True
 

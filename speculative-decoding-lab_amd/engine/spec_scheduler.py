@@ -198,18 +198,34 @@ class VerifyStep:
     def attend_layers(self, seq_ids: Sequence[int], start_positions: Sequence[int],
                       q_layers: Sequence[torch.Tensor], k_layers: Sequence[torch.Tensor],
                       v_layers: Sequence[torch.Tensor],
-                      outs: Optional[Sequence[torch.Tensor]] = None) -> List[torch.Tensor]:
+                      outs: Optional[Sequence[torch.Tensor]] = None,
+                      events: Optional[list] = None) -> List[torch.Tensor]:
+        """Append and attend, layer by layer. With ``events`` (a list), timing
+        events are recorded on the current stream and appended to it: before
+        each layer's append, before its attention, and after the last attention
+        (``2 * layers + 1`` events)."""
         chunk = self.gamma + 1
         max_ctx = max(int(s) for s in start_positions) + chunk
         sid_t = _hip.i32(seq_ids, self.kv.device)
         st_t = _hip.i32(start_positions, self.kv.device)
         results = []
         self.kv._grow_width(-(-max_ctx // self.kv.block_size))
+
+        def mark():
+            if events is not None:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record()
+                events.append(e)
+
         for layer in range(len(q_layers)):
+            mark()
+            # the first layer's call allocates the chunk's blocks for every layer
             self.kv.write_block_device(layer, sid_t, st_t, k_layers[layer].to(self.kv.dtype).contiguous(),
-                                       v_layers[layer].to(self.kv.dtype).contiguous())
+                                       v_layers[layer].to(self.kv.dtype).contiguous(), alloc=layer == 0)
+            mark()
             results.append(verify_attention(q_layers[layer], self.kv, layer, sid_t, st_t, max_ctx,
                                             out=None if outs is None else outs[layer]))
+        mark()
         return results
 
     def sample_and_commit(self, seq_ids: Sequence[int], start_positions: Sequence[int],

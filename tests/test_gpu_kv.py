@@ -420,3 +420,69 @@ def test_large_rewinds_match_oracle(cuda, n_seq, blocks, truncate_to):
         if f:
             cpu.clear(s)
     _same_state(gpu, cpu)
+
+
+@pytest.mark.parametrize("exhaust", [False, True])
+def test_later_layers_write_without_allocating(cuda, exhaust):
+    """A verify round writes every layer of one chunk; only the first call
+    allocates. Later layers (alloc=False) must store exactly what per-layer
+    host-checked writes store, and after an exhaustion at the first layer they
+    keep its verdict: the same sequences and positions are cut off."""
+    H, d, bs = 2, 8, 2
+    cap = 7 if exhaust else 16
+    gpu = PagedKVCache(2, H, d, cap, bs, cuda, torch.float32)
+    cpu = ref.PagedKVCache(2, H, d, cap, bs)
+    for kv in (gpu, cpu):
+        for s in range(3):
+            kv.add_sequence(s)
+    g = torch.Generator().manual_seed(4)
+    k0 = torch.randn(3, 3, H, d, generator=g)
+    gpu.write_block(0, [0, 1, 2], [0, 0, 0], k0.to(cuda), k0.to(cuda))
+    cpu.write_block(0, [0, 1, 2], [0, 0, 0], k0, k0)
+    gpu.write_block(1, [0, 1, 2], [0, 0, 0], k0.to(cuda), k0.to(cuda))
+    cpu.write_block(1, [0, 1, 2], [0, 0, 0], k0, k0)
+    sids, starts = [2, 0, 1], [3, 3, 1]
+    kn = [torch.randn(3, 5, H, d, generator=g) for _ in range(2)]
+    vn = [torch.randn(3, 5, H, d, generator=g) for _ in range(2)]
+    sid_t = torch.tensor(sids, dtype=torch.int32, device=cuda)
+    st_t = torch.tensor(starts, dtype=torch.int32, device=cuda)
+    for layer in range(2):
+        gpu.write_block_device(layer, sid_t, st_t, kn[layer].to(cuda), vn[layer].to(cuda), alloc=layer == 0)
+    raised = False
+    for layer in range(2):
+        try:
+            cpu.write_block(layer, sids, starts, kn[layer], vn[layer])
+        except ref.BlockExhaustedError:
+            raised = True  # the reference stops at the raise
+            break
+    assert raised == exhaust
+    if exhaust:
+        with pytest.raises(BlockExhaustedError):
+            gpu.seq_lengths
+    _same_state(gpu, cpu)
+    if exhaust:
+        # Sequence 2 (batch index 0) fails: 1 free block for 2 missing ones.
+        # It writes positions 3..5; sequences 0 and 1 come after it and write
+        # nothing. Layer 1 (written without allocating) holds its own data in
+        # exactly the positions layer 0 wrote.
+        assert cpu.seq_lengths == [3, 3, 6]
+        for s in range(3):
+            n = cpu.seq_lengths[s]
+            got0 = gather_ctx(gpu, 0, s, n).cpu()
+            want0 = torch.stack([torch.cat([cpu.k[0, b] for b in cpu.block_tables[s]])[:n],
+                                 torch.cat([cpu.v[0, b] for b in cpu.block_tables[s]])[:n]])
+            assert torch.equal(got0, want0)
+            got1 = gather_ctx(gpu, 1, s, n).cpu()
+            if s == 2:
+                want1 = torch.stack([torch.cat([k0[2], kn[1][0, :3]]), torch.cat([k0[2], vn[1][0, :3]])])
+            else:
+                want1 = torch.stack([k0[s], k0[s]])
+            assert torch.equal(got1, want1)
+    else:
+        for layer in range(2):
+            for s in range(3):
+                n = cpu.seq_lengths[s]
+                got = gather_ctx(gpu, layer, s, n).cpu()
+                want = torch.stack([torch.cat([cpu.k[layer, b] for b in cpu.block_tables[s]])[:n],
+                                    torch.cat([cpu.v[layer, b] for b in cpu.block_tables[s]])[:n]])
+                assert torch.equal(got, want)
