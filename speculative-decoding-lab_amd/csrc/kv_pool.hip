@@ -6,8 +6,11 @@
 // order. Here the same state lives in HBM and each batched operation is one
 // launch: allocation/rewind are single-workgroup kernels (an exclusive scan over
 // the batch fixes every sequence's slice of the stack, so the resulting stack
-// order is exactly the order the sequential list operations would produce) and
-// the K/V copy of an append is a separate many-workgroup kernel.
+// order is exactly the order the sequential list operations would produce). An
+// append is one many-workgroup launch in which every workgroup recomputes that
+// scan for itself; the separate allocation and copy kernels remain for the
+// cases that launch does not cover (allocation only, no allocation, chunks that
+// touch more than 8 blocks, head dims whose rows are not 16-byte multiples).
 #include "spv_common.h"
 
 using namespace spv;
@@ -202,6 +205,161 @@ __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(
         reinterpret_cast<uint4*>(kdst + (size_t)(lo + ik / vec) * (d * ES))[ik % vec] = kreg[k];
       const int iv = base + (int)threadIdx.x + k * kWriteThreads;
       if (iv < nv && lo + iv / d < hi) vdst[(size_t)(iv % d) * bs + lo + iv / d] = vreg[k];
+    }
+  }
+}
+
+// Allocation and copy of an append in one launch. Every workgroup, one per
+// (batch entry b, kv head h), recomputes the batch's allocation from the
+// launch-start state -- the same exclusive scan over the batch as
+// kv_alloc_kernel, with the stack's top entries staged in LDS -- so it knows
+// the physical block of each of its chunk's tokens without waiting for another
+// workgroup. The state the scan reads (block counts, stack height) must not
+// change while any workgroup still reads it, so the workgroup that arrives last
+// (every workgroup counts itself in once its loads have returned) writes the
+// new block counts, the stack height and the exhaustion verdict; the
+// workgroups with h = 0 write their own sequence's new table entries, flags and
+// length, which no workgroup reads. Round trips: ids / starts / stack height
+// (and the chunk's new keys and values, which depend on nothing), then the
+// block counts, existing table entries and stack entries; then the arrival
+// count travels while the copy is stored.
+constexpr int kFusedThreads = 256;
+constexpr int kFusedMaxB = 1024;    // batch entries the block counts are kept for in LDS
+constexpr int kFusedStage = 1024;   // stack entries staged in LDS
+constexpr int kFusedMaxBlocks = 8;  // blocks one chunk can touch: C <= 6 * bs
+
+template <int ES>
+__global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
+    uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool, const uint8_t* __restrict__ knew,
+    const uint8_t* __restrict__ vnew, int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+    int32_t* __restrict__ seq_lens, const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+    int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start,
+    int32_t B, int32_t C, int32_t layer, int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t limit_b) {
+  using T = typename Elem<ES>::T;
+  __shared__ int s_scan[kFusedThreads / 64];
+  __shared__ int s_free[kFusedStage];
+  __shared__ int s_nbnew[kFusedMaxB], s_sid[kFusedMaxB];
+  __shared__ int s_fail, s_off, s_got, s_nbold, s_flag;
+  __shared__ int s_phys[kFusedMaxBlocks];
+  const int b = blockIdx.x / hkv, h = blockIdx.x - b * hkv;
+  const size_t row_elems = (size_t)hkv * d;
+  const int vec = (d * ES) >> 4;  // 16-byte pieces of one K row
+  const int nk = C * vec, nv = C * d;
+  // The chunk's new keys and values (round trip 1, independent of the state).
+  uint4 kreg[kWriteItems];
+  T vreg[kWriteItems];
+#pragma unroll
+  for (int k = 0; k < kWriteItems; ++k) {
+    const int ik = min((int)threadIdx.x + k * kFusedThreads, nk - 1);
+    kreg[k] = reinterpret_cast<const uint4*>(knew + (((size_t)b * C + ik / vec) * row_elems + (size_t)h * d) * ES)[ik % vec];
+    const int iv = min((int)threadIdx.x + k * kFusedThreads, nv - 1);
+    vreg[k] = reinterpret_cast<const T*>(vnew)[((size_t)b * C + iv / d) * row_elems + (size_t)h * d + iv % d];
+  }
+  const int top = ctr[CTR_TOP];
+  const int sid = seq_ids[b], s0 = start[b];
+  const int e0 = min((int)threadIdx.x, B - 1);
+  const int sid_e0 = seq_ids[e0], st_e0 = start[e0];
+  // Round trip 2: block counts of the whole batch, the stack's top entries and
+  // this entry's existing table entries (clamped, used only when they exist).
+  int nb_e = nblocks[sid_e0];
+  const int maxneed = min(B * ((C + bs - 1) / bs + 1), kFusedStage);
+  const int nstage = min(top, maxneed);
+  for (int i = threadIdx.x; i < nstage; i += kFusedThreads) s_free[i] = free_stack[top - 1 - i];
+  const int blk0 = max(s0, 0) / bs;
+  const int nyb = (max(s0, 0) + C - 1) / bs - blk0 + 1;  // blocks the chunk touches
+  int tab = 0;
+  if ((int)threadIdx.x < nyb) tab = tables[(size_t)sid * maxb + min(blk0 + (int)threadIdx.x, maxb - 1)];
+  if (threadIdx.x == 0) s_fail = B;
+  int consumed = 0;
+  for (int base = 0; base < B; base += kFusedThreads) {
+    const int e = base + threadIdx.x;
+    int nb = 0, need = 0;
+    if (e < B) {
+      const int st = base == 0 ? st_e0 : start[e];
+      nb = base == 0 ? nb_e : nblocks[seq_ids[e]];
+      need = max(0, (st + C - 1) / bs + 1 - nb);
+    }
+    int total;
+    const int off = block_exclusive_scan(need, s_scan, &total);
+    const int avail = top - consumed;
+    const int got = min(need, max(0, avail - off));
+    if (e < B) {
+      if (got < need) atomicMin(&s_fail, e);
+      s_nbnew[e] = nb + got;
+      s_sid[e] = base == 0 ? sid_e0 : seq_ids[e];
+      if (e == b) {
+        s_off = consumed + off;
+        s_got = got;
+        s_nbold = nb;
+      }
+    }
+    consumed += min(total, max(avail, 0));
+    __syncthreads();
+  }
+  const int off = s_off, got = s_got, nb_old = s_nbold, fail = s_fail;
+  const int nb_new = nb_old + got;
+  auto stack_at = [&](int pos) { return pos < nstage ? s_free[pos] : free_stack[top - 1 - pos]; };
+  if ((int)threadIdx.x < nyb) {
+    const int blk = blk0 + threadIdx.x;
+    s_phys[threadIdx.x] = blk < nb_old ? tab : (blk < nb_new ? stack_at(off + blk - nb_old) : -1);
+  }
+  if (h == 0 && (int)threadIdx.x < got && nb_old + (int)threadIdx.x < maxb) {
+    const int id = stack_at(off + threadIdx.x);
+    tables[(size_t)sid * maxb + nb_old + threadIdx.x] = id;
+    free_flag[id] = 0;
+  }
+  __syncthreads();
+  // Every load of the block counts and the stack height has returned (the
+  // scan consumed them before the barrier): count this workgroup in now and
+  // take the answer only after the copy has been issued.
+  int arrived = 0;
+  if (threadIdx.x == 0) arrived = __hip_atomic_fetch_add(&ctr[CTR_ARRIVE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // The copy: entries after the write limit store nothing, the limit entry
+  // only the tokens whose block exists.
+  const int lim = limit_b >= 0 ? limit_b : (fail < B ? fail : 0x7fffffff);
+  const int n = (b > lim || s0 < 0) ? 0 : min(C, nb_new * bs - s0);
+  if (n > 0) {
+    if (h == 0 && threadIdx.x == 0 && seq_lens[sid] < s0 + n) seq_lens[sid] = s0 + n;
+    for (int base = 0; base < max(nk, nv); base += kWriteItems * kFusedThreads) {
+      if (base > 0) {
+#pragma unroll
+        for (int k = 0; k < kWriteItems; ++k) {
+          const int ik = min(base + (int)threadIdx.x + k * kFusedThreads, nk - 1);
+          kreg[k] = reinterpret_cast<const uint4*>(knew + (((size_t)b * C + ik / vec) * row_elems + (size_t)h * d) * ES)[ik % vec];
+          const int iv = min(base + (int)threadIdx.x + k * kFusedThreads, nv - 1);
+          vreg[k] = reinterpret_cast<const T*>(vnew)[((size_t)b * C + iv / d) * row_elems + (size_t)h * d + iv % d];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kWriteItems; ++k) {
+        const int ik = base + (int)threadIdx.x + k * kFusedThreads;
+        if (ik < nk && ik / vec < n) {
+          const int p = s0 + ik / vec, phys = s_phys[p / bs - blk0];
+          if ((unsigned)phys < (unsigned)cap) {
+            uint8_t* kdst = kpool + ((((size_t)layer * cap + phys) * hkv + h) * bs + p % bs) * (size_t)(d * ES);
+            reinterpret_cast<uint4*>(kdst)[ik % vec] = kreg[k];
+          }
+        }
+        const int iv = base + (int)threadIdx.x + k * kFusedThreads;
+        if (iv < nv && iv / d < n) {
+          const int p = s0 + iv / d, phys = s_phys[p / bs - blk0];
+          if ((unsigned)phys < (unsigned)cap) {
+            T* vdst = reinterpret_cast<T*>(vpool) + (((size_t)layer * cap + phys) * hkv + h) * (size_t)d * bs;
+            vdst[(size_t)(iv % d) * bs + p % bs] = vreg[k];
+          }
+        }
+      }
+    }
+  }
+  // The last workgroup to arrive publishes the counts and the stack height.
+  if (threadIdx.x == 0) s_flag = arrived + 1 == (int)gridDim.x;
+  __syncthreads();
+  if (s_flag) {
+    for (int e = threadIdx.x; e < B; e += kFusedThreads) nblocks[s_sid[e]] = s_nbnew[e];
+    if (threadIdx.x == 0) {
+      ctr[CTR_ARRIVE] = 0;
+      ctr[CTR_TOP] = top - consumed;
+      ctr[CTR_EXHAUSTED] = fail < B ? fail + 1 : 0;
     }
   }
 }
@@ -594,6 +752,24 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
   if ((C + block_size - 1) / block_size + 1 > 65535) return SPV_ERR_ARG;  // blocks one chunk can touch
   if (B == 0) return SPV_OK;
   hipStream_t s = (hipStream_t)stream;
+  const bool vec16 = (head_dim * es) % 16 == 0;
+  if (may_alloc && !alloc_only && vec16 && B <= kFusedMaxB &&
+      (C + block_size - 1) / block_size + 1 <= kFusedMaxBlocks) {
+    if (!free_stack || !free_flag || !ctr) return SPV_ERR_ARG;
+    auto* kp = static_cast<uint8_t*>(k_pool);
+    auto* vp = static_cast<uint8_t*>(v_pool);
+    auto* kn = static_cast<const uint8_t*>(k_new);
+    auto* vn = static_cast<const uint8_t*>(v_new);
+#define SPV_FUSED(ES)                                                                                           \
+  hipLaunchKernelGGL(kv_append_fused_kernel<ES>, dim3(B * num_kv_heads), dim3(kFusedThreads), 0, s, kp, vp, kn,  \
+                     vn, block_tables, max_blocks_per_seq, num_blocks, seq_lens, free_stack, free_flag, ctr,      \
+                     seq_ids, start_pos, B, C, layer, capacity, block_size, num_kv_heads, head_dim, write_limit_b)
+    if (es == 4) SPV_FUSED(4);
+    else SPV_FUSED(2);
+#undef SPV_FUSED
+    SPV_CHECK_LAUNCH();
+    return SPV_OK;
+  }
   if (may_alloc) {
     if (!free_stack || !free_flag || !ctr) return SPV_ERR_ARG;
     hipLaunchKernelGGL(kv_alloc_kernel, dim3(1), dim3(kPoolThreads), 0, s, block_tables, max_blocks_per_seq,
@@ -607,7 +783,6 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
   auto* vp = static_cast<uint8_t*>(v_pool);
   auto* kn = static_cast<const uint8_t*>(k_new);
   auto* vn = static_cast<const uint8_t*>(v_new);
-  const bool vec16 = (head_dim * es) % 16 == 0;
 #define SPV_WRITE(KER)                                                                                          \
   hipLaunchKernelGGL(KER, grid, blk, 0, s, kp, vp, kn, vn, block_tables, max_blocks_per_seq, num_blocks,       \
                      seq_lens, seq_ids, start_pos, ctr, C, layer, capacity, block_size, num_kv_heads, head_dim, \

@@ -26,6 +26,7 @@ enum : int {
   CTR_SLOWPATH = 2,   // count of rewinds that took the exact sequential path
   CTR_PUSHED = 3,     // blocks actually pushed by the last rewind / free
   CTR_POPPED = 4,     // block id returned by the last single alloc (-1 if exhausted)
+  CTR_ARRIVE = 5,     // arrival count of the one-launch append (zero between launches)
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) {
