@@ -94,6 +94,31 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype,
                   int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
                   int32_t may_alloc, int32_t write_limit_b, void* stream);
 
+/* spv_kv_append for an fp8 (OCP e4m3, SPV_FP8E4M3) pool with one fp32 scale
+ * per (layer, block, K | V): kv_scales is [num_layers][capacity][2] (K, V), a
+ * stored code q meaning q * scale. The reference pool has no fp8 storage
+ * (engine/kv.py:99-101 allocates the model dtype); this entry point keeps
+ * spv_kv_append's allocation, exhaustion, write-limit and length semantics and
+ * replaces the copy by a quantisation. Blocks the allocation hands out get zero
+ * scales in every layer. For each block the chunk writes, separately for K
+ * and V: a = max |x| over the chunk's rows in the block (all heads and dims),
+ * scale' = max(scale, a / 448); if scale' > scale every other row of the block
+ * is re-encoded as e4m3((q * scale) / scale'); the chunk's rows are stored as
+ * e4m3(x / scale') (0 when scale' = 0). e4m3 rounds to nearest even and
+ * saturates at +-448; every product and quotient is a correctly rounded fp32
+ * operation. k_new/v_new are (B, C, Hkv, d) in new_dtype (f32, bf16 or f16);
+ * k_new = v_new = NULL allocates only. */
+int spv_kv_append_fp8(void* k_pool, void* v_pool, float* kv_scales, int new_dtype,
+                      const void* k_new, const void* v_new,
+                      int32_t* block_tables, int32_t max_blocks_per_seq,
+                      int32_t* num_blocks, int32_t* seq_lens,
+                      int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                      const int32_t* seq_ids, const int32_t* start_pos,
+                      int32_t B, int32_t C, int32_t layer, int32_t num_layers,
+                      int32_t capacity, int32_t block_size, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t may_alloc, int32_t write_limit_b,
+                      void* stream);
+
 /* Rewind of a spec round (engine/spec_scheduler.py:302-307, 320-322) built
  * from PagedKVCache.truncate (engine/kv.py:150-162) and .clear (kv.py:164-171),
  * applied per entry in order: if new_len[i] >= 0 (and, with shrink_only, only

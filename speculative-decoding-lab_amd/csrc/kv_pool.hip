@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
     int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
     const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
     const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, int32_t B, int32_t C,
-    int32_t bs) {
+    int32_t bs, float* __restrict__ scales, int32_t num_layers, int32_t cap) {
   __shared__ int s_scan[kPoolThreads / 64];
   __shared__ int s_fail;
   __shared__ int s_free[kAllocStage];  // s_free[i] = free_stack[top - 1 - i]
@@ -101,6 +101,9 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
       const int id = pos < nstage ? s_free[pos] : free_stack[top - 1 - pos];
       tables[(size_t)sid * maxb + nb + i] = id;
       free_flag[id] = 0;
+      if (scales)  // an fp8 pool: the block starts with zero scales in every layer
+        for (int l = 0; l < num_layers; ++l)
+          *reinterpret_cast<float2*>(&scales[((size_t)l * cap + id) * 2]) = make_float2(0.f, 0.f);
     }
     if (b < B && got > 0) nblocks[sid] = nb + got;
     consumed += min(total, max(avail, 0));
@@ -362,6 +365,98 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
       ctr[CTR_EXHAUSTED] = fail < B ? fail + 1 : 0;
     }
   }
+}
+
+// Append into an fp8 (OCP e4m3) pool with one fp32 scale per (layer, block,
+// K | V), shared by the block's kv heads: a stored code q means q * scale.
+// One workgroup per (batch entry, block the chunk touches), after the
+// allocation (which zeroes the scales of the blocks it hands out). For K and
+// for V separately: a = max |x| over the chunk's rows in the block (every head
+// and dim), scale' = max(scale, a / 448); when the scale grows, every other row
+// of the block is re-encoded as e4m3((q * scale) / scale'); the chunk's rows
+// are encoded as e4m3(x / scale') (all codes 0 when scale' is 0). Divisions
+// and products are correctly rounded fp32 operations, in that order.
+constexpr int kFp8Threads = 256;
+
+template <int IT>
+__global__ __launch_bounds__(kFp8Threads) void kv_write_fp8_kernel(
+    uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool, float* __restrict__ scales,
+    const void* __restrict__ knew, const void* __restrict__ vnew, const int32_t* __restrict__ tables, int32_t maxb,
+    const int32_t* __restrict__ nblocks, int32_t* __restrict__ seq_lens, const int32_t* __restrict__ seq_ids,
+    const int32_t* __restrict__ start, const int32_t* __restrict__ ctr, int32_t C, int32_t layer, int32_t cap,
+    int32_t bs, int32_t hkv, int32_t d, int32_t limit_b) {
+  __shared__ float s_red[2][kFp8Threads / 64];
+  __shared__ float s_scale[4];  // old K, old V, new K, new V
+  const int b = blockIdx.x;
+  const int sid = seq_ids[b], s0 = start[b];
+  if (limit_b < 0) {
+    const int ex = ctr[CTR_EXHAUSTED];
+    limit_b = ex ? ex - 1 : 0x7fffffff;
+  }
+  if (b > limit_b || s0 < 0) return;
+  const int n = min(C, nblocks[sid] * bs - s0);
+  if (n <= 0) return;
+  const int blk = s0 / bs + (int)blockIdx.y;
+  if (blk > (s0 + n - 1) / bs) return;
+  const int phys = tables[(size_t)sid * maxb + blk];
+  if ((unsigned)phys >= (unsigned)cap) return;  // never write outside the pool
+  if (blockIdx.y == 0 && threadIdx.x == 0 && seq_lens[sid] < s0 + n) seq_lens[sid] = s0 + n;
+  const int lo = max(s0, blk * bs) - blk * bs, hi = min(s0 + n, (blk + 1) * bs) - blk * bs;
+  const int rows = hi - lo, per_row = hkv * d;
+  const size_t src0 = ((size_t)b * C + (blk * bs + lo - s0)) * per_row;  // the block's first new row
+  float ak = 0.f, av = 0.f;
+  for (int i = threadIdx.x; i < rows * per_row; i += kFp8Threads) {
+    ak = fmaxf(ak, fabsf(load_elem<IT>(knew, src0 + i)));
+    av = fmaxf(av, fabsf(load_elem<IT>(vnew, src0 + i)));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ak = fmaxf(ak, __shfl_xor(ak, o, 64));
+    av = fmaxf(av, __shfl_xor(av, o, 64));
+  }
+  const size_t sidx = ((size_t)layer * cap + phys) * 2;
+  if ((threadIdx.x & 63) == 0) {
+    s_red[0][threadIdx.x >> 6] = ak;
+    s_red[1][threadIdx.x >> 6] = av;
+  }
+  if (threadIdx.x == 0) {
+    s_scale[0] = scales[sidx];
+    s_scale[1] = scales[sidx + 1];
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    float a = 0.f;
+    for (int w = 0; w < kFp8Threads / 64; ++w) a = fmaxf(a, s_red[threadIdx.x][w]);
+    s_scale[2 + threadIdx.x] = fmaxf(s_scale[threadIdx.x], __fdiv_rn(a, 448.f));
+  }
+  __syncthreads();
+  const float old_k = s_scale[0], old_v = s_scale[1], sk = s_scale[2], sv = s_scale[3];
+  const size_t page = ((size_t)layer * cap + phys) * hkv;  // first (block, head) page of the block
+  // Re-encode the other rows of the block under a grown scale. K pages are
+  // [head][row][d], V pages [head][d][row].
+  const int others = (bs - rows) * per_row;
+  if (sk > old_k || sv > old_v) {
+    for (int i = threadIdx.x; i < others; i += kFp8Threads) {
+      int r = i / per_row;
+      const int rem = i - r * per_row, h = rem / d, e = rem - h * d;
+      if (r >= lo) r += rows;  // skip the chunk's rows
+      if (sk > old_k) {
+        uint8_t* q = kpool + ((page + h) * bs + r) * (size_t)d + e;
+        *q = f32_to_fp8e4m3(__fdiv_rn(__fmul_rn(fp8e4m3_to_f32(*q), old_k), sk));
+      }
+      if (sv > old_v) {
+        uint8_t* q = vpool + ((page + h) * d + e) * (size_t)bs + r;
+        *q = f32_to_fp8e4m3(__fdiv_rn(__fmul_rn(fp8e4m3_to_f32(*q), old_v), sv));
+      }
+    }
+  }
+  for (int i = threadIdx.x; i < rows * per_row; i += kFp8Threads) {
+    const int r = lo + i / per_row, rem = i % per_row, h = rem / d, e = rem - h * d;
+    const float xk = load_elem<IT>(knew, src0 + i), xv = load_elem<IT>(vnew, src0 + i);
+    kpool[((page + h) * bs + r) * (size_t)d + e] = sk > 0.f ? f32_to_fp8e4m3(__fdiv_rn(xk, sk)) : 0;
+    vpool[((page + h) * d + e) * (size_t)bs + r] = sv > 0.f ? f32_to_fp8e4m3(__fdiv_rn(xv, sv)) : 0;
+  }
+  if (threadIdx.x == 0) *reinterpret_cast<float2*>(&scales[sidx]) = make_float2(sk, sv);
 }
 
 // K rows whose byte length is not a multiple of 16: element-wise copy (rare
@@ -773,7 +868,8 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
   if (may_alloc) {
     if (!free_stack || !free_flag || !ctr) return SPV_ERR_ARG;
     hipLaunchKernelGGL(kv_alloc_kernel, dim3(1), dim3(kPoolThreads), 0, s, block_tables, max_blocks_per_seq,
-                       num_blocks, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, block_size);
+                       num_blocks, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, block_size, nullptr, 0,
+                       capacity);
     SPV_CHECK_LAUNCH();
   }
   if (alloc_only) return SPV_OK;
@@ -795,6 +891,47 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
     else SPV_WRITE(kv_write_small_kernel<2>);
   }
 #undef SPV_WRITE
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_kv_append_fp8(void* k_pool, void* v_pool, float* kv_scales, int new_dtype, const void* k_new,
+                      const void* v_new, int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks,
+                      int32_t* seq_lens, int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                      const int32_t* seq_ids, const int32_t* start_pos, int32_t B, int32_t C, int32_t layer,
+                      int32_t num_layers, int32_t capacity, int32_t block_size, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t may_alloc, int32_t write_limit_b, void* stream) {
+  const bool alloc_only = !k_new && !v_new;
+  if (!k_pool || !v_pool || !kv_scales || (!alloc_only && (!k_new || !v_new)) || !block_tables || !num_blocks ||
+      !seq_lens || !seq_ids || !start_pos)
+    return SPV_ERR_ARG;
+  if (!alloc_only && new_dtype != SPV_F32 && new_dtype != SPV_BF16 && new_dtype != SPV_F16) return SPV_ERR_ARG;
+  if (B < 0 || C < 1 || layer < 0 || num_layers < 1 || layer >= num_layers || capacity < 1 || block_size < 1 ||
+      num_kv_heads < 1 || head_dim < 1 || max_blocks_per_seq < 1 || write_limit_b < -1 || write_limit_b > B)
+    return SPV_ERR_ARG;
+  if (write_limit_b < 0 && !ctr) return SPV_ERR_ARG;
+  if ((C + block_size - 1) / block_size + 1 > 65535) return SPV_ERR_ARG;
+  if (B == 0) return SPV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (may_alloc) {
+    if (!free_stack || !free_flag || !ctr) return SPV_ERR_ARG;
+    hipLaunchKernelGGL(kv_alloc_kernel, dim3(1), dim3(kPoolThreads), 0, s, block_tables, max_blocks_per_seq,
+                       num_blocks, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, block_size, kv_scales,
+                       num_layers, capacity);
+    SPV_CHECK_LAUNCH();
+  }
+  if (alloc_only) return SPV_OK;
+  const dim3 grid(B, (C + block_size - 1) / block_size + 1), blk(kFp8Threads);
+  auto* kp = static_cast<uint8_t*>(k_pool);
+  auto* vp = static_cast<uint8_t*>(v_pool);
+#define SPV_FP8W(IT)                                                                                         \
+  hipLaunchKernelGGL(kv_write_fp8_kernel<IT>, grid, blk, 0, s, kp, vp, kv_scales, k_new, v_new, block_tables, \
+                     max_blocks_per_seq, num_blocks, seq_lens, seq_ids, start_pos, ctr, C, layer, capacity,   \
+                     block_size, num_kv_heads, head_dim, write_limit_b)
+  if (new_dtype == SPV_F32) SPV_FP8W(SPV_F32);
+  else if (new_dtype == SPV_BF16) SPV_FP8W(SPV_BF16);
+  else SPV_FP8W(SPV_F16);
+#undef SPV_FP8W
   SPV_CHECK_LAUNCH();
   return SPV_OK;
 }

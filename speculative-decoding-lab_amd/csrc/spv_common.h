@@ -58,6 +58,26 @@ __device__ __forceinline__ float fp8e4m3_to_f32(uint8_t v) {
   return s ? -r : r;
 }
 
+// fp32 -> OCP fp8 e4m3, round to nearest even, saturating at +-448 (the
+// largest finite value; no NaN is produced for finite or infinite input).
+// Normal results round the fp32 mantissa to 3 bits (a carry moves into the
+// exponent); below 2^-6 the result is the subnormal m * 2^-9 with m = the
+// even-rounded a * 2^9 (exact scaling), m = 8 being the smallest normal.
+__device__ __forceinline__ uint8_t f32_to_fp8e4m3(float x) {
+  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+  float a = fabsf(x);
+  a = a != a ? 0.f : fminf(a, 448.f);  // NaN input (never produced here) is stored as 0
+  uint32_t code;
+  if (a < 0.015625f) {
+    code = static_cast<uint32_t>(__builtin_rintf(a * 512.f));  // 0 .. 8
+  } else {
+    const uint32_t u = __float_as_uint(a);
+    const uint32_t r = u + 0x7ffffu + ((u >> 20) & 1u);  // round to 3 mantissa bits, ties to even
+    code = ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+  }
+  return static_cast<uint8_t>(sign | code);
+}
+
 template <int DT>
 __device__ __forceinline__ float load_elem(const void* base, size_t i) {
   if constexpr (DT == SPV_F32) return static_cast<const float*>(base)[i];

@@ -37,9 +37,10 @@ def _expand_to_q_heads(kv: torch.Tensor, num_q_heads: int) -> torch.Tensor:
 
 
 def gather_ctx(kv: PagedKVCache, layer: int, seq_id: int, length: int) -> torch.Tensor:
-    """The stored K/V prefix of one sequence, ``(2, length, kv_heads, d)`` (K row 0, V row 1)."""
+    """The stored K/V prefix of one sequence, ``(2, length, kv_heads, d)`` (K row 0, V row 1);
+    an fp8 pool's is dequantised to float32 (code * scale of its block)."""
     length = int(length)
-    out_dtype = kv.dtype
+    out_dtype = torch.float32 if kv.fp8 else kv.dtype
     out = torch.empty((2, max(length, 0), kv.num_kv_heads, kv.head_dim), dtype=out_dtype,
                       device=kv.device)
     if length <= 0:
@@ -48,7 +49,7 @@ def gather_ctx(kv: PagedKVCache, layer: int, seq_id: int, length: int) -> torch.
     kv._refresh()
     if -(-length // kv.block_size) > kv._nb[seq_id]:
         raise IndexError("length {} exceeds the blocks of sequence {}".format(length, seq_id))
-    call("spv_kv_gather", ptr(kv.k_pool), ptr(kv.v_pool), kv._dt, None, ptr(kv.tables_dev),
+    call("spv_kv_gather", ptr(kv.k_pool), ptr(kv.v_pool), kv._dt, ptr(kv.scales), ptr(kv.tables_dev),
          kv.max_blocks_per_seq, seq_id, length, int(layer), kv.allocator.capacity, kv.block_size,
          kv.num_kv_heads, kv.head_dim, ptr(out), _hip.stream_of(kv.device))
     return out
@@ -82,7 +83,7 @@ def verify_attention(query_3d: torch.Tensor, kv: PagedKVCache, layer: int,
                                                           kv.block_size, int(max_ctx))
     ws = _workspace.get(ws_bytes, kv.device) if ws_bytes else None
     call("spv_verify_attn", ptr(out), ptr(q), _hip.dtype_code(q.dtype), ptr(kv.k_pool), ptr(kv.v_pool),
-         kv._dt, None, ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t), B, chunk,
+         kv._dt, ptr(kv.scales), ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t), B, chunk,
          hq, kv.num_kv_heads, d, kv.block_size, int(layer), kv.allocator.capacity, int(max_ctx),
          scale, ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
     return out

@@ -156,10 +156,18 @@ class PagedKVCache:
         self._dt = _hip.dtype_code(dtype)
         self.allocator = BlockAllocator(capacity_blocks, device, dtype)
         cap = self.allocator.capacity
+        self.fp8 = self._dt == _hip.SPV_FP8E4M3
+        # fp8 pools hold e4m3 codes (zero bytes at start) and one fp32 scale
+        # per (layer, block, K | V).
+        store = torch.uint8 if self.fp8 else dtype
         self.k_pool = torch.zeros((num_layers, cap, num_kv_heads, block_size, head_dim),
-                                  dtype=dtype, device=device)
+                                  dtype=store, device=device)
         self.v_pool = torch.zeros((num_layers, cap, num_kv_heads, head_dim, block_size),
-                                  dtype=dtype, device=device)
+                                  dtype=store, device=device)
+        if self.fp8:
+            self.k_pool = self.k_pool.view(dtype)
+            self.v_pool = self.v_pool.view(dtype)
+        self.scales = torch.zeros((num_layers, cap, 2), dtype=torch.float32, device=device) if self.fp8 else None
         self._max_seqs = max(1, int(max_seqs))
         self._maxb = int(max_blocks_per_seq) if max_blocks_per_seq else min(cap, 64)
         self.tables_dev = torch.full((self._max_seqs, self._maxb), -1, dtype=torch.int32, device=device)
@@ -287,15 +295,10 @@ class PagedKVCache:
                 raise ValueError("k/v must have shape {}".format(shape))
             if k_new.device != self.device or v_new.device != self.device:
                 raise ValueError("k/v must live on {}".format(self.device))
-            k_new = k_new.to(self.dtype).contiguous()
-            v_new = v_new.to(self.dtype).contiguous()
+            k_new, v_new = self._new_kv(k_new, v_new)
         sid_t = _hip.i32(seq_ids, self.device)
         start_t = _hip.i32(starts, self.device)
-        call("spv_kv_append", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
-             ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
-             ptr(self.allocator.free_stack), ptr(self.allocator.free_flag), ptr(self.allocator.ctr),
-             ptr(sid_t), ptr(start_t), B, chunk, int(layer), self.allocator.capacity, bs,
-             self.num_kv_heads, self.head_dim, 1 if sum(grants) else 0, fail, self._stream())
+        self._launch_append(layer, sid_t, start_t, k_new, v_new, B, chunk, 1 if sum(grants) else 0, fail)
         # Mirrors: allocation, then the lengths the (possibly truncated) writes reach.
         for b, sid in enumerate(seq_ids):
             self._nb[sid] += grants[b]
@@ -323,13 +326,34 @@ class PagedKVCache:
         B, chunk = int(k_new.shape[0]), int(k_new.shape[1])
         if B == 0:
             return
-        call("spv_kv_append", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
-             ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
-             ptr(self.allocator.free_stack), ptr(self.allocator.free_flag), ptr(self.allocator.ctr),
-             ptr(seq_ids), ptr(start_positions), B, chunk, int(layer), self.allocator.capacity,
-             self.block_size, self.num_kv_heads, self.head_dim, 1 if alloc else 0, -1, self._stream())
+        k_new, v_new = self._new_kv(k_new, v_new)
+        self._launch_append(layer, seq_ids, start_positions, k_new, v_new, B, chunk, 1 if alloc else 0, -1)
         self._stale = True
         self.allocator._stale = True
+
+    def _new_kv(self, k_new: torch.Tensor, v_new: torch.Tensor):
+        """New keys / values as the append takes them: the pool dtype, or for an
+        fp8 pool the caller's f32 / bf16 / f16 (quantised on the device)."""
+        if self.fp8:
+            if k_new.dtype not in (torch.float32, torch.bfloat16, torch.float16) or v_new.dtype != k_new.dtype:
+                raise ValueError("an fp8 pool takes new keys / values in float32, bfloat16 or float16")
+            return k_new.contiguous(), v_new.contiguous()
+        return k_new.to(self.dtype).contiguous(), v_new.to(self.dtype).contiguous()
+
+    def _launch_append(self, layer, sid_t, start_t, k_new, v_new, B, chunk, may_alloc, limit) -> None:
+        a = self.allocator
+        if self.fp8:
+            new_dt = _hip.dtype_code(k_new.dtype) if k_new is not None else 0
+            call("spv_kv_append_fp8", ptr(self.k_pool), ptr(self.v_pool), ptr(self.scales), new_dt, ptr(k_new),
+                 ptr(v_new), ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
+                 ptr(a.free_stack), ptr(a.free_flag), ptr(a.ctr), ptr(sid_t), ptr(start_t), B, chunk, int(layer),
+                 self.num_layers, a.capacity, self.block_size, self.num_kv_heads, self.head_dim, may_alloc, limit,
+                 self._stream())
+            return
+        call("spv_kv_append", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
+             ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
+             ptr(a.free_stack), ptr(a.free_flag), ptr(a.ctr), ptr(sid_t), ptr(start_t), B, chunk, int(layer),
+             a.capacity, self.block_size, self.num_kv_heads, self.head_dim, may_alloc, limit, self._stream())
 
     def _ensure_blocks_up_to(self, seq_id: int, max_block_index: int) -> None:
         """Lazily extend a table to cover ``max_block_index`` (kv.py:119-122)."""
@@ -453,7 +477,8 @@ class PagedKVCache:
 
     @property
     def kv_memory_bytes(self) -> int:
-        return 2 * self.k_pool.numel() * self.k_pool.element_size()
+        scales = 0 if self.scales is None else self.scales.numel() * 4
+        return 2 * self.k_pool.numel() * self.k_pool.element_size() + scales
 
     # ------------------------------------------------------ read (for attention)
     def _read_blocks(self, layer: int, phys: List[int], is_value: int) -> torch.Tensor:

@@ -32,7 +32,7 @@ def lib():
 def test_header_declares_the_path_entry_points():
     names = set(_declared())
     for need in ("spv_kv_append", "spv_kv_rewind", "spv_verify_attn", "spv_verify_sample",
-                 "spv_pool_alloc_one", "spv_pool_free_one", "spv_kv_gather"):
+                 "spv_pool_alloc_one", "spv_pool_free_one", "spv_kv_gather", "spv_kv_append_fp8"):
         assert need in names
 
 
@@ -59,6 +59,15 @@ def test_argument_validation_needs_no_gpu(lib):
     assert lib.spv_verify_sample(None, None, 0, 1.0, None, None, None, None, None, -1, 1, 5, 8,
                                  None, None, None, None, None, None, 0, None, 0, None) == ARG
     assert lib.spv_race_argmax(None, None, 8, None, None) == ARG
+    # fp8 append: no scales, then an input dtype the quantiser does not take
+    assert lib.spv_kv_append_fp8(None, None, None, 0, None, None, None, 4, None, None, None, None, None,
+                                 None, None, 1, 1, 0, 1, 8, 16, 2, 8, 1, 1, None) == ARG
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    assert lib.spv_kv_append_fp8(p, p, p, 3, p, p, p, 4, p, p, p, p, p, p, p, 1, 1, 0, 1, 8, 16, 2, 8, 1,
+                                 1, None) == ARG
+    assert lib.spv_kv_append_fp8(p, p, p, 0, p, p, p, 4, p, p, p, p, p, p, p, 1, 1, 2, 2, 8, 16, 2, 8, 1,
+                                 1, None) == ARG  # layer beyond num_layers
 
 
 def test_workspace_queries(lib):
