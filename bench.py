@@ -378,6 +378,70 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
     return out
 
 
+# Long context: Qwen2.5-0.5B-shaped heads, fp8 (e4m3) KV with per-block scales.
+LC_B, LC_HQ, LC_HKV, LC_D, LC_GAMMA, LC_CTX, LC_REPLICAS = 16, 14, 2, 64, 8, 32768, 4
+
+
+def long_context(dev, seed=0):
+    """Verify attention over 32768-token contexts (16 sequences, 14q/2kv heads,
+    head_dim 64, gamma 8 -> 9 rows) on an fp8 pool and on a bf16 pool of the
+    same contexts, and the fp8 append of the 9 verify tokens. Four layers of
+    K/V (N(0,1), quantised by the fp8 append) serve as replicas that the timed
+    calls cycle over, so no call finds its pages in the last-level cache."""
+    import torch
+
+    from engine.attention import verify_attention
+    from engine.kv import PagedKVCache
+
+    chunk = LC_GAMMA + 1
+    lens = [LC_CTX] * LC_B
+    blocks = LC_B * (-(-(LC_CTX + chunk) // BS))
+    g = torch.Generator(device=dev).manual_seed(seed)
+    out = {"workload": "Qwen2.5-0.5B-shaped long-context verify: batch {}, ctx {}, gamma {} ({} rows), "
+                       "{}q/{}kv heads, head_dim {}, block {}; fp8 e4m3 KV with one fp32 scale per (layer, "
+                       "block, K|V), and the same contexts in bf16; calls cycle over {} layers".format(
+                           LC_B, LC_CTX, LC_GAMMA, chunk, LC_HQ, LC_HKV, LC_D, BS, LC_REPLICAS)}
+    q = torch.randn(LC_B, chunk, LC_HQ, LC_D, generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn(LC_B, chunk, LC_HKV, LC_D, generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn(LC_B, chunk, LC_HKV, LC_D, generator=g, device=dev).to(torch.bfloat16)
+    sid = torch.arange(LC_B, dtype=torch.int32, device=dev)
+    st = torch.tensor(lens, dtype=torch.int32, device=dev)
+    reps = 3 * LC_REPLICAS
+    for name, dtype in (("fp8", torch.float8_e4m3fn), ("bf16", torch.bfloat16)):
+        kv = PagedKVCache(LC_REPLICAS, LC_HKV, LC_D, blocks + LC_B, BS, dev, dtype, max_seqs=LC_B,
+                          max_blocks_per_seq=-(-(LC_CTX + chunk) // BS) + 1)
+        for s in range(LC_B):
+            kv.add_sequence(s)
+        for layer in range(LC_REPLICAS):
+            for s in range(LC_B):
+                k = torch.randn(1, LC_CTX, LC_HKV, LC_D, generator=g, device=dev).to(torch.bfloat16)
+                v = torch.randn(1, LC_CTX, LC_HKV, LC_D, generator=g, device=dev).to(torch.bfloat16)
+                kv.write_block(layer, [s], [0], k, v)
+        for layer in range(LC_REPLICAS):  # the verify chunk, written before it is attended
+            kv.write_block(layer, list(range(LC_B)), lens, kn, vn)
+        o = torch.empty_like(q)
+        attend = lambda i: verify_attention(q, kv, i % LC_REPLICAS, sid, st, LC_CTX + chunk, out=o)
+        for i in range(LC_REPLICAS):
+            attend(i)
+        torch.cuda.synchronize()
+        gr = graph_of(lambda: [attend(i) for i in range(reps)], 1, torch)
+        us = time_graph(gr, 5, torch) * 1000.0 / reps
+        kv_bytes = 1 if name == "fp8" else 2
+        nbytes = sum((L + chunk) * 2 * LC_HKV * LC_D * kv_bytes + 2 * chunk * LC_HQ * LC_D * 2
+                     + (4 + (8 if name == "fp8" else 0)) * math.ceil((L + chunk) / BS) + 8 for L in lens)
+        out[name + "_attn_us"] = round(us, 2)
+        out[name + "_attn_gbs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+        out[name + "_attn_bytes_per_call"] = nbytes
+        if name == "fp8":
+            # append of the verify chunk into the fp8 pool (blocks exist: quantise only)
+            ap = lambda i: kv.write_block_device(i % LC_REPLICAS, sid, st, kn, vn, alloc=False)
+            ga = graph_of(lambda: [ap(i) for i in range(reps)], 1, torch)
+            out["fp8_append_us"] = round(time_graph(ga, 5, torch) * 1000.0 / reps, 2)
+        del kv, gr
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -387,6 +451,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--full-depth-rounds", type=int, default=24,
                     help="rounds of the 36-layer continuous-batching measurement (0 skips it)")
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip the 32768-token fp8 / bf16 verify-attention measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -486,6 +552,13 @@ def main() -> int:
         torch.cuda.empty_cache()
         print("bench: full-depth continuous batching", file=sys.stderr, flush=True)
         line["full_depth"] = full_depth(dev, args.full_depth_rounds, 4, args.seed)
+    if not args.no_long_context:
+        if args.full_depth_rounds <= 0:
+            del g_step, g_att, g_smp, g_ar, step, parts, res, w
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+        print("bench: long-context fp8 / bf16 attention", file=sys.stderr, flush=True)
+        line["long_context"] = long_context(dev, args.seed)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -163,6 +163,9 @@ __device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ u32x2_t load_b64(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, 0);
 }
+__device__ __forceinline__ uint32_t load_b32(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t uniform_off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)lane_off, (int)uniform_off, 0);
+}
 // Lane offset plus a uniform offset (scalar operand, no lane register per constant).
 __device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t uniform_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)lane_off, (int)uniform_off, 0);

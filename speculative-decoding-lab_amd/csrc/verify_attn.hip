@@ -230,10 +230,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_valu_kernel(AttnParams p) {
 // counters are zero between calls.
 constexpr int kMfmaWGsMax = 512;  // bound on the persistent grid (slot numbering)
 constexpr int kMfmaMaxB = 512;    // the page and piece prefixes of the batch live in LDS
-// Register page buffers per wave: one page in flight while one is computed.
-// One workgroup of eight waves per CU (two per SIMD, <= 256 registers each, so
-// every operand stays in VGPRs) keeps eight pages in flight per CU.
-__host__ __device__ constexpr int ring_depth(int, int) { return 2; }
+// Register page buffers per wave: one page in flight while one is computed
+// (bf16). One workgroup of eight waves per CU (two per SIMD, <= 256 registers
+// each, so every operand stays in VGPRs) keeps eight pages in flight per CU.
+// fp8 pages take half the registers (8 for head_dim 64) and keep three in
+// flight per wave.
+__host__ __device__ constexpr int ring_depth(int, int, int kt) { return kt == SPV_FP8E4M3 ? 4 : 2; }
 constexpr int kMfmaThreads = 512;
 // O^T tiles combined per LDS round: as many as fit beside the other buffers
 // (the slots take 8 waves x 16 * nt rows x 64 B per tile).
@@ -398,12 +400,43 @@ __device__ __forceinline__ int share_of_block(int bid, int nw) {
   return (nw & 7) ? bid : (bid & 7) * (nw >> 3) + (bid >> 3);
 }
 
-// One page as a wave holds it: the K rows for S^T and the V^T tiles for O^T.
+// One page as a wave holds it: the K rows for S^T and the V^T tiles for O^T
+// (bf16, or fp8 e4m3 codes with the block's two scales).
+template <int D, int KT>
+struct PageRegs;
 template <int D>
-struct PageRegs {
+struct PageRegs<D, SPV_BF16> {
   uint4 k[D / 32];  // key i16, dims 32 ks + 8 g .. + 7
   uint2 v[D / 16];  // dim 16 mt + i16, keys 4 g .. 4 g + 3
 };
+template <int D>
+struct PageRegs<D, SPV_FP8E4M3> {
+  uint2 k[D / 32];     // key i16, dims 32 ks + 8 g .. + 7 (codes)
+  uint32_t v[D / 16];  // dim 16 mt + i16, keys 4 g .. 4 g + 3 (codes)
+  float sk, sv;        // the block's K and V scales
+};
+
+// e4m3 codes -> bf16, exactly (every e4m3 value is a bf16 value): the gfx950
+// conversion with scale 1.
+template <bool HI>  // bytes 2, 3 of w (else 0, 1)
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, HI));
+}
+
+// The MFMA operands of a page: K rows as bf16x8, V^T columns as 4 bf16.
+template <int D>
+__device__ __forceinline__ uint4 k_frag(const PageRegs<D, SPV_BF16>& f, int ks) { return f.k[ks]; }
+template <int D>
+__device__ __forceinline__ uint4 k_frag(const PageRegs<D, SPV_FP8E4M3>& f, int ks) {
+  return make_uint4(fp8x2_to_bf16x2<false>(f.k[ks].x), fp8x2_to_bf16x2<true>(f.k[ks].x),
+                    fp8x2_to_bf16x2<false>(f.k[ks].y), fp8x2_to_bf16x2<true>(f.k[ks].y));
+}
+template <int D>
+__device__ __forceinline__ uint2 v_frag(const PageRegs<D, SPV_BF16>& f, int mt) { return f.v[mt]; }
+template <int D>
+__device__ __forceinline__ uint2 v_frag(const PageRegs<D, SPV_FP8E4M3>& f, int mt) {
+  return make_uint2(fp8x2_to_bf16x2<false>(f.v[mt]), fp8x2_to_bf16x2<true>(f.v[mt]));
+}
 
 // Merge of one segment's partial slots slot_of(0 .. ns - 1) (rows qr0 .. qr0 +
 // nr - 1) into the output. Each thread takes (row, 4 dims) items and issues every
@@ -475,8 +508,9 @@ __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b
   }
 }
 
-template <int NT, int D, int QT, bool BAL>
+template <int NT, int D, int QT, bool BAL, int KT>
 __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p) {
+  constexpr bool kFp8 = KT == SPV_FP8E4M3;
   constexpr int KS = D / 32;  // 32-dim k-steps of S^T
   constexpr int MT = D / 16;  // 16-dim tiles of O^T
   constexpr int BS = 16;
@@ -523,6 +557,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   const long long x_end = balanced ? page_start(wg + 1) : div_floor((long long)(wg + 1) * N, nw);
   const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
   const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
+  const uint8_t* kbase8 = static_cast<const uint8_t*>(p.kpool);
+  const uint8_t* vbase8 = static_cast<const uint8_t*>(p.vpool);
   const uint16_t* qbase = static_cast<const uint16_t*>(p.q);
   const float sl2 = p.scale_log2;
 
@@ -603,11 +639,22 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // for K and one for V (the k-step and tile offsets are scalar operands), so
     // no 64-bit lane address lives across the walk to be spilled and reloaded.
     const uint32_t koff = (uint32_t)(i16 * D + 8 * g) * 2u, voff = (uint32_t)(i16 * BS + 4 * g) * 2u;
-    auto load_page = [&](PageRegs<D>& f, int page) {
+    auto load_page = [&](PageRegs<D, KT>& f, int page) {
       const int phys = uni(sTab[page - tab0]);
       const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
-      const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase + slot, BS * D * 2), rv = span_rsrc(vbase + slot, BS * D * 2);
-      if constexpr (NT >= 4) {
+      if constexpr (kFp8) {
+        // codes: one byte per element; K lane: 8 dims, V lane: 4 keys
+        const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase8 + slot, BS * D), rv = span_rsrc(vbase8 + slot, BS * D);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint2, load_b64(rk, koff / 2, 32u * ks));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) f.v[mt] = load_b32(rv, voff / 2, 16u * BS * mt);
+        const float2 sc = *reinterpret_cast<const float2*>(p.scales + ((size_t)p.layer * p.cap + phys) * 2);
+        f.sk = sc.x;
+        f.sv = sc.y;
+      } else if constexpr (NT >= 4) {
+        const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase + slot, BS * D * 2);
+        const __amdgpu_buffer_rsrc_t rv = span_rsrc(vbase + slot, BS * D * 2);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint4, load_b128(rk, koff, 64u * ks));
 #pragma unroll
@@ -622,19 +669,36 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       }
     };
 
-    auto compute_page = [&](PageRegs<D>& f, int page) {
+    auto compute_page = [&](PageRegs<D, KT>& f, int page) {
       const int kpos0 = page * BS + 4 * g;  // key position of accumulator element 0
+      // V^T as bf16: the page registers themselves, or an fp8 page's conversion.
+      uint2 vb8[kFp8 ? MT : 1];
+      auto vfrag = [&](int mt) -> uint2& {
+        if constexpr (kFp8) return vb8[mt];
+        else return f.v[mt];
+      };
+      if constexpr (kFp8) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) vb8[mt] = v_frag<D>(f, mt);
+      }
       if (page * BS + BS > L) {
         // Keys at or beyond L are stale pool contents: zero their V.
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          uint32_t lo = f.v[mt].x, hi = f.v[mt].y;
+          uint32_t lo = vfrag(mt).x, hi = vfrag(mt).y;
           if (kpos0 + 0 >= L) lo &= 0xffff0000u;
           if (kpos0 + 1 >= L) lo &= 0x0000ffffu;
           if (kpos0 + 2 >= L) hi &= 0xffff0000u;
           if (kpos0 + 3 >= L) hi &= 0x0000ffffu;
-          f.v[mt] = make_uint2(lo, hi);
+          vfrag(mt) = make_uint2(lo, hi);
         }
+      }
+      // An fp8 page's K scale multiplies its scores, its V scale the P that
+      // meets its V (the row sums take P itself).
+      float spage = sl2, vscale = 1.f;
+      if constexpr (kFp8) {
+        spage = sl2 * f.sk;
+        vscale = f.sv;
       }
       // The query fragments (B operand: row 16 nt + i16, dims 32 ks + 8 g .. + 7)
       // are re-read from LDS for every page instead of being hoisted into
@@ -648,7 +712,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const uint4 qv = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
-          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, f.k[ks]),
+          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k_frag<D>(f, ks)),
                                                            __builtin_bit_cast(bf16x8_t, qv), sc[nt], 0, 0, 0);
         }
       const bool need_mask = page * BS + BS - 1 > start;
@@ -658,7 +722,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          x[nt][jj] = sc[nt][jj] * sl2;
+          x[nt][jj] = sc[nt][jj] * spage;
           if (need_mask && kpos0 + jj > start + jrow[nt]) x[nt][jj] = -INFINITY;
           grow |= x[nt][jj] > m[nt] + kSlack;
         }
@@ -690,6 +754,10 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(x4[jj] - mu);
         l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
+        if constexpr (kFp8) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) e[jj] *= vscale;
+        }
         // P = hi + lo, both bf16: slots 0..3 carry hi, 4..7 lo of the same keys,
         // so one 16x16x32 MFMA against {V, V} accumulates P V to ~16 bits.
         const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
@@ -703,7 +771,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         // {V^T, V^T}: the same keys in both halves of the k-slots.
-        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(f.v[mt].x, f.v[mt].y, f.v[mt].x, f.v[mt].y));
+        const uint2 vv = vfrag(mt);
+        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(vv.x, vv.y, vv.x, vv.y));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[nt], o[mt][nt], 0, 0, 0);
       }
@@ -711,8 +780,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
 
     // Wave w takes pages tab0 + w, tab0 + w + NWV, ...; kRing rotating
     // register buffers keep kRing - 1 pages in flight while one is computed.
-    constexpr int kRing = ring_depth(NT, D);
-    PageRegs<D> buf[kRing];
+    constexpr int kRing = ring_depth(NT, D, KT);
+    PageRegs<D, KT> buf[kRing];
     for (; tab0 < lp1; tab0 += kTabChunk) {
       const int wend = min(lp1, tab0 + kTabChunk);
       if (tab0 != lp0) {
@@ -911,7 +980,8 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
   // offsets (bytes for the partials).
   const bool fits32 = (long long)B * C * Hq * d < (1LL << 31) &&
                       2LL * kMfmaWGsMax * G * d * (long long)sizeof(float) < (1LL << 31);
-  pl.mfma = kv_dtype == SPV_BF16 && q_dtype == SPV_BF16 && bs == 16 && (d == 128 || d == 64) && G >= 16 &&
+  pl.mfma = (kv_dtype == SPV_BF16 || kv_dtype == SPV_FP8E4M3) && q_dtype == SPV_BF16 && bs == 16 &&
+            (d == 128 || d == 64) && G >= 16 &&
             B <= kMfmaMaxB && fits32;
   const int max_pages = (max_ctx + bs - 1) / bs;
   if (pl.mfma) {
@@ -983,26 +1053,26 @@ int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s) {
   return SPV_OK;
 }
 
-template <int D, bool BAL>
+template <int D, bool BAL, int KT>
 void launch_mfma_mode(const AttnParams& p, int nt, hipStream_t s, dim3 grid, size_t smem) {
   const dim3 blk(kMfmaThreads);
   switch (nt) {
-    case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_mfma_kernel<3, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
-    default: hipLaunchKernelGGL((attn_mfma_kernel<4, D, SPV_BF16, BAL>), grid, blk, smem, s, p); break;
+    case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
+    case 3: hipLaunchKernelGGL((attn_mfma_kernel<3, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
+    default: hipLaunchKernelGGL((attn_mfma_kernel<4, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
   }
 }
 
 // Equal pieces when the workgroups outnumber the (sequence, kv head, row
 // group) segments, else the page-balanced split.
-template <int D>
+template <int D, int KT>
 void launch_mfma(const AttnParams& p, int nt, hipStream_t s) {
   const size_t smem = (size_t)4 * (p.B + 1) * sizeof(int);  // page / piece prefixes, ids, starts
   const int nw = persistent_wgs();
   const bool balanced = (long long)p.Hkv * p.nrg * p.B >= nw;
-  if (balanced) launch_mfma_mode<D, true>(p, nt, s, dim3(nw), smem);
-  else launch_mfma_mode<D, false>(p, nt, s, dim3(nw), smem);
+  if (balanced) launch_mfma_mode<D, true, KT>(p, nt, s, dim3(nw), smem);
+  else launch_mfma_mode<D, false, KT>(p, nt, s, dim3(nw), smem);
 }
 
 }  // namespace
@@ -1074,8 +1144,9 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
   }
   hipStream_t s = (hipStream_t)stream;
   if (pl.mfma) {
-    if (head_dim == 128) launch_mfma<128>(p, pl.nt, s);
-    else launch_mfma<64>(p, pl.nt, s);
+    const bool fp8 = kv_dtype == SPV_FP8E4M3;
+    if (head_dim == 128) fp8 ? launch_mfma<128, SPV_FP8E4M3>(p, pl.nt, s) : launch_mfma<128, SPV_BF16>(p, pl.nt, s);
+    else fp8 ? launch_mfma<64, SPV_FP8E4M3>(p, pl.nt, s) : launch_mfma<64, SPV_BF16>(p, pl.nt, s);
     SPV_CHECK_LAUNCH();
     return SPV_OK;
   }

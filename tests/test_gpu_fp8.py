@@ -177,3 +177,39 @@ def test_fp8_attention_matches_oracle_on_dequantized_kv(cuda, qdtype):
         got = gather_ctx(gpu, 0, s, L + C).cpu()
         want_ctx = ref_attn.gather_ctx(cpu.dequantized(), 0, s, L + C)
         assert torch.equal(got, want_ctx)
+
+
+def _fp8_pool_with(cuda, lens, H, d, bs, C, seed):
+    cap = sum(-(-(L + C) // bs) for L in lens) + 4
+    gpu = PagedKVCache(1, H, d, cap, bs, cuda, FP8, max_seqs=len(lens))
+    cpu = Fp8PagedKVCache(1, H, d, cap, bs)
+    g = torch.Generator().manual_seed(seed)
+    for s, L in enumerate(lens):
+        gpu.add_sequence(s)
+        cpu.add_sequence(s)
+        k = torch.randn(1, L, H, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, L, H, d, generator=g).to(torch.bfloat16)
+        gpu.write_block(0, [s], [0], k.to(cuda), v.to(cuda))
+        cpu.write_block(0, [s], [0], k, v)
+    sids = list(range(len(lens)))
+    kn = torch.randn(len(lens), C, H, d, generator=g).to(torch.bfloat16)
+    vn = torch.randn(len(lens), C, H, d, generator=g).to(torch.bfloat16)
+    gpu.write_block(0, sids, lens, kn.to(cuda), vn.to(cuda))
+    cpu.write_block(0, sids, lens, kn, vn)
+    return gpu, cpu, g
+
+
+@pytest.mark.parametrize("Hq,H,d,C,lens", [
+    (14, 2, 64, 9, [2000, 37, 700, 1, 129, 1500]),     # head_dim 64, pieces split across workgroups
+    (12, 2, 128, 6, [3000, 256, 1, 999, 4000, 17]),    # head_dim 128
+    (12, 2, 128, 6, [(i * 37) % 211 + 1 for i in range(140)]),  # segments outnumber workgroups
+])
+def test_fp8_mfma_attention_matches_oracle(cuda, Hq, H, d, C, lens):
+    """bf16 queries over an fp8 pool take the MFMA path: codes converted to
+    bf16 in registers, the K scale on the scores and the V scale on P."""
+    gpu, cpu, g = _fp8_pool_with(cuda, lens, H, d, 16, C, 9)
+    q = torch.randn(len(lens), C, Hq, d, generator=g).to(torch.bfloat16)
+    sids = list(range(len(lens)))
+    out = verify_attention(q.to(cuda), gpu, 0, sids, lens, max(lens) + C).float().cpu()
+    want = ref_attn.paged_attention_extend(q.float(), cpu.dequantized(), 0, sids, lens, Hq)
+    _bf16_check(out, want)
