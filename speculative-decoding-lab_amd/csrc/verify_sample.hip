@@ -13,9 +13,9 @@
 //
 // Kernels (HBM-bound; every logits row is read once by the stats pass, the one
 // raced row pair and its noise row once more by the race pass):
-//   1. row_stats  grid (chunks, B * rows): per 8192-entry chunk max & sum exp (or
-//                 argmax); the last workgroup of each sequence combines the
-//                 chunks, gathers p[x], q[x] and decides k (greedy: also commits)
+//   1. row_stats  grid (B * rows), one workgroup per logits row: the row's max
+//                 and sum exp (or argmax); the last workgroup of each sequence
+//                 gathers p[x], q[x] and decides k (greedy: also commits)
 //   1'. decide    grid (B): the decision alone, for probability inputs
 //   2. race       grid (chunks, B): residual sum and the top-2 of r/E per chunk;
 //                 the last workgroup of each sequence makes the draw and the
