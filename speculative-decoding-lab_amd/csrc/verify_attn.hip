@@ -236,6 +236,11 @@ constexpr int kMfmaMaxB = 512;    // the page and piece prefixes of the batch li
 // fp8 pages take half the registers (8 for head_dim 64) and keep three in
 // flight per wave.
 __host__ __device__ constexpr int ring_depth(int, int, int kt) { return kt == SPV_FP8E4M3 ? 4 : 2; }
+// The fixed cost of a piece (query staging, wave combine, partial and merge)
+// in pages of the walk, for the page-balanced split: 48 pages of 8 KB (bf16,
+// head_dim 128; measured best among 0..128 at batch 128, 16/2 heads, contexts
+// log-uniform in [512, 8192]), scaled to the page size.
+__host__ __device__ constexpr int piece_cost(int d, int kt) { return 48 * 8192 / (16 * d * 2 * (kt == SPV_FP8E4M3 ? 1 : 2)); }
 constexpr int kMfmaThreads = 512;
 // O^T tiles combined per LDS round: as many as fit beside the other buffers
 // (the slots take 8 waves x 16 * nt rows x 64 B per tile).
@@ -337,11 +342,13 @@ __device__ __forceinline__ int ceil_div(int a, int P, float rP) {
 //   s_kpref[b] = pieces of one segment of each sequence before b, s_kpref[B] = total;
 //   s_sid[b], s_start[b] = seq_ids[b], start_pos[b].
 // When the segments alone are at least as many as the workgroups, pieces are
-// not used: the kernel splits the concatenated pages evenly instead, and the
-// search and s_kpref are skipped.
+// not used: the kernel splits the segments' costs evenly instead -- a
+// segment costs its pages plus `piece_cost` pages for the set-up, combine and
+// merge of a piece, so s_pref[b] sums (pages + piece_cost) -- and the search
+// and s_kpref are skipped.
 template <int BS, bool BAL>
 __device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, int* s_sid, int* s_start, long long HR,
-                           int nw) {
+                           int nw, int piece_cost) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const bool one = p.B <= 64;  // the common case keeps every count in a register
@@ -355,8 +362,9 @@ __device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, int* 
         s_sid[b] = p.seq_ids[b];
         np = min((st + p.C + BS - 1) / BS, p.max_pages);
       }
-      const int incl = wave_incl_sum(np);
-      if (b < p.B) s_pref[b] = carry + incl - np;
+      const int wgt = np + (BAL && b < p.B ? piece_cost : 0);
+      const int incl = wave_incl_sum(wgt);
+      if (b < p.B) s_pref[b] = carry + incl - wgt;
       carry += lane63(incl);
       maxnp = max(maxnp, lane63(wave_incl_max(np)));
       np1 = np;
@@ -540,21 +548,38 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   int* s_sid = s_kpref + p.B + 1;
   int* s_start = s_sid + p.B + 1;
   const long long HR = (long long)p.Hkv * p.nrg;
-  build_plan<BS, BAL>(p, s_pref, s_kpref, s_sid, s_start, HR, nw);
+  constexpr int KPC = BAL ? piece_cost(D, KT) : 0;
+  build_plan<BS, BAL>(p, s_pref, s_kpref, s_sid, s_start, HR, nw, KPC);
   if (s_pref[p.B] == 0) return;
-  // Page-balanced mode (segments >= workgroups): workgroup wg takes pages
-  // [A(wg), A(wg + 1)) of the segments laid end to end (sequence-major, then
-  // (kv head, row group)), A(w) = floor(w * T / nw). Whole segments write the
-  // output; a segment cut by these bounds leaves a partial in slot 2 wg (the
-  // workgroup's first piece) or 2 wg + 1 (its last) for each workgroup
-  // w_a .. w_b that holds part of it. Otherwise: equal pieces, one slot each.
+  // Cost-balanced mode (segments >= workgroups): every segment costs KPC
+  // units (its piece overhead) followed by one unit per page; the segments
+  // are laid end to end (sequence-major, then (kv head, row group)) and
+  // workgroup wg takes units [A(wg), A(wg + 1)), A(w) = floor(w * T / nw), i.e.
+  // the pages among them. Whole segments write the output; a segment cut by
+  // these bounds leaves a partial in slot 2 wg (when the workgroup's range
+  // starts at or after the segment's first unit: its first piece) or 2 wg + 1
+  // (its last piece) for each workgroup w_a .. w_b that holds pages of it.
+  // Otherwise: equal pieces, one slot each.
   constexpr bool balanced = BAL;  // chosen by the host: HR * B >= nw
-  const long long T = HR * s_pref[p.B];  // pages of all segments
+  const long long T = HR * s_pref[p.B];  // units of all segments
   auto page_start = [&](long long w) { return div_floor(w * T, nw); };
-  auto owner = [&](long long g) { return (int)div_floor((g + 1) * nw - 1, T); };  // workgroup holding page g
+  auto owner = [&](long long g) { return (int)div_floor((g + 1) * nw - 1, T); };  // workgroup holding unit g
   const long long N = balanced ? 0 : HR * s_kpref[p.B];  // pieces in the batch
   const long long x_begin = balanced ? page_start(wg) : div_floor((long long)wg * N, nw);
   const long long x_end = balanced ? page_start(wg + 1) : div_floor((long long)(wg + 1) * N, nw);
+  // A range that ends among a segment's overhead units (no page of it) stops
+  // at that segment, so every piece of the loop holds pages.
+  long long x_stop = x_end;
+  if constexpr (BAL) {
+    if (x_end > x_begin) {
+      const long long xl = x_end - 1;
+      const int bl = uni(seq_of(s_pref, p.B, HR, xl));
+      const int npwl = uni(s_pref[bl + 1] - s_pref[bl]);
+      const long long locl = xl - HR * s_pref[bl];
+      const long long Gl = HR * s_pref[bl] + (locl / npwl) * npwl;
+      if (xl - Gl < KPC) x_stop = max(x_begin, Gl);
+    }
+  }
   const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
   const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
   const uint8_t* kbase8 = static_cast<const uint8_t*>(p.kpool);
@@ -562,23 +587,25 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   const uint16_t* qbase = static_cast<const uint16_t*>(p.q);
   const float sl2 = p.scale_log2;
 
-  for (long long x = x_begin; x < x_end;) {
+  for (long long x = x_begin; x < x_stop;) {
     // This piece: pages [lp0, lp1) of segment (b, hr); its partial slot, and
     // the number of pieces (arrivals) of its segment.
     int b, hr, lp0, lp1, slot, narr, x0 = 0, w_a = 0;
     long long Gs = 0;
     if constexpr (BAL) {
       b = uni(seq_of(s_pref, p.B, HR, x));
-      const int np = uni(s_pref[b + 1] - s_pref[b]);
+      const int npw = uni(s_pref[b + 1] - s_pref[b]);  // units of a segment: KPC + pages
+      const int np = npw - KPC;
       const int local = (int)(x - HR * s_pref[b]);
-      hr = local / np;
-      lp0 = local - hr * np;
-      lp1 = (int)min((long long)np, lp0 + (x_end - x));
-      Gs = HR * s_pref[b] + (long long)hr * np;
-      w_a = owner(Gs);
-      narr = owner(Gs + np - 1) - w_a + 1;
-      slot = 2 * wg + (x == x_begin ? 0 : 1);
-      x += lp1 - lp0;
+      hr = local / npw;
+      Gs = HR * s_pref[b] + (long long)hr * npw;  // the segment's first unit
+      const long long cend = min(Gs + npw, x_stop);
+      lp0 = max(0, (int)(x - Gs) - KPC);
+      lp1 = (int)(cend - Gs) - KPC;
+      w_a = owner(Gs + KPC);  // the workgroup holding page 0
+      narr = owner(Gs + KPC + np - 1) - w_a + 1;
+      slot = 2 * wg + (page_start(wg) >= Gs ? 0 : 1);
+      x = cend;
     } else {
       b = uni(seq_of(s_kpref, p.B, HR, x));
       const int kb = uni(s_kpref[b + 1] - s_kpref[b]);  // pieces per segment of sequence b

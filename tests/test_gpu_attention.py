@@ -256,3 +256,27 @@ def test_page_balanced_split_when_segments_outnumber_workgroups(cuda, B, C, Hq):
     assert torch.equal(outs[0], outs[1])
     assert int(torch.count_nonzero(A._workspace._buf[: 1 << 18])) == 0
     _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, Hq))
+
+
+@pytest.mark.parametrize("n_short,n_long,d", [(280, 24, 128), (300, 6, 64), (257, 0, 128)])
+def test_balanced_split_with_piece_costs(cuda, n_short, n_long, d):
+    """Cost-balanced split with many one- and two-page segments beside long
+    ones: workgroups hold several whole segments, ranges end among a segment's
+    overhead units (that segment starts in the next workgroup), and long
+    segments are cut over several workgroups."""
+    import engine.attention as A
+
+    Hq, Hkv, C = 12, 2, 6
+    g = torch.Generator().manual_seed(n_short + n_long)
+    lens = [int(x) for x in torch.randint(1, 27, (n_short,), generator=g)]
+    lens += [int(x) for x in torch.randint(600, 3000, (n_long,), generator=g)]
+    order = torch.randperm(len(lens), generator=g).tolist()
+    lens = [lens[i] for i in order]
+    B = len(lens)
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.bfloat16, seed=B + d)
+    q = torch.randn(B, C, Hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    outs = [verify_attention(q, gpu, 0, list(range(B)), lens, max(lens) + C).clone() for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert int(torch.count_nonzero(A._workspace._buf[: 1 << 18])) == 0
+    _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, Hq))
