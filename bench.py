@@ -442,6 +442,63 @@ def long_context(dev, seed=0):
     return out
 
 
+def draft_decode(dev, seed=0):
+    """One draft decode step's paged work per layer at a Qwen2.5-0.5B-shaped
+    draft (14q/2kv heads, head_dim 64, bf16): append the one new token of
+    each sequence, then decode attention (one query row) over its context.
+    Batch 32 with the verify workload's context lengths; calls cycle over 8
+    replicas on disjoint pages."""
+    import torch
+
+    from engine.attention import verify_attention
+    from engine.kv import PagedKVCache
+
+    hq, hkv, d, reps = 14, 2, 64, 8
+    lens, g = workload_lens(seed)
+    need = [-(-(L + 1) // BS) for L in lens]
+    cap = sum(need) * reps + 64
+    kv = PagedKVCache(1, hkv, d, cap, BS, dev, torch.bfloat16, max_seqs=B * reps,
+                      max_blocks_per_seq=max(need) + 1)
+    ids = torch.randperm(cap, generator=g).tolist()
+    tables, pos = [], 0
+    for _ in range(reps):
+        for n, L in zip(need, lens):
+            tables.append(ids[pos: pos + -(-L // BS)])
+            pos += n
+    free = ids[pos:]
+    kv.load_state(tables, lens * reps, free)
+    kv.k_pool.normal_()
+    kv.v_pool.normal_()
+    gd = torch.Generator(device=dev).manual_seed(seed + 5)
+    q = torch.randn(B, 1, hq, d, generator=gd, device=dev).to(torch.bfloat16)
+    kn = torch.randn(B, 1, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
+    vn = torch.randn(B, 1, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
+    sids = [torch.arange(r * B, (r + 1) * B, dtype=torch.int32, device=dev) for r in range(reps)]
+    st = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    max_ctx = max(lens) + 1
+    for r in range(reps):  # the new token's blocks exist from here on
+        kv.write_block_device(0, sids[r], st, kn, vn)
+    attend = lambda i: verify_attention(q, kv, 0, sids[i % reps], st, max_ctx, out=out)
+    append = lambda i: kv.write_block_device(0, sids[i % reps], st, kn, vn, alloc=False)
+    n = 3 * reps
+    for i in range(reps):
+        attend(i)
+    torch.cuda.synchronize()
+    ga = graph_of(lambda: [attend(i) for i in range(n)], 1, torch)
+    attn_us = time_graph(ga, 5, torch) * 1000.0 / n
+    gw = graph_of(lambda: [append(i) for i in range(n)], 1, torch)
+    app_us = time_graph(gw, 5, torch) * 1000.0 / n
+    nbytes = attention_bytes(lens, 1, hq, hkv, d, BS)
+    res = {"workload": "Qwen2.5-0.5B-shaped draft decode: batch 32, one query row, 14q/2kv heads, head_dim 64, "
+                       "block 16, bf16 KV, the verify workload's contexts (U[256,4096], seed 0); 8 replicas",
+           "attn_us": round(attn_us, 2), "attn_gbs": round(nbytes / (attn_us * 1e-6) / 1e9, 1),
+           "attn_bytes_per_call": nbytes, "append_us": round(app_us, 2)}
+    del kv, ga, gw
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -546,6 +603,9 @@ def main() -> int:
     if not args.no_cpu_baseline:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(w)
+    if not args.no_long_context:
+        print("bench: draft decode", file=sys.stderr, flush=True)
+        line["draft_decode"] = draft_decode(dev, args.seed)
     if args.full_depth_rounds > 0:
         del g_step, g_att, g_smp, g_ar, step, parts, res, w
         torch.cuda.synchronize()

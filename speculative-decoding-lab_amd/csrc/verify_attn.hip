@@ -12,7 +12,8 @@
 // shares; a sequence cut by share boundaries is combined by whichever of its
 // workgroups finishes last, inside the same kernel.
 //
-// MFMA path (bf16 K/V, head_dim 64/128, block_size 16, G >= 16), per page:
+// MFMA path (bf16 queries, bf16 or fp8 K/V, head_dim 64/128, block_size 16;
+// G below 16 pads one query tile), per page:
 //   S^T = K Q^T  with v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims straight
 //         from the K page, B = Q^T fragments held in registers);
 //   O^T += V^T P^T with v_mfma_f32_16x16x32_bf16 where A = {V^T, V^T} straight
@@ -1007,9 +1008,10 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
   // offsets (bytes for the partials).
   const bool fits32 = (long long)B * C * Hq * d < (1LL << 31) &&
                       2LL * kMfmaWGsMax * G * d * (long long)sizeof(float) < (1LL << 31);
+  // Any G: below 16 rows (decode, G = Hq / Hkv) the one query tile is padded
+  // with zero rows; the pages still cross HBM once, which is what bounds it.
   pl.mfma = (kv_dtype == SPV_BF16 || kv_dtype == SPV_FP8E4M3) && q_dtype == SPV_BF16 && bs == 16 &&
-            (d == 128 || d == 64) && G >= 16 &&
-            B <= kMfmaMaxB && fits32;
+            (d == 128 || d == 64) && B <= kMfmaMaxB && fits32;
   const int max_pages = (max_ctx + bs - 1) / bs;
   if (pl.mfma) {
     pl.nt = G >= 64 ? 4 : (G + 15) / 16;

@@ -154,7 +154,11 @@ def test_qwen15_shaped_bf16_mfma(cuda, seed):
     (9, 14, 2, 64),    # 0.5B-shaped heads: G = 63, d = 64
     (2, 16, 2, 128),   # G = 16, one tile
     (3, 12, 2, 128),   # G = 18, two tiles with padding
-    (1, 4, 2, 128),    # decode-like G = 2 on bf16: VALU path
+    (1, 4, 2, 128),    # decode G = 2: one padded tile
+    (1, 14, 2, 64),    # 0.5B-shaped draft decode: G = 7
+    (1, 12, 2, 128),   # 1.5B-shaped decode: G = 6
+    (1, 2, 2, 128),    # G = 1
+    (2, 14, 2, 64),    # G = 14
 ])
 def test_bf16_shapes(cuda, shape):
     C, Hq, Hkv, d = shape
@@ -165,6 +169,19 @@ def test_bf16_shapes(cuda, shape):
     out = paged_attention_extend(q.to(cuda), gpu, 0, list(range(len(lens))), lens, Hq)
     want = ref_attn.extend_attention_dense(q, keys, values, lens, Hq)
     _bf16_check(out, want)
+
+
+def test_bf16_draft_decode_batch(cuda):
+    """paged_attention_decode at a draft model's shape (one row, 14/2 heads,
+    head_dim 64) over ragged contexts: the padded single-tile MFMA path."""
+    g = torch.Generator().manual_seed(31)
+    B, Hq, Hkv, d = 48, 14, 2, 64
+    lens = torch.randint(1, 3000, (B,), generator=g).tolist()
+    gpu, keys, values = _dense_pool(cuda, [L - 1 for L in lens], 1, Hkv, d, 16, torch.bfloat16, seed=31)
+    q = torch.randn(B, Hq, d, generator=g).to(torch.bfloat16)
+    out = paged_attention_decode(q.to(cuda), gpu, 0, list(range(B)), lens, Hq)
+    want = ref_attn.extend_attention_dense(q.unsqueeze(1), keys, values, [L - 1 for L in lens], Hq).squeeze(1)
+    _bf16_check(out.unsqueeze(1), want.unsqueeze(1))
 
 
 def test_stale_nan_beyond_context_never_leaks(cuda):

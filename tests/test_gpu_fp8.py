@@ -203,6 +203,7 @@ def _fp8_pool_with(cuda, lens, H, d, bs, C, seed):
     (14, 2, 64, 9, [2000, 37, 700, 1, 129, 1500]),     # head_dim 64, pieces split across workgroups
     (12, 2, 128, 6, [3000, 256, 1, 999, 4000, 17]),    # head_dim 128
     (12, 2, 128, 6, [(i * 37) % 211 + 1 for i in range(140)]),  # segments outnumber workgroups
+    (14, 2, 64, 1, [(i * 997) % 3001 + 1 for i in range(32)]),  # draft decode: one row, G = 7
 ])
 def test_fp8_mfma_attention_matches_oracle(cuda, Hq, H, d, C, lens):
     """bf16 queries over an fp8 pool take the MFMA path: codes converted to
