@@ -72,6 +72,7 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
   __shared__ int s_scan[kPoolThreads / 64];
   __shared__ int s_fail;
   __shared__ int s_free[kAllocStage];  // s_free[i] = free_stack[top - 1 - i]
+  __shared__ int s_eoff[kPoolThreads], s_esid[kPoolThreads], s_enb[kPoolThreads];  // the chunk's entries
   const int top = ctr[CTR_TOP];
   // The first chunk of entries (one chunk for B <= blockDim.x), clamped loads.
   const int bc = min((int)threadIdx.x, B - 1);
@@ -96,17 +97,34 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
     const int avail = top - consumed;
     const int got = min(need, max(0, avail - off));
     if (b < B && got < need) atomicMin(&s_fail, b);
-    for (int i = 0; i < got; ++i) {
-      const int pos = consumed + off + i;
+    // The chunk pops positions [0, popped) of its part of the stack: entry e
+    // takes [off_e, off_e + got_e), contiguous in batch order. Every thread
+    // takes positions j, j + blockDim.x, ... and finds its entry (the last one
+    // whose offset is <= j: entries after it start beyond j) by bisection, so
+    // a long prompt's blocks are written by the whole workgroup.
+    s_eoff[threadIdx.x] = b < B ? off : 0x7fffffff;
+    s_esid[threadIdx.x] = sid;
+    s_enb[threadIdx.x] = nb;
+    if (b < B && got > 0) nblocks[sid] = nb + got;
+    const int popped = min(total, max(avail, 0));
+    __syncthreads();
+    const int nent = min((int)blockDim.x, B - base);
+    for (int j = threadIdx.x; j < popped; j += blockDim.x) {
+      int lo = 0, hi = nent - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_eoff[mid] <= j) lo = mid;
+        else hi = mid - 1;
+      }
+      const int pos = consumed + j;
       const int id = pos < nstage ? s_free[pos] : free_stack[top - 1 - pos];
-      tables[(size_t)sid * maxb + nb + i] = id;
+      tables[(size_t)s_esid[lo] * maxb + s_enb[lo] + (j - s_eoff[lo])] = id;
       free_flag[id] = 0;
       if (scales)  // an fp8 pool: the block starts with zero scales in every layer
         for (int l = 0; l < num_layers; ++l)
           *reinterpret_cast<float2*>(&scales[((size_t)l * cap + id) * 2]) = make_float2(0.f, 0.f);
     }
-    if (b < B && got > 0) nblocks[sid] = nb + got;
-    consumed += min(total, max(avail, 0));
+    consumed += popped;
     __syncthreads();
   }
   if (threadIdx.x == 0) {
