@@ -32,7 +32,6 @@ from typing import Callable, List, Optional, Sequence
 
 import torch
 
-from . import _hip
 from .kv import PagedKVCache
 from .spec_scheduler import VerifyResult, VerifyStep
 

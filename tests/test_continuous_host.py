@@ -5,7 +5,7 @@ from __future__ import annotations
 
 import pytest
 
-from engine.continuous import Request, SeqState, SpecContinuousDriver, poisson_requests, DriverResult
+from engine.continuous import DriverResult, Request, SpecContinuousDriver, poisson_requests
 
 
 class _Alloc:
