@@ -661,6 +661,20 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       l[nt] = 0.f;
     }
 
+    // head_dim 64: a page is half the bytes for the same per-key softmax work,
+    // which then bounds the walk (fp8 pages most). There the query fragments
+    // stay in registers for the whole walk, and the softmax takes the lean
+    // form of compute_page. (At head_dim 128 both measured slower.)
+    constexpr bool kLean = D == 64;
+    uint4 qreg[kLean ? KS : 1][kLean ? NT : 1];
+    if constexpr (kLean) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          qreg[ks][nt] = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
+    }
+
     int tab0 = lp0;  // first page whose block id is sTab[0]
     // With four query tiles (no registers to spare) pages are read through raw
     // buffers: the page's base is scalar and each lane keeps one 32-bit offset
@@ -729,8 +743,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         vscale = f.sv;
       }
       // The query fragments (B operand: row 16 nt + i16, dims 32 ks + 8 g .. + 7)
-      // are re-read from LDS for every page instead of being hoisted into
-      // registers for the whole walk.
+      // are re-read from LDS for every page at head_dim 128 instead of being
+      // hoisted into registers for the whole walk.
       asm volatile("" ::: "memory");
       f32x4_t sc[NT];
 #pragma unroll
@@ -739,20 +753,42 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          const uint4 qv = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
+          uint4 qv;
+          if constexpr (kLean) qv = qreg[ks][nt];
+          else qv = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
           sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k_frag<D>(f, ks)),
                                                            __builtin_bit_cast(bf16x8_t, qv), sc[nt], 0, 0, 0);
         }
       const bool need_mask = page * BS + BS - 1 > start;
       float x[NT][4];
       bool grow = false;
+      if constexpr (kLean) {
+        // Masks only on the pages that reach the chunk's own keys (a uniform
+        // branch); the growth test on the raw scores against (m + kSlack) /
+        // scale; the scale is applied inside the exponent's fma below.
+        if (need_mask) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
+          for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          x[nt][jj] = sc[nt][jj] * spage;
-          if (need_mask && kpos0 + jj > start + jrow[nt]) x[nt][jj] = -INFINITY;
-          grow |= x[nt][jj] > m[nt] + kSlack;
+            for (int jj = 0; jj < 4; ++jj)
+              if (kpos0 + jj > start + jrow[nt]) sc[nt][jj] = -INFINITY;
+        }
+        const float rsp = __builtin_amdgcn_rcpf(spage);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const float t = (m[nt] + kSlack) * rsp;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) grow |= sc[nt][jj] > t;
+        }
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            x[nt][jj] = sc[nt][jj] * spage;
+            if (need_mask && kpos0 + jj > start + jrow[nt]) x[nt][jj] = -INFINITY;
+            grow |= x[nt][jj] > m[nt] + kSlack;
+          }
         }
       }
       // m[nt] is a reference, not the running max: scores may exceed it by up
@@ -762,7 +798,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       if (__any(grow)) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          float mx = fmaxf(fmaxf(x[nt][0], x[nt][1]), fmaxf(x[nt][2], x[nt][3]));
+          float mx;
+          if constexpr (kLean) mx = fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])) * spage;
+          else mx = fmaxf(fmaxf(x[nt][0], x[nt][1]), fmaxf(x[nt][2], x[nt][3]));
           mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
           mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
           const float m_new = fmaxf(m[nt], mx);
@@ -776,11 +814,13 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       bf16x8_t pf[NT];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const float* x4 = x[nt];
         const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
         float e[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(x4[jj] - mu);
+        for (int jj = 0; jj < 4; ++jj) {
+          if constexpr (kLean) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[nt][jj], spage, -mu));
+          else e[jj] = __builtin_amdgcn_exp2f(x[nt][jj] - mu);
+        }
         l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
         if constexpr (kFp8) {
 #pragma unroll
