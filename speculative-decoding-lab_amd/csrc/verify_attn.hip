@@ -633,19 +633,55 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + i16, nr - 1)) / p.ratio;
 
-    // The previous segment's LDS readers are done: stage the segment's query
-    // rows (zero past nr) and the first block ids.
-    __syncthreads();
-    for (int t = threadIdx.x; t < min(kTabChunk, lp1 - lp0); t += blockDim.x)
-      sTab[t] = safe_block(p, table[lp0 + t]);
-    for (int idx = threadIdx.x; idx < RPG * (D / 8); idx += blockDim.x) {
-      const int rr = idx / (D / 8), c = idx - rr * (D / 8);
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (rr < nr) {
-        const int r = qr0 + rr, j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
-        v = *reinterpret_cast<const uint4*>(qbase + (((size_t)b * p.C + j) * p.Hq + hq) * D + 8 * c);
+    // Stage the segment's query rows (zero past nr) and the first block ids
+    // once the previous segment's LDS readers are done. Batched: every load is
+    // issued before that barrier and before any of them is stored, so the
+    // staging costs one round trip, not one per item. The head_dim-128
+    // kernels with four query tiles, or three in the cost-balanced split, keep
+    // the item-by-item loop: the batch's registers make them spill there.
+    constexpr bool kBatchStage = D == 64 || NT <= 2 || (NT == 3 && !BAL);
+    if constexpr (kBatchStage) {
+      static_assert(kTabChunk == kMfmaThreads, "one block id per thread");
+      constexpr int kQItems = (RPG * (D / 8) + kMfmaThreads - 1) / kMfmaThreads;
+      // The thread index is opaque so that no staging address is hoisted out
+      // of the piece loop, where it would live across the walk.
+      int stid = threadIdx.x;
+      asm volatile("" : "+v"(stid));
+      const int ntab = min(kTabChunk, lp1 - lp0);
+      int tabv = 0;
+      if (stid < ntab) tabv = table[lp0 + stid];
+      uint4 qv[kQItems];
+#pragma unroll
+      for (int k = 0; k < kQItems; ++k) {
+        const int idx = stid + k * kMfmaThreads;
+        const int rr = idx / (D / 8), c = idx - rr * (D / 8);
+        qv[k] = make_uint4(0, 0, 0, 0);
+        if (rr < nr) {  // rr < nr <= RPG: idx is in range
+          const int r = qr0 + rr, j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
+          qv[k] = *reinterpret_cast<const uint4*>(qbase + (((size_t)b * p.C + j) * p.Hq + hq) * D + 8 * c);
+        }
       }
-      *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = v;
+      __syncthreads();
+      if (stid < ntab) sTab[stid] = safe_block(p, tabv);
+#pragma unroll
+      for (int k = 0; k < kQItems; ++k) {
+        const int idx = stid + k * kMfmaThreads;
+        const int rr = idx / (D / 8), c = idx - rr * (D / 8);
+        if (idx < RPG * (D / 8)) *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = qv[k];
+      }
+    } else {
+      __syncthreads();
+      for (int t = threadIdx.x; t < min(kTabChunk, lp1 - lp0); t += blockDim.x)
+        sTab[t] = safe_block(p, table[lp0 + t]);
+      for (int idx = threadIdx.x; idx < RPG * (D / 8); idx += blockDim.x) {
+        const int rr = idx / (D / 8), c = idx - rr * (D / 8);
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (rr < nr) {
+          const int r = qr0 + rr, j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
+          v = *reinterpret_cast<const uint4*>(qbase + (((size_t)b * p.C + j) * p.Hq + hq) * D + 8 * c);
+        }
+        *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = v;
+      }
     }
     __syncthreads();
 
