@@ -456,6 +456,10 @@ __device__ __forceinline__ uint2 v_frag(const PageRegs<D, SPV_FP8E4M3>& f, int m
 template <int QT, int RPG, int D, typename SlotOf>
 __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b, int h, int qr0, int nr) {
   constexpr int kItems = (RPG * (D / 4) + kMfmaThreads - 1) / kMfmaThreads;  // float4 outputs per thread
+  // With 64-row groups, an opaque thread index: the item addresses are
+  // computed here, not hoisted over the caller's page walk and spilled.
+  int mtid = threadIdx.x;
+  if constexpr (RPG == 64) asm volatile("" : "+v"(mtid));
   float M[kItems], Ls[kItems];
   f32x4_t acc[kItems];
 #pragma unroll
@@ -473,7 +477,7 @@ __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b
     f32x4_t ov[kItems][kMergeChunk];
 #pragma unroll
     for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kMfmaThreads;
+      const int idx = mtid + it * kMfmaThreads;
       const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
 #pragma unroll
       for (int k = 0; k < kMergeChunk; ++k) {
@@ -505,7 +509,7 @@ __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b
   }
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
-    const int idx = threadIdx.x + it * kMfmaThreads;
+    const int idx = mtid + it * kMfmaThreads;
     const int rr = idx / (D / 4), e0 = (idx - rr * (D / 4)) * 4;
     if (rr >= nr) continue;
     const int r = qr0 + rr;
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   // (its last piece) for each workgroup w_a .. w_b that holds pages of it.
   // Otherwise: equal pieces, one slot each.
   constexpr bool balanced = BAL;  // chosen by the host: HR * B >= nw
-  const long long T = HR * s_pref[p.B];  // units of all segments
+  long long T = HR * s_pref[p.B];  // units of all segments
   auto page_start = [&](long long w) { return div_floor(w * T, nw); };
   auto owner = [&](long long g) { return (int)div_floor((g + 1) * nw - 1, T); };  // workgroup holding unit g
   const long long N = balanced ? 0 : HR * s_kpref[p.B];  // pieces in the batch
@@ -589,6 +593,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   const float sl2 = p.scale_log2;
 
   for (long long x = x_begin; x < x_stop;) {
+    // T is opaque here: what depends on it (its double) is recomputed per
+    // piece, not hoisted out of the loop and held across the walk.
+    if constexpr (BAL) asm volatile("" : "+s"(T));
     // This piece: pages [lp0, lp1) of segment (b, hr); its partial slot, and
     // the number of pieces (arrivals) of its segment.
     int b, hr, lp0, lp1, slot, narr, x0 = 0, w_a = 0;
@@ -629,9 +636,15 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     const int nr = min(RPG, p.G - qr0);
     const int32_t* table = p.tables + (size_t)uni(s_sid[b]) * p.maxb;
 
+    // With four query tiles the row index and the ratio are opaque here, so
+    // that what derives from them (the rows 16 nt + i16, the divisor's
+    // reciprocal) is recomputed per piece rather than held across the walk.
+    int jt = threadIdx.x, ratio = p.ratio;
+    if constexpr (NT == 4) asm volatile("" : "+v"(jt), "+s"(ratio));
+    const int ji16 = jt & 15;
     int jrow[NT];  // chunk row j of query column 16 nt + i16 (rows past nr repeat the last)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + i16, nr - 1)) / p.ratio;
+    for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + ji16, nr - 1)) / ratio;
 
     // Stage the segment's query rows (zero past nr) and the first block ids
     // once the previous segment's LDS readers are done. Batched: every load is
@@ -912,17 +925,27 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       }
     }
 
+    // With four query tiles (no registers to spare) the code after the walk
+    // takes its lane indices from an opaque copy of the thread index, so that
+    // the addresses derived from them are computed here, per piece, instead of
+    // being hoisted out of the piece loop and spilled across the walk (a
+    // scratch round trip per piece; the batch-128 Qwen2.5-3B shape ran 7%
+    // slower with them hoisted). With fewer tiles the plain indices allocate
+    // better.
+    int ptid = threadIdx.x;
+    if constexpr (NT == 4) asm volatile("" : "+v"(ptid));
+    const int pi16 = NT == 4 ? (ptid & 15) : i16, pg = NT == 4 ? ((ptid >> 4) & 3) : g;
     // Row sums: the four lane groups hold disjoint keys of the same query column.
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       l[nt] += __shfl_xor(l[nt], 16, 64);
       l[nt] += __shfl_xor(l[nt], 32, 64);
     }
-    if (g == 0) {
+    if (pg == 0) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        sm_m[w][16 * nt + i16] = m[nt];
-        sm_l[w][16 * nt + i16] = l[nt];
+        sm_m[w][16 * nt + pi16] = m[nt];
+        sm_l[w][16 * nt + pi16] = l[nt];
       }
     }
     __syncthreads();
@@ -937,8 +960,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // 2^(m_w - M) in place (sm_m[w][r]) and the row's 1 / L into sm_l[0][r],
     // and writes the row's (M, L) partial; the first round's barrier publishes
     // them to the combiners.
-    if ((int)threadIdx.x < nr) {
-      const int r = threadIdx.x;
+    if (ptid < nr) {
+      const int r = ptid;
       float cM = sm_m[0][r];
 #pragma unroll
       for (int ww = 1; ww < NWV; ++ww) cM = fmaxf(cM, sm_m[ww][r]);
@@ -959,8 +982,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // is made opaque here so that the combine's addresses are computed now,
     // not hoisted over the page walk (where they would spill).
     constexpr int kCItems = (TPR * RPG * 4 + kMfmaThreads - 1) / kMfmaThreads;
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
+    int tid = ptid;
+    if constexpr (NT != 4) asm volatile("" : "+v"(tid));
     int ct[kCItems], crow[kCItems], cd4[kCItems];
     bool combiner[kCItems];
     uint32_t cbase[kCItems];
@@ -990,8 +1013,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       for (int t = 0; t < TPR; ++t)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          if (16 * nt + i16 < nr)  // rows past nr are padding
-            *reinterpret_cast<f32x4_t*>(&sm_x[(((w * TPR) + t) * RPG + 16 * nt + i16) * 16 + 4 * g]) = o[mt0 + t][nt];
+          if (16 * nt + pi16 < nr)  // rows past nr are padding
+            *reinterpret_cast<f32x4_t*>(&sm_x[(((w * TPR) + t) * RPG + 16 * nt + pi16) * 16 + 4 * pg]) = o[mt0 + t][nt];
       __syncthreads();
 #pragma unroll
       for (int ci = 0; ci < kCItems; ++ci) {
