@@ -521,6 +521,13 @@ __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b
   }
 }
 
+// The combine slots hold a row's 16 dims as four 16-byte chunks; chunk c of
+// row r sits at position c ^ xswz(r). Without it the 16 lanes of a store
+// (rows r .. r + 15, one chunk) hit banks 64 B apart, four or eight to a bank
+// (with 64 or 32 banks); with it every 8 and every 16 consecutive rows cover
+// distinct banks.
+__device__ __forceinline__ int xswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
 template <int NT, int D, int QT, bool BAL, int KT>
 __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p) {
   constexpr bool kFp8 = KT == SPV_FP8E4M3;
@@ -1014,7 +1021,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
           if (16 * nt + pi16 < nr)  // rows past nr are padding
-            *reinterpret_cast<f32x4_t*>(&sm_x[(((w * TPR) + t) * RPG + 16 * nt + pi16) * 16 + 4 * pg]) = o[mt0 + t][nt];
+            *reinterpret_cast<f32x4_t*>(&sm_x[(((w * TPR) + t) * RPG + 16 * nt + pi16) * 16 + 4 * (pg ^ xswz(16 * nt + pi16))]) = o[mt0 + t][nt];
       __syncthreads();
 #pragma unroll
       for (int ci = 0; ci < kCItems; ++ci) {
@@ -1022,7 +1029,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         f32x4_t v[NWV];
 #pragma unroll
         for (int ww = 0; ww < NWV; ++ww)
-          v[ww] = *reinterpret_cast<const f32x4_t*>(&sm_x[(((ww * TPR) + ct[ci]) * RPG + crow[ci]) * 16 + 4 * cd4[ci]]);
+          v[ww] = *reinterpret_cast<const f32x4_t*>(&sm_x[(((ww * TPR) + ct[ci]) * RPG + crow[ci]) * 16 + 4 * (cd4[ci] ^ xswz(crow[ci]))]);
         f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ww = 0; ww < NWV; ++ww) acc += v[ww] * sm_m[ww][crow[ci]];
