@@ -238,10 +238,11 @@ constexpr int kMfmaMaxB = 512;    // the page and piece prefixes of the batch li
 // flight per wave.
 __host__ __device__ constexpr int ring_depth(int, int, int kt) { return kt == SPV_FP8E4M3 ? 4 : 2; }
 // The fixed cost of a piece (query staging, wave combine, partial and merge)
-// in pages of the walk, for the page-balanced split: 48 pages of 8 KB (bf16,
-// head_dim 128; measured best among 0..128 at batch 128, 16/2 heads, contexts
-// log-uniform in [512, 8192]), scaled to the page size.
-__host__ __device__ constexpr int piece_cost(int d, int kt) { return 48 * 8192 / (16 * d * 2 * (kt == SPV_FP8E4M3 ? 1 : 2)); }
+// in pages of the walk, for the page-balanced split: 32 pages of 8 KB (bf16,
+// head_dim 128; measured best among 24..56 at batch 128, 16/2 heads, contexts
+// log-uniform in [512, 8192], 2-3% ahead of 48, the best before the combine
+// and spill fixes), scaled to the page size.
+__host__ __device__ constexpr int piece_cost(int d, int kt) { return 32 * 8192 / (16 * d * 2 * (kt == SPV_FP8E4M3 ? 1 : 2)); }
 constexpr int kMfmaThreads = 512;
 // O^T tiles combined per LDS round: as many as fit beside the other buffers
 // (the slots take 8 waves x 16 * nt rows x 64 B per tile).
