@@ -297,3 +297,43 @@ def test_balanced_split_with_piece_costs(cuda, n_short, n_long, d):
     assert torch.equal(outs[0], outs[1])
     assert int(torch.count_nonzero(A._workspace._buf[: 1 << 18])) == 0
     _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, Hq))
+
+
+def _balanced_pieces(pages, hkv, cost, nw):
+    """Pieces of the cost-balanced split, as the host sees them: every
+    (sequence, kv head) segment is `cost` overhead units followed by its
+    pages, laid end to end; workgroup w takes units [w T / nw, (w + 1) T / nw).
+    Returns the page count of every non-empty (workgroup, segment) piece."""
+    seg = [n for n in pages for _ in range(hkv)]
+    total = sum(n + cost for n in seg)
+    starts, s0 = [], 0
+    for n in seg:
+        starts.append(s0)
+        s0 += n + cost
+    pieces = []
+    for w in range(nw):
+        a, b = w * total // nw, (w + 1) * total // nw
+        for st, n in zip(starts, seg):
+            lo, hi = max(a, st + cost), min(b, st + cost + n)
+            if hi > lo:
+                pieces.append(hi - lo)
+    return pieces
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_pieces_longer_than_the_block_id_window(cuda, d):
+    """Cost-balanced split with pieces of more than 512 pages: a workgroup
+    stages a piece's block ids in windows of 512 and restages them mid-walk.
+    128 sequences of 12,000-13,000 keys over 2 kv heads (256 segments)."""
+    Hq, Hkv, C, B = 2, 2, 2, 128
+    g = torch.Generator().manual_seed(d)
+    lens = [int(x) for x in torch.randint(12000, 13000, (B,), generator=g)]
+    pages = [-(-(L + C) // 16) for L in lens]
+    nw = torch.cuda.get_device_properties(0).multi_processor_count
+    cost = 32 * 8192 // (16 * d * 2 * 2)  # the kernel's piece cost, bf16 pages
+    pieces = _balanced_pieces(pages, Hkv, cost, nw)
+    assert B * Hkv >= nw and max(pieces) > 512, (nw, max(pieces))
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.bfloat16, seed=d + 1)
+    q = torch.randn(B, C, Hq, d, generator=g).to(torch.bfloat16)
+    out = verify_attention(q.to(cuda), gpu, 0, list(range(B)), lens, max(lens) + C)
+    _bf16_check(out, ref_attn.extend_attention_dense(q, keys, values, lens, Hq))
