@@ -34,7 +34,9 @@ using namespace spv;
 
 namespace {
 
-constexpr int kChunk = 8192;  // elements of a row per stats / race workgroup
+// Elements of a row per race workgroup: 16,384 (10 chunks at V = 151,936) ran
+// about 1 us faster per sampling call than 8,192 or 32,768, and 4,096 3 us slower.
+constexpr int kChunk = 16384;
 constexpr int kThreads = 256;
 constexpr int kVecPerThread = kChunk / 4 / kThreads;
 constexpr float kLog2e = 1.4426950408889634f;
