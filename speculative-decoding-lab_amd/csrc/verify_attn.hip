@@ -245,9 +245,12 @@ __host__ __device__ constexpr int ring_depth(int, int, int kt) { return kt == SP
 __host__ __device__ constexpr int piece_cost(int d, int kt) { return 32 * 8192 / (16 * d * 2 * (kt == SPV_FP8E4M3 ? 1 : 2)); }
 constexpr int kMfmaThreads = 512;
 // O^T tiles combined per LDS round: as many as fit beside the other buffers
-// (the slots take 8 waves x 16 * nt rows x 64 B per tile).
+// (the slots take 8 waves x 16 * nt rows x 64 B per tile). With four query
+// tiles: all four of head_dim 64 in one round (long context 2 us faster than
+// two rounds), two at head_dim 128 (four tiles per round made the batch-128
+// 3B shape spill more and run 1-4% slower).
 __host__ __device__ constexpr int combine_tiles(int nt, int mt) {
-  return (nt == 1 ? 8 : nt <= 3 ? 4 : 2) < mt ? (nt == 1 ? 8 : nt <= 3 ? 4 : 2) : mt;
+  return (nt == 1 ? 8 : nt <= 3 ? 4 : mt <= 4 ? 4 : 2) < mt ? (nt == 1 ? 8 : nt <= 3 ? 4 : mt <= 4 ? 4 : 2) : mt;
 }
 constexpr int kTabChunk = 512;    // block ids staged in LDS per window
 constexpr int kMergeChunk = 4;    // partial slots the merging workgroup loads at once
