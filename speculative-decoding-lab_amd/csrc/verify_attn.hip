@@ -520,8 +520,14 @@ __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b
     const float inv = 1.f / Ls[it];
     const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
     const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
+    if constexpr (QT == SPV_BF16) {
+      // four bf16 in one 8-byte store (e0 is a multiple of 4)
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + ob) =
+          make_uint2(pack2_bf16(acc[it][0] * inv, acc[it][1] * inv), pack2_bf16(acc[it][2] * inv, acc[it][3] * inv));
+    } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) store_out<QT>(p, ob + k, acc[it][k] * inv);
+      for (int k = 0; k < 4; ++k) store_out<QT>(p, ob + k, acc[it][k] * inv);
+    }
   }
 }
 
