@@ -172,8 +172,9 @@ size_t spv_verify_attn_workspace_bytes(int32_t B, int32_t C, int32_t num_q_heads
  * head h / (Hq/Hkv) (attention.py:32-38). q/out are (B, C, Hq, d) in q_dtype
  * (f32/bf16/f16); the pool holds kv_dtype. For SPV_FP8E4M3 pools kv_scales is
  * [layers][capacity][2] fp32 (K, V scale of each block). max_ctx must be >=
- * start_b + C for every b. bf16 pools with head_dim 128 (or 64), block_size 16
- * and (Hq/Hkv)*C >= 16 take the MFMA path; everything else the VALU path. */
+ * start_b + C for every b. bf16 queries over bf16 or fp8 pools with head_dim
+ * 128 or 64 and block_size 16 take the MFMA path (any (Hq/Hkv)*C); everything
+ * else the VALU path. */
 int spv_verify_attn(void* out, const void* q, int q_dtype,
                     const void* k_pool, const void* v_pool, int kv_dtype,
                     const float* kv_scales, const int32_t* block_tables,
