@@ -231,12 +231,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_valu_kernel(AttnParams p) {
 // counters are zero between calls.
 constexpr int kMfmaWGsMax = 512;  // bound on the persistent grid (slot numbering)
 constexpr int kMfmaMaxB = 512;    // the page and piece prefixes of the batch live in LDS
-// Register page buffers per wave: one page in flight while one is computed
-// (bf16). One workgroup of eight waves per CU (two per SIMD, <= 256 registers
-// each, so every operand stays in VGPRs) keeps eight pages in flight per CU.
-// fp8 pages take half the registers (8 for head_dim 64) and keep three in
-// flight per wave.
-__host__ __device__ constexpr int ring_depth(int, int, int kt) { return kt == SPV_FP8E4M3 ? 4 : 2; }
+// Register page buffers per wave: one page in flight while one is computed.
+// One workgroup of eight waves per CU (two per SIMD, <= 256 registers each, so
+// every operand stays in VGPRs) keeps eight pages in flight per CU. Deeper
+// rings measured slower: bf16 decode 16.0 -> 17.3 us with three, fp8 pages at
+// the long-context shape (batch 16, 32,768 keys, head_dim 64) 48.8 -> 50.4 us
+// with four, where the conversions and softmax, not the bytes, set the rate.
+__host__ __device__ constexpr int ring_depth(int, int, int) { return 2; }
 // The fixed cost of a piece (query staging, wave combine, partial and merge)
 // in pages of the walk, for the page-balanced split: 32 pages of 8 KB (bf16,
 // head_dim 128; measured best among 24..56 at batch 128, 16/2 heads, contexts
