@@ -12,14 +12,25 @@ the free list. One step =
      (target logits N(0, 2^2), draft = target + N(0, 1), T = 1, caller noise),
   4. rewind of the pool to start + n_commit with the sampled lengths.
 
-All inputs are resident in HBM before timing; steps run as captured HIP graphs.
-The batch exists in 8 replicas on disjoint random pages of the pool (and the
-logits in 2 sets); consecutive calls use different replicas, so none finds its
-K/V in the 256 MB last-level cache -- each call reads HBM as one layer of a
-deep model would. The headline ``value`` is the verify-attention HBM bandwidth (algorithmic
-bytes / measured time of the attention call); ``spec_step_us_per_seq`` is the
-whole step per sequence. ``cpu_baseline`` times the CPU oracle (the reference's
-gather + repeat_interleave + masked SDPA per sequence) on the host.
+All inputs are resident in HBM before timing. The batch exists in 8 replicas on
+disjoint random pages of the pool, each with its own draw of the context
+lengths (seeds seed .. seed + 7, so the headline is not one draw's luck), and
+the logits in 2 sets; consecutive steps use different replicas, so none finds
+its K/V in the 256 MB last-level cache -- each call reads HBM as one layer of
+a deep model would.
+
+The timed region is exactly ``--steps`` steps, launched back to back on the
+current stream behind a bounded device-side delay (so the host has queued
+them all before the GPU reaches the first), with HIP events around the whole
+region and around every attention call. The headline ``value`` is the
+verify-attention HBM bandwidth: algorithmic bytes of the timed calls / their
+summed event-measured durations. ``spec_step_us_per_seq`` is the whole step
+per sequence over the same region; ``graph_ms_per_step`` is the same step as a
+captured graph replay (outside the timed region). ``cpu_baseline`` times the
+CPU oracle's whole step (per-token write loop, gather + repeat_interleave +
+masked SDPA per sequence, batch_accept with a live generator, tail-first
+truncate with the free-list scan) on the host, with all host threads and with
+one.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -79,6 +90,11 @@ def workload_lens(seed=0):
     return torch.randint(256, 4097, (B,), generator=g).tolist(), g
 
 
+def replica_lens(seed=0):
+    """Context lengths of each replica: replica r is the draw of seed + r."""
+    return [workload_lens(seed + r)[0] for r in range(REPLICAS)]
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_attn_qwen15_b32_traffic.md")
 
 
@@ -120,10 +136,11 @@ def build_workload(dev, seed=0):
 
     from engine.kv import PagedKVCache
 
-    lens, g = workload_lens(seed)
+    rlens = replica_lens(seed)
+    g = torch.Generator().manual_seed(seed)
     perm = torch.randperm(CAP, generator=g).tolist()
     tables, pos = [], 0
-    for _ in range(REPLICAS):
+    for lens in rlens:
         for L in lens:
             n = -(-L // BS)
             tables.append(perm[pos: pos + n])
@@ -131,10 +148,10 @@ def build_workload(dev, seed=0):
     free = perm[pos:]
     kv = PagedKVCache(1, HKV, D, CAP, BS, dev, torch.bfloat16, max_seqs=B * REPLICAS,
                       max_blocks_per_seq=-(-(4096 + C) // BS) + 1)
-    kv.load_state(tables, lens * REPLICAS, free)
+    kv.load_state(tables, [L for lens in rlens for L in lens], free)
     gd = torch.Generator(device=dev).manual_seed(seed)
     keys, values = [], []
-    for r in range(REPLICAS):
+    for r, lens in enumerate(rlens):
         for s, L in enumerate(lens):
             k = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
             v = torch.randn(1, L, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
@@ -143,7 +160,10 @@ def build_workload(dev, seed=0):
                 keys.append(k[0])
                 values.append(v[0])
     w = {
-        "lens": lens,
+        "lens": rlens[0],
+        "rlens": rlens,
+        "tables0": tables[:B],
+        "free": free,
         "kv": kv,
         "keys": keys,
         "values": values,
@@ -151,7 +171,8 @@ def build_workload(dev, seed=0):
         "k_new": torch.randn(B, C, HKV, D, generator=gd, device=dev).to(torch.bfloat16),
         "v_new": torch.randn(B, C, HKV, D, generator=gd, device=dev).to(torch.bfloat16),
         "sids": [torch.arange(r * B, (r + 1) * B, dtype=torch.int32, device=dev) for r in range(REPLICAS)],
-        "start": torch.tensor(lens, dtype=torch.int32, device=dev),
+        "start": [torch.tensor(lens, dtype=torch.int32, device=dev) for lens in rlens],
+        "max_ctx": [max(lens) + C for lens in rlens],
         "logits": [],
     }
     for _ in range(LOGIT_SETS):
@@ -174,30 +195,32 @@ def make_step(w):
     from engine.spec_scheduler import _new_result, verify_sample
 
     kv = w["kv"]
-    max_ctx = max(w["lens"]) + C
     res = _new_result(B, GAMMA, kv.device)
 
     def append(r):
-        kv.write_block_device(0, w["sids"][r], w["start"], w["k_new"], w["v_new"])
+        kv.write_block_device(0, w["sids"][r], w["start"][r], w["k_new"], w["v_new"])
 
     def attend(r):
-        verify_attention(w["q"], kv, 0, w["sids"][r], w["start"], max_ctx, out=w["attn_out"])
+        verify_attention(w["q"], kv, 0, w["sids"][r], w["start"][r], w["max_ctx"][r], out=w["attn_out"])
 
-    def sample(t):
+    def sample(t, r=0):
         target, draft, proposals = w["logits"][t]
         verify_sample(target, draft, proposals, w["u"], w["noise"], 1.0,
-                      start_pos=w["start"], result=res, validate=False)
+                      start_pos=w["start"][r], result=res, validate=False)
 
     def rewind(r):
-        # All replicas share the context lengths, so the sampled new lengths
-        # apply to any of them.
+        # the new lengths were sampled against replica r's start positions
         kv.rewind_device(w["sids"][r], res.new_len, res.finished)
 
-    def step(i):
+    def step(i, events=None):
         r, t = i % REPLICAS, i % LOGIT_SETS
         append(r)
+        if events is not None:
+            events[0].record()
         attend(r)
-        sample(t)
+        if events is not None:
+            events[1].record()
+        sample(t, r)
         rewind(r)
 
     return step, {"append": append, "attend": attend, "sample": sample, "rewind": rewind}, res
@@ -243,46 +266,124 @@ def copy_bandwidth(dev, nbytes=1 << 30):
     return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(w, budget_s=10.0):
-    """The oracle's paged extend attention (gather per block, GQA expand, masked
-    SDPA per sequence) on the host, in GB/s of the same algorithmic bytes."""
+def sleep_cycles_per_ms(torch):
+    """Rate of ``torch.cuda._sleep`` (a bounded spin on the device clock), for
+    the delay queued ahead of the timed region."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    torch.cuda._sleep(2_000_000)
+    b.record()
+    torch.cuda.synchronize()
+    return 2_000_000 / max(a.elapsed_time(b), 1e-3)
+
+
+def timed_steps(step, steps, torch, host_us_per_step=400.0):
+    """Exactly ``steps`` steps on the current stream, queued behind a bounded
+    device-side delay long enough for the host to enqueue all of them, so the
+    GPU never waits on a launch. Events bracket the region and every attention
+    call. Returns (ms per step, per-call attention ms list)."""
+    rate = sleep_cycles_per_ms(torch)
+    delay_ms = min(400.0, 5.0 + steps * host_us_per_step / 1000.0)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    torch.cuda._sleep(int(rate * delay_ms))
+    start.record()
+    for i in range(steps):
+        step(i, ev[i])
+    end.record()
+    queued_ms = (time.perf_counter() - t0) * 1e3
+    torch.cuda.synchronize()
+    if queued_ms > delay_ms:
+        print("bench: warning: the host took {:.1f} ms to queue the timed steps, more than the {:.1f} ms "
+              "delay ahead of them".format(queued_ms, delay_ms), file=sys.stderr, flush=True)
+    return start.elapsed_time(end) / steps, [a.elapsed_time(b) for a, b in ev]
+
+
+def cpu_baseline(w, dev, budget_s=12.0):
+    """The CPU oracle's whole verify step on the host, timed with all host
+    threads and with one: the per-token write loop with lazy allocation from the
+    LIFO free list (the workload's own, ~30k entries), the per-block gather +
+    repeat_interleave + masked SDPA per sequence, logits_to_probs of every row
+    and batch_accept with a live generator, and the commit's tail-first
+    truncate with the free list's membership scan. Replica 0 of the workload,
+    fp32 K/V. ``value`` is the attention part in GB/s of the same algorithmic
+    bytes as the GPU headline."""
     import torch
 
     from oracle import attention as ref_attn
     from oracle import kv_pool as ref
+    from oracle import sampler as S
 
-    n_seq = len(w["lens"])  # the whole batch
-    lens = w["lens"][:n_seq]
-    cap = sum(-(-(L + C) // BS) for L in lens)
-    cpu = ref.PagedKVCache(1, HKV, D, cap, BS, dtype=torch.float32)
-    k_new = w["k_new"][:n_seq].float().cpu()
-    v_new = w["v_new"][:n_seq].float().cpu()
+    lens = w["lens"]
+    cpu = ref.PagedKVCache(1, HKV, D, CAP, BS, dtype=torch.float32)
+    cpu.load_state(w["tables0"], lens, w["free"])
     for s, L in enumerate(lens):
-        cpu.add_sequence(s)
-        cpu.write_block(0, [s], [0], w["keys"][s].float().cpu().unsqueeze(0),
-                        w["values"][s].float().cpu().unsqueeze(0))
-    cpu.write_block(0, list(range(n_seq)), lens, k_new, v_new)
-    q = w["q"][:n_seq].float().cpu()
+        k, v = w["keys"][s].float().cpu(), w["values"][s].float().cpu()
+        for bi, phys in enumerate(w["tables0"][s]):
+            n = min(BS, L - bi * BS)
+            cpu.k[0, phys, :n] = k[bi * BS: bi * BS + n]
+            cpu.v[0, phys, :n] = v[bi * BS: bi * BS + n]
+    k_new = w["k_new"].float().cpu()
+    v_new = w["v_new"].float().cpu()
+    q = w["q"].float().cpu()
+    target, draft, proposals = (x.cpu() for x in w["logits"][0])
+    props = proposals.tolist()
+    sids = list(range(B))
     nbytes = attention_bytes(lens)
+    gen = torch.Generator().manual_seed(1234)
+
+    def one_step():
+        t = [time.perf_counter()]
+        cpu.write_block(0, sids, lens, k_new, v_new)
+        t.append(time.perf_counter())
+        ref_attn.paged_attention_extend(q, cpu, 0, sids, lens, HQ)
+        t.append(time.perf_counter())
+        p = S.logits_to_probs(target, 1.0)
+        qd = S.logits_to_probs(draft, 1.0)
+        acc = S.batch_accept({s: p[s] for s in sids}, {s: list(qd[s]) for s in sids},
+                             {s: props[s] for s in sids}, gen)
+        t.append(time.perf_counter())
+        for s in sids:
+            cpu.truncate(s, lens[s] + len(acc[s]))
+        t.append(time.perf_counter())
+        return [b - a for a, b in zip(t, t[1:])]
+
+    def run(threads, budget):
+        torch.set_num_threads(threads)
+        one_step()  # warm-up
+        rows, t_end = [], time.perf_counter() + budget
+        while (time.perf_counter() < t_end or len(rows) < 3) and len(rows) < 200:
+            rows.append(one_step())
+        med = [sorted(r[i] for r in rows)[len(rows) // 2] for i in range(4)]
+        step_s = sorted(sum(r) for r in rows)[len(rows) // 2]
+        return {
+            "attn_gbs": round(nbytes / med[1] / 1e9, 3),
+            "spec_step_us_per_seq": round(step_s * 1e6 / B, 1),
+            "parts_ms": {k: round(v * 1e3, 2) for k, v in zip(("append", "attend", "sample", "rewind"), med)},
+            "runs": len(rows),
+        }
+
     threads = os.cpu_count() or 1
+    allc = run(threads, budget_s * 0.6)
+    one = run(1, budget_s * 0.4)
     torch.set_num_threads(threads)
-    ref_attn.paged_attention_extend(q, cpu, 0, list(range(n_seq)), lens, HQ)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while (time.perf_counter() < t_end or len(times) < 5) and len(times) < 500:
-        t0 = time.perf_counter()
-        ref_attn.paged_attention_extend(q, cpu, 0, list(range(n_seq)), lens, HQ)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
     return {
-        "value": round(nbytes / med / 1e9, 3),
+        "value": allc["attn_gbs"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": "oracle paged_attention_extend (per-block gather, repeat_interleave, masked SDPA "
-                  "per sequence, fp32) over all {} sequences of the batch, 1 layer, median of {} runs "
-                  "({:.1f} ms each)".format(n_seq, len(times), med * 1e3),
+        "sample": "the oracle's whole verify step on replica 0 of the workload (32 sequences, 1 layer, fp32 K/V): "
+                  "per-token write loop, per-block gather + repeat_interleave + masked SDPA per sequence, "
+                  "softmax of all 352 logits rows + batch_accept with a live generator, tail-first truncate with "
+                  "the free-list scan over ~30k free blocks; medians of {} runs on {} threads and {} runs on 1 "
+                  "thread. value = the attention part in GB/s".format(allc["runs"], threads, one["runs"]),
+        "spec_step_us_per_seq": allc["spec_step_us_per_seq"],
+        "parts_ms": allc["parts_ms"],
+        "one_thread": {"value": one["attn_gbs"], "spec_step_us_per_seq": one["spec_step_us_per_seq"],
+                       "parts_ms": one["parts_ms"]},
     }
 
 
@@ -311,13 +412,17 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
 
     from engine.continuous import SpecContinuousDriver, SyntheticVerifyModel, poisson_requests
     from engine.kv import PagedKVCache
+    from engine.scheduler import blocks_for_hbm, bytes_per_block
 
     chunk = FD_GAMMA + 1
     model = SyntheticVerifyModel(FD_LAYERS, FD_HQ, FD_HKV, FD_D, VOCAB, FD_GAMMA, FD_BATCH, dev,
                                  torch.bfloat16, seed=seed, draft_sigma=FD_SIGMA, prompt_cap=FD_CTX[1])
-    block_bytes = FD_LAYERS * 2 * FD_HKV * FD_BS * FD_D * 2
-    free, total = torch.cuda.mem_get_info(dev)
-    cap = int(pool_frac * free) // block_bytes
+    # The pool: pool_frac of the free HBM, in blocks of all 36 layers' K and V
+    # (engine.scheduler's sizing of the reference's build_kv).
+    block_bytes = bytes_per_block(FD_LAYERS, FD_BS, FD_HKV, FD_D, torch.bfloat16)
+    _free, total = torch.cuda.mem_get_info(dev)
+    cap = blocks_for_hbm(FD_LAYERS, FD_BS, FD_HKV, FD_D, torch.bfloat16, dev, reserve_bytes=0,
+                         fraction=pool_frac)
     maxb = -(-(FD_CTX[1] + FD_BUDGET[1] + chunk) // FD_BS) + 1
     n_req = FD_BATCH + int(FD_RATE * (rounds + warmup)) + 16
     kv = PagedKVCache(FD_LAYERS, FD_HKV, FD_D, cap, FD_BS, dev, torch.bfloat16, max_seqs=n_req,
@@ -528,25 +633,27 @@ def main() -> int:
     for i in range(max(1, args.warmup) * REPLICAS):
         step(i)
     torch.cuda.synchronize()
-    print("bench: warm-up done, capturing", file=sys.stderr, flush=True)
+    print("bench: warm-up done, timing {} steps".format(args.steps), file=sys.stderr, flush=True)
 
-    # Timed region: K whole steps; one graph replay runs REPLICAS steps (each
-    # on its own replica of the batch), so the K steps are ceil(K / REPLICAS)
-    # replays.
+    # Timed region: exactly --steps steps, events around each attention call.
+    ms_per_step, attn_ms = timed_steps(step, args.steps, torch)
+    rl = w["rlens"]
+    attn_bytes_timed = sum(attention_bytes(rl[i % REPLICAS]) for i in range(args.steps))
+    attn_us = 1000.0 * sum(attn_ms) / len(attn_ms)
+    attn_gbs = attn_bytes_timed / (sum(attn_ms) * 1e-3) / 1e9
+
+    # Outside the timed region: the step as a captured graph (one replay runs
+    # REPLICAS steps), and per-part graphs of back-to-back calls cycling over
+    # the replicas / logits sets.
     g_step = graph_of(lambda: [step(i) for i in range(REPLICAS)], 1, torch)
-    for _ in range(args.warmup):
+    for _ in range(2):
         g_step.replay()
-    torch.cuda.synchronize()
-    replays = max(1, -(-args.steps // REPLICAS))
-    ms_per_step = time_graph(g_step, replays, torch) / REPLICAS
-
-    # Per-part timings outside the timed region: graphs of back-to-back calls
-    # cycling over the replicas / logits sets.
+    graph_ms_per_step = time_graph(g_step, 4, torch) / REPLICAS
     reps = 3 * REPLICAS
     part_us = {}
     g_att = graph_of(lambda: [parts["attend"](i % REPLICAS) for i in range(reps)], 1, torch)
     part_us["attend"] = time_graph(g_att, 5, torch) * 1000.0 / reps
-    g_smp = graph_of(lambda: [parts["sample"](i % LOGIT_SETS) for i in range(reps)], 1, torch)
+    g_smp = graph_of(lambda: [parts["sample"](i % LOGIT_SETS, i % REPLICAS) for i in range(reps)], 1, torch)
     part_us["sample"] = time_graph(g_smp, 5, torch) * 1000.0 / reps
     g_ar = graph_of(lambda: [(parts["append"](i % REPLICAS), parts["rewind"](i % REPLICAS)) for i in range(reps)],
                     1, torch)
@@ -556,8 +663,7 @@ def main() -> int:
 
     copy_gbs = copy_bandwidth(dev)
     lens = w["lens"]
-    attn_bytes = attention_bytes(lens)
-    attn_gbs = attn_bytes / (part_us["attend"] * 1e-6) / 1e9
+    all_lens = [L for r in rl for L in r]
     samp_gbs = sample_bytes(B) / (part_us["sample"] * 1e-6) / 1e9
     accept = res.accept_len.float().mean().item()
 
@@ -566,7 +672,7 @@ def main() -> int:
         "value": round(attn_gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": replays * REPLICAS,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
@@ -577,18 +683,23 @@ def main() -> int:
         "config": {
             "workload": "Qwen2.5-1.5B-shaped paged verify step: batch 32, gamma 5 (6 rows), "
                         "12q/2kv heads, head_dim 128, block 16, ctx U[256,4096], 65536-block pool, "
-                        "1 layer; fused sampling over V=151936 fp32 at T=1; calls cycle over 8 "
-                        "replicas of the batch on disjoint pages (no last-level-cache reuse)",
+                        "1 layer; fused sampling over V=151936 fp32 at T=1; 8 replicas of the batch on "
+                        "disjoint pages, each its own context draw (seeds {}..{}), cycled so no call "
+                        "reuses the last-level cache".format(args.seed, args.seed + REPLICAS - 1),
             "global_batch": B,
-            "seq_len": int(sum(lens) / len(lens)),
+            "seq_len": int(sum(all_lens) / len(all_lens)),
             "parallelism": "single-gpu",
         },
         "pct_of_peak": round(100.0 * attn_gbs / HBM_PEAK_GBS, 2),
         "copy_gbs": round(copy_gbs, 1),
+        "attn_us": round(attn_us, 2),
+        "attn_bytes_per_call": round(attn_bytes_timed / args.steps),
         "spec_step_us_per_seq": round(ms_per_step * 1000.0 / B, 3),
+        "graph_ms_per_step": round(graph_ms_per_step, 4),
+        "graph_spec_step_us_per_seq": round(graph_ms_per_step * 1000.0 / B, 3),
         "parts_us": {k: round(v, 2) for k, v in part_us.items()},
         "sample_gbs": round(samp_gbs, 1),
-        "attn_bytes_per_call": attn_bytes,
+        "mean_ctx": round(sum(all_lens) / len(all_lens), 1),
         "mean_accepted_drafts": round(accept, 3),
         "roofline": {
             "bound": "hbm",
@@ -602,7 +713,7 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(w)
+        line["cpu_baseline"] = cpu_baseline(w, dev)
     if not args.no_long_context:
         print("bench: draft decode", file=sys.stderr, flush=True)
         line["draft_decode"] = draft_decode(dev, args.seed)

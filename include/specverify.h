@@ -15,7 +15,12 @@
  *   V pool  [num_layers][capacity][num_kv_heads][head_dim][block_size]
  *   block_tables [max_seqs][max_blocks_per_seq] int32, num_blocks[max_seqs],
  *   seq_lens[max_seqs], free_stack[capacity] (bottom..top), free_flag[capacity]
- *   (1 = on the free list), ctr[SPV_CTR_WORDS] (ctr[0] = free count).
+ *   (1 = on the free list), ctr[SPV_CTR_WORDS]: [0] free count, [1] 1 + batch
+ *   index whose allocation exhausted the pool (last allocation), [2] slow-path
+ *   rewinds, [3] blocks pushed by the last rewind, [4] last single alloc, [5]
+ *   arrival count (zero between calls), [6] sticky 1 + batch index whose
+ *   allocation the table width (max_blocks_per_seq) capped, [7] sticky 1 +
+ *   batch index of a forbidden attention read (see spv_verify_attn).
  *
  * Reference interfaces replaced (paths relative to the reference repository):
  *   engine/kv.py, engine/attention.py, engine/spec_scheduler.py,
@@ -83,7 +88,11 @@ int spv_pool_free_one(int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
  * need not know the index in advance.
  * seq_lens[sid] = max(seq_lens[sid], last written position + 1). seq_ids must
  * be distinct within one call. k_new = v_new = NULL allocates only
- * (PagedKVCache._ensure_blocks_up_to, kv.py:119-122): no copy, no length change. */
+ * (PagedKVCache._ensure_blocks_up_to, kv.py:119-122): no copy, no length change.
+ * A table holds at most max_blocks_per_seq blocks (the reference's list has no
+ * bound): a sequence whose chunk needs more gets only the blocks that fit, its
+ * tokens beyond them are not written, and ctr[6] is set to 1 + its batch index
+ * (sticky). Callers keep start + C <= max_blocks_per_seq * block_size. */
 int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype,
                   const void* k_new, const void* v_new,
                   int32_t* block_tables, int32_t max_blocks_per_seq,
@@ -173,13 +182,19 @@ size_t spv_verify_attn_workspace_bytes(int32_t B, int32_t C, int32_t num_q_heads
  * (f32/bf16/f16); the pool holds kv_dtype. For SPV_FP8E4M3 pools kv_scales is
  * [layers][capacity][2] fp32 (K, V scale of each block). max_ctx must be >=
  * start_b + C for every b. bf16 queries over bf16 or fp8 pools with head_dim
- * 128 or 64 and block_size 16 take the MFMA path (any (Hq/Hkv)*C); everything
- * else the VALU path. */
+ * 128 or 64, block_size 16 and B <= 2048 take the MFMA path (any (Hq/Hkv)*C);
+ * everything else (including larger batches) the VALU path.
+ * seq_lens / ctr (the pool's, both may be NULL): a read the contract forbids
+ * -- a table entry outside [0, capacity), start_b + C > seq_lens[seq_ids[b]]
+ * (keys not written yet), start_b < 0 or start_b + C > max_ctx -- sets
+ * ctr[7] = 1 + b (sticky; the caller clears it). Such a page reads block 0
+ * instead, so the call never faults, and the rows of b are meaningless. */
 int spv_verify_attn(void* out, const void* q, int q_dtype,
                     const void* k_pool, const void* v_pool, int kv_dtype,
                     const float* kv_scales, const int32_t* block_tables,
                     int32_t max_blocks_per_seq, const int32_t* seq_ids,
-                    const int32_t* start_pos, int32_t B, int32_t C,
+                    const int32_t* start_pos, const int32_t* seq_lens,
+                    int32_t* ctr, int32_t B, int32_t C,
                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                     int32_t block_size, int32_t layer, int32_t capacity,
                     int32_t max_ctx, float scale, void* workspace,

@@ -39,13 +39,7 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    if not sources:
-        raise RuntimeError("no HIP sources under " + CSRC)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + ["-o", tmp] + sources
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
@@ -55,6 +49,27 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError("hipcc failed ({}):\n{}".format(proc.returncode, out))
     if verbose and out.strip():
         print(out)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every csrc/*.hip to an object (in parallel), then link the library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(LIB_DIR, exist_ok=True)
+    obj_dir = os.path.join(LIB_DIR, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    if not sources:
+        raise RuntimeError("no HIP sources under " + CSRC)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    objs = [os.path.join(obj_dir, os.path.basename(s)[:-4] + ".o") for s in sources]
+    jobs = max(1, min(len(sources), int(os.environ.get("MAX_JOBS", "8"))))
+    with ThreadPoolExecutor(jobs) as ex:
+        for f in [ex.submit(_run, [hipcc()] + compile_flags + ["-c", s, "-o", o], verbose)
+                  for s, o in zip(sources, objs)]:
+            f.result()
+    tmp = LIB_PATH + ".tmp"
+    _run([hipcc(), "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", tmp] + objs, verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
     const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, int32_t B, int32_t C,
     int32_t bs, float* __restrict__ scales, int32_t num_layers, int32_t cap) {
   __shared__ int s_scan[kPoolThreads / 64];
-  __shared__ int s_fail;
+  __shared__ int s_fail, s_ovf;
   __shared__ int s_free[kAllocStage];  // s_free[i] = free_stack[top - 1 - i]
   __shared__ int s_eoff[kPoolThreads], s_esid[kPoolThreads], s_enb[kPoolThreads];  // the chunk's entries
   const int top = ctr[CTR_TOP];
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
   const int maxneed = (int)min((long long)B * ((C + bs - 1) / bs + 1), (long long)kAllocStage);
   const int nstage = min(top, maxneed);
   for (int i = threadIdx.x; i < nstage; i += blockDim.x) s_free[i] = free_stack[top - 1 - i];
-  if (threadIdx.x == 0) s_fail = B;
+  if (threadIdx.x == 0) s_fail = s_ovf = B;
   __syncthreads();
   int consumed = 0;
   for (int base = 0; base < B; base += blockDim.x) {
@@ -91,7 +91,10 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
       st = start[b];
       nb = nblocks[sid];
     }
-    const int need = b < B ? max(0, (st + C - 1) / bs + 1 - nb) : 0;
+    // A table holds at most maxb blocks: a longer need is capped (and reported).
+    const int want = b < B ? max(0, (st + C - 1) / bs + 1 - nb) : 0;
+    const int need = min(want, max(0, maxb - nb));
+    if (need < want) atomicMin(&s_ovf, b);
     int total;
     const int off = block_exclusive_scan(need, s_scan, &total);
     const int avail = top - consumed;
@@ -130,6 +133,7 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
   if (threadIdx.x == 0) {
     ctr[CTR_TOP] = top - consumed;
     ctr[CTR_EXHAUSTED] = s_fail < B ? s_fail + 1 : 0;
+    if (s_ovf < B) ctr[CTR_OVERFLOW] = s_ovf + 1;
   }
 }
 
@@ -260,7 +264,7 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
   __shared__ int s_scan[kFusedThreads / 64];
   __shared__ int s_free[kFusedStage];
   __shared__ int s_nbnew[kFusedMaxB], s_sid[kFusedMaxB];
-  __shared__ int s_fail, s_off, s_got, s_nbold, s_flag;
+  __shared__ int s_fail, s_ovf, s_off, s_got, s_nbold, s_flag;
   __shared__ int s_phys[kFusedMaxBlocks];
   const int b = blockIdx.x / hkv, h = blockIdx.x - b * hkv;
   const size_t row_elems = (size_t)hkv * d;
@@ -290,7 +294,7 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
   const int nyb = (max(s0, 0) + C - 1) / bs - blk0 + 1;  // blocks the chunk touches
   int tab = 0;
   if ((int)threadIdx.x < nyb) tab = tables[(size_t)sid * maxb + min(blk0 + (int)threadIdx.x, maxb - 1)];
-  if (threadIdx.x == 0) s_fail = B;
+  if (threadIdx.x == 0) s_fail = s_ovf = B;
   int consumed = 0;
   for (int base = 0; base < B; base += kFusedThreads) {
     const int e = base + threadIdx.x;
@@ -298,7 +302,10 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
     if (e < B) {
       const int st = base == 0 ? st_e0 : start[e];
       nb = base == 0 ? nb_e : nblocks[seq_ids[e]];
-      need = max(0, (st + C - 1) / bs + 1 - nb);
+      // capped at the table width (reported), as in kv_alloc_kernel
+      const int want = max(0, (st + C - 1) / bs + 1 - nb);
+      need = min(want, max(0, maxb - nb));
+      if (need < want) atomicMin(&s_ovf, e);
     }
     int total;
     const int off = block_exclusive_scan(need, s_scan, &total);
@@ -317,7 +324,7 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
     consumed += min(total, max(avail, 0));
     __syncthreads();
   }
-  const int off = s_off, got = s_got, nb_old = s_nbold, fail = s_fail;
+  const int off = s_off, got = s_got, nb_old = s_nbold, fail = s_fail, ovf = s_ovf;
   const int nb_new = nb_old + got;
   auto stack_at = [&](int pos) { return pos < nstage ? s_free[pos] : free_stack[top - 1 - pos]; };
   if ((int)threadIdx.x < nyb) {
@@ -381,6 +388,7 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
       ctr[CTR_ARRIVE] = 0;
       ctr[CTR_TOP] = top - consumed;
       ctr[CTR_EXHAUSTED] = fail < B ? fail + 1 : 0;
+      if (ovf < B) ctr[CTR_OVERFLOW] = ovf + 1;
     }
   }
 }

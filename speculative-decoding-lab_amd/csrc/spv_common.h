@@ -27,6 +27,8 @@ enum : int {
   CTR_PUSHED = 3,     // blocks actually pushed by the last rewind / free
   CTR_POPPED = 4,     // block id returned by the last single alloc (-1 if exhausted)
   CTR_ARRIVE = 5,     // arrival count of the one-launch append (zero between launches)
+  CTR_OVERFLOW = 6,   // sticky: 1 + batch index of a sequence whose table width capped an allocation
+  CTR_BAD_READ = 7,   // sticky: 1 + batch index of an attention row over an unwritten / out-of-pool page
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) {
@@ -188,6 +190,14 @@ __device__ __forceinline__ bool arrive_last(int* counter, int total, int* s_flag
   __syncthreads();
   return *s_flag;
 }
+
+// spv_verify_attn with the workspace passed in (verify_attn.hip).
+int verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_pool, const void* v_pool, int kv_dtype,
+                     const float* kv_scales, const int32_t* block_tables, int32_t max_blocks_per_seq,
+                     const int32_t* seq_ids, const int32_t* start_pos, const int32_t* seq_lens, int32_t* ctr,
+                     int32_t B, int32_t C, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t block_size, int32_t layer, int32_t capacity, int32_t max_ctx, float scale,
+                     void* workspace, size_t workspace_bytes, bool exact_layout, void* stream);
 
 }  // namespace spv
 

@@ -53,6 +53,8 @@ struct AttnParams {
   const int32_t* tables;
   const int32_t* seq_ids;
   const int32_t* start;
+  const int32_t* lens;  // the pool's sequence lengths (NULL: not checked)
+  int32_t* ctr;         // the pool's counters: CTR_BAD_READ is set on a forbidden read (NULL: not reported)
   int* counters;   // MFMA path: pages finished per segment, [B][Hkv][nrg]
   float* part_o;   // partial rows x d
   float* part_ml;  // partial rows x 2 (m in log2 units, l)
@@ -67,10 +69,19 @@ __device__ __forceinline__ int context_pages(const AttnParams& p, int L) {
   return min((L + p.bs - 1) / p.bs, p.max_pages);
 }
 
-// A table entry outside the pool (an unwritten slot) reads block 0 instead of
-// faulting; callers validate tables on the host.
-__device__ __forceinline__ int safe_block(const AttnParams& p, int phys) {
-  return (unsigned)phys < (unsigned)p.cap ? phys : 0;
+// Records a read the attention contract forbids -- a table entry outside the
+// pool (an unwritten slot), a chunk beyond its sequence's written length, or a
+// context longer than max_ctx -- as 1 + the batch index in ctr[CTR_BAD_READ]
+// (sticky; any offending index may win). The kernel still never faults: such
+// a page reads block 0 instead.
+__device__ __forceinline__ void flag_bad_read(const AttnParams& p, int b) {
+  if (p.ctr) p.ctr[CTR_BAD_READ] = b + 1;
+}
+
+__device__ __forceinline__ int safe_block(const AttnParams& p, int phys, int b) {
+  if ((unsigned)phys < (unsigned)p.cap) return phys;
+  flag_bad_read(p, b);
+  return 0;
 }
 
 __device__ __forceinline__ size_t slot_index(const AttnParams& p, int phys, int h) {
@@ -99,6 +110,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_valu_kernel(AttnParams p) {
   const int d = p.d;
   const int sid = p.seq_ids[b];
   const int32_t* table = p.tables + (size_t)sid * p.maxb;
+  if (threadIdx.x == 0 && s == 0 && rg == 0 && h == 0 &&
+      ((p.lens && p.lens[sid] < L) || (L + p.bs - 1) / p.bs > p.max_pages))
+    flag_bad_read(p, b);
 
   float* Qs = smem;              // [64][d]
   float* Ks = Qs + 64 * d;       // [16][d]
@@ -129,7 +143,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_valu_kernel(AttnParams p) {
     for (int idx = threadIdx.x; idx < nt * d; idx += blockDim.x) {
       const int tt = idx / d, e = idx - tt * d;
       const int pos = t0 + tt, blk = pos / p.bs, off = pos - blk * p.bs;
-      const int phys = safe_block(p, table[blk]);
+      const int phys = safe_block(p, table[blk], b);
       const size_t slot = slot_index(p, phys, h);
       float kv = load_elem<KT>(p.kpool, (slot * p.bs + off) * d + e);
       float vv = load_elem<KT>(p.vpool, (slot * d + e) * p.bs + off);
@@ -230,7 +244,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_valu_kernel(AttnParams p) {
 // count merges the segment's partials and sets the counter back to zero, so the
 // counters are zero between calls.
 constexpr int kMfmaWGsMax = 512;  // bound on the persistent grid (slot numbering)
-constexpr int kMfmaMaxB = 512;    // the page and piece prefixes of the batch live in LDS
+constexpr int kMfmaMaxB = 2048;   // the page and piece prefixes of the batch live in LDS (32 KB at 2048)
 // Register page buffers per wave: one page in flight while one is computed.
 // One workgroup of eight waves per CU (two per SIMD, <= 256 registers each, so
 // every operand stays in VGPRs) keeps eight pages in flight per CU. Deeper
@@ -367,6 +381,7 @@ __device__ void build_plan(const AttnParams& p, int* s_pref, int* s_kpref, int* 
         s_start[b] = st;
         s_sid[b] = p.seq_ids[b];
         np = min((st + p.C + BS - 1) / BS, p.max_pages);
+        if (st < 0 || (st + p.C + BS - 1) / BS > p.max_pages) flag_bad_read(p, b);
       }
       const int wgt = np + (BAL && b < p.B ? piece_cost : 0);
       const int incl = wave_incl_sum(wgt);
@@ -652,7 +667,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     const int L = start + p.C;
     const int qr0 = rg * RPG;
     const int nr = min(RPG, p.G - qr0);
-    const int32_t* table = p.tables + (size_t)uni(s_sid[b]) * p.maxb;
+    const int sid = uni(s_sid[b]);
+    const int32_t* table = p.tables + (size_t)sid * p.maxb;
 
     // With four query tiles the row index and the ratio are opaque here, so
     // that what derives from them (the rows 16 nt + i16, the divisor's
@@ -679,8 +695,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       int stid = threadIdx.x;
       asm volatile("" : "+v"(stid));
       const int ntab = min(kTabChunk, lp1 - lp0);
-      int tabv = 0;
+      int tabv = 0, lenv = 0x7fffffff;
       if (stid < ntab) tabv = table[lp0 + stid];
+      if (stid == 0 && p.lens) lenv = p.lens[sid];
       uint4 qv[kQItems];
 #pragma unroll
       for (int k = 0; k < kQItems; ++k) {
@@ -693,7 +710,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         }
       }
       __syncthreads();
-      if (stid < ntab) sTab[stid] = safe_block(p, tabv);
+      if (stid < ntab) sTab[stid] = safe_block(p, tabv, b);
+      if (lenv < L) flag_bad_read(p, b);
 #pragma unroll
       for (int k = 0; k < kQItems; ++k) {
         const int idx = stid + k * kMfmaThreads;
@@ -701,9 +719,11 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         if (idx < RPG * (D / 8)) *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = qv[k];
       }
     } else {
+      const int lenv = threadIdx.x == 0 && p.lens ? p.lens[sid] : 0x7fffffff;
       __syncthreads();
       for (int t = threadIdx.x; t < min(kTabChunk, lp1 - lp0); t += blockDim.x)
-        sTab[t] = safe_block(p, table[lp0 + t]);
+        sTab[t] = safe_block(p, table[lp0 + t], b);
+      if (lenv < L) flag_bad_read(p, b);
       for (int idx = threadIdx.x; idx < RPG * (D / 8); idx += blockDim.x) {
         const int rr = idx / (D / 8), c = idx - rr * (D / 8);
         uint4 v = make_uint4(0, 0, 0, 0);
@@ -921,7 +941,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       const int wend = min(lp1, tab0 + kTabChunk);
       if (tab0 != lp0) {
         __syncthreads();
-        for (int t = threadIdx.x; t < wend - tab0; t += blockDim.x) sTab[t] = safe_block(p, table[tab0 + t]);
+        for (int t = threadIdx.x; t < wend - tab0; t += blockDim.x) sTab[t] = safe_block(p, table[tab0 + t], b);
         __syncthreads();
       }
       const int pg0 = tab0 + w, last = wend - 1;
@@ -1147,10 +1167,12 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
   return pl;
 }
 
-// Partial rows the plan may write (0: the call needs no partials).
-size_t partial_rows(const Plan& pl, int B, int C, int Hq, int Hkv) {
+// Partial rows the plan may write (0: the call needs no partials). The MFMA
+// path keeps two partial slots per workgroup of a persistent grid of `nw`
+// workgroups (kMfmaWGsMax when the device is not known yet).
+size_t partial_rows(const Plan& pl, int B, int C, int Hq, int Hkv, int nw = kMfmaWGsMax) {
   const size_t G = (size_t)C * (Hq / Hkv);
-  if (pl.mfma) return (size_t)2 * kMfmaWGsMax * G;  // two partial slots per workgroup
+  if (pl.mfma) return (size_t)2 * nw * G;
   if (pl.max_splits <= 1) return 0;
   return (size_t)B * Hkv * pl.max_splits * G;
 }
@@ -1158,9 +1180,9 @@ size_t partial_rows(const Plan& pl, int B, int C, int Hq, int Hkv) {
 // Bytes of the (m, l) rows, padded so the O rows that follow are 256-byte aligned.
 size_t ml_bytes(size_t rows) { return (rows * 2 * sizeof(float) + 255) & ~(size_t)255; }
 
-size_t workspace_for(const Plan& pl, int B, int C, int Hq, int Hkv, int d) {
+size_t workspace_for(const Plan& pl, int B, int C, int Hq, int Hkv, int d, int nw = kMfmaWGsMax) {
   if (!pl.mfma && pl.max_splits <= 1) return 0;
-  const size_t rows = partial_rows(pl, B, C, Hq, Hkv);
+  const size_t rows = partial_rows(pl, B, C, Hq, Hkv, nw);
   return (size_t)SPV_ATTN_COUNTER_BYTES + ml_bytes(rows) + rows * d * sizeof(float);
 }
 
@@ -1237,11 +1259,17 @@ size_t spv_verify_attn_workspace_bytes(int32_t B, int32_t C, int32_t num_q_heads
   return wa > wv ? wa : wv;
 }
 
-int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, const void* v_pool, int kv_dtype,
-                    const float* kv_scales, const int32_t* block_tables, int32_t max_blocks_per_seq,
-                    const int32_t* seq_ids, const int32_t* start_pos, int32_t B, int32_t C, int32_t num_q_heads,
-                    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t layer, int32_t capacity,
-                    int32_t max_ctx, float scale, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// The body of spv_verify_attn, shared with the library's allocation-free
+// variant: `exact_layout` sizes the MFMA partial slots for this device's
+// persistent grid instead of the largest one.
+int spv::verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_pool, const void* v_pool, int kv_dtype,
+                     const float* kv_scales, const int32_t* block_tables, int32_t max_blocks_per_seq,
+                     const int32_t* seq_ids, const int32_t* start_pos, const int32_t* seq_lens, int32_t* ctr,
+                     int32_t B, int32_t C, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t block_size, int32_t layer, int32_t capacity, int32_t max_ctx, float scale,
+                     void* workspace, size_t workspace_bytes, bool exact_layout, void* stream) {
   if (!out || !q || !k_pool || !v_pool || !block_tables || !seq_ids || !start_pos) return SPV_ERR_ARG;
   if (q_dtype != SPV_F32 && q_dtype != SPV_BF16 && q_dtype != SPV_F16) return SPV_ERR_ARG;
   if (dtype_size(kv_dtype) == 0) return SPV_ERR_ARG;
@@ -1252,7 +1280,8 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
     return SPV_ERR_ARG;
   if (B == 0) return SPV_OK;
   const Plan pl = make_plan(B, C, num_q_heads, num_kv_heads, head_dim, block_size, max_ctx, kv_dtype, q_dtype);
-  const size_t need = workspace_for(pl, B, C, num_q_heads, num_kv_heads, head_dim);
+  const int nw_layout = exact_layout ? persistent_wgs() : kMfmaWGsMax;
+  const size_t need = workspace_for(pl, B, C, num_q_heads, num_kv_heads, head_dim, nw_layout);
   if (need > 0 && (!workspace || workspace_bytes < need)) return SPV_ERR_WORKSPACE;
 
   AttnParams p{};
@@ -1264,6 +1293,8 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
   p.tables = block_tables;
   p.seq_ids = seq_ids;
   p.start = start_pos;
+  p.lens = seq_lens;
+  p.ctr = ctr;
   p.maxb = max_blocks_per_seq;
   p.B = B;
   p.C = C;
@@ -1282,7 +1313,7 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
   p.max_pages = (max_ctx + block_size - 1) / block_size;
   p.scale_log2 = scale * kLog2e;
   if (need > 0) {
-    const size_t rows = partial_rows(pl, B, C, num_q_heads, num_kv_heads);
+    const size_t rows = partial_rows(pl, B, C, num_q_heads, num_kv_heads, nw_layout);
     char* ws = static_cast<char*>(workspace);
     p.counters = reinterpret_cast<int*>(ws);
     p.part_ml = reinterpret_cast<float*>(ws + SPV_ATTN_COUNTER_BYTES);
@@ -1316,6 +1347,19 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
     SPV_CHECK_LAUNCH();
   }
   return SPV_OK;
+}
+
+extern "C" {
+
+int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, const void* v_pool, int kv_dtype,
+                    const float* kv_scales, const int32_t* block_tables, int32_t max_blocks_per_seq,
+                    const int32_t* seq_ids, const int32_t* start_pos, const int32_t* seq_lens, int32_t* ctr,
+                    int32_t B, int32_t C, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                    int32_t block_size, int32_t layer, int32_t capacity, int32_t max_ctx, float scale,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  return spv::verify_attn_impl(out, q, q_dtype, k_pool, v_pool, kv_dtype, kv_scales, block_tables, max_blocks_per_seq,
+                          seq_ids, start_pos, seq_lens, ctr, B, C, num_q_heads, num_kv_heads, head_dim, block_size,
+                          layer, capacity, max_ctx, scale, workspace, workspace_bytes, false, stream);
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@ SPV_ERR_WORKSPACE = -3
 SPV_ERR_UNSUPPORTED = -4
 SPV_CTR_WORDS = 8
 CTR_TOP, CTR_EXHAUSTED, CTR_SLOWPATH, CTR_PUSHED = 0, 1, 2, 3
+CTR_OVERFLOW, CTR_BAD_READ = 6, 7  # sticky error words (see include/specverify.h)
 
 SPV_F32, SPV_BF16, SPV_F16, SPV_FP8E4M3 = 0, 1, 2, 3
 _DTYPE_CODE = {torch.float32: SPV_F32, torch.bfloat16: SPV_BF16, torch.float16: SPV_F16}
@@ -53,7 +54,7 @@ SIGNATURES = {
     "spv_kv_gather": (I, [P, P, I, P, P, I, I, I, I, I, I, I, I, P, P]),
     "spv_kv_read_blocks": (I, [P, I, I, P, I, I, I, I, I, I, P, P]),
     "spv_verify_attn_workspace_bytes": (S, [I, I, I, I, I, I, I]),
-    "spv_verify_attn": (I, [P, P, I, P, P, I, P, P, I, P, P, I, I, I, I, I, I, I, I, I, F, P, S, P]),
+    "spv_verify_attn": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P, S, P]),
     "spv_verify_sample_workspace_bytes": (S, [I, I, I]),
     "spv_verify_sample": (I, [P, P, I, F, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, I, P, S, P]),
     "spv_logits_to_probs": (I, [P, P, I, I, F, P]),

@@ -83,9 +83,13 @@ def verify_attention(query_3d: torch.Tensor, kv: PagedKVCache, layer: int,
                                                           kv.block_size, int(max_ctx))
     ws = _workspace.get(ws_bytes, kv.device) if ws_bytes else None
     call("spv_verify_attn", ptr(out), ptr(q), _hip.dtype_code(q.dtype), ptr(kv.k_pool), ptr(kv.v_pool),
-         kv._dt, ptr(kv.scales), ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t), B, chunk,
+         kv._dt, ptr(kv.scales), ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t),
+         ptr(kv.lens_dev), ptr(kv.allocator.ctr), B, chunk,
          hq, kv.num_kv_heads, d, kv.block_size, int(layer), kv.allocator.capacity, int(max_ctx),
          scale, ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
+    # A read of unwritten keys is flagged on the device and raised (IndexError)
+    # at the next metadata query, without a synchronisation here.
+    kv._stale = True
     return out
 
 

@@ -193,10 +193,25 @@ class PagedKVCache:
             self.allocator._stale = True
             self.allocator._refresh()
             self._stale = False
-            exhausted = int(self.allocator.ctr[_hip.CTR_EXHAUSTED].item())
-            if exhausted:
-                self.allocator.ctr[_hip.CTR_EXHAUSTED] = 0
+            ctr = self.allocator.ctr.tolist()
+            words = (_hip.CTR_EXHAUSTED, _hip.CTR_OVERFLOW, _hip.CTR_BAD_READ)
+            if not any(ctr[w] for w in words):
+                return
+            # One error is raised; the others set since the last query follow
+            # from it (an exhausted or full table leaves keys unwritten that a
+            # later attention then reads), so all are cleared.
+            for w in words:
+                if ctr[w]:
+                    self.allocator.ctr[w] = 0
+            if ctr[_hip.CTR_EXHAUSTED]:
                 raise _exhausted(self.allocator.capacity)
+            if ctr[_hip.CTR_OVERFLOW]:
+                raise IndexError("batch entry {}: the chunk needs more than max_blocks_per_seq={} blocks; "
+                                 "its table was filled and the tokens beyond it were not written".format(
+                                     ctr[_hip.CTR_OVERFLOW] - 1, self._maxb))
+            raise IndexError("batch entry {}: verify attention read positions that were never written "
+                             "(or a block id outside the pool, or beyond max_ctx)".format(
+                                 ctr[_hip.CTR_BAD_READ] - 1))
 
     def _grow_rows(self, n: int) -> None:
         if n <= self._max_seqs:

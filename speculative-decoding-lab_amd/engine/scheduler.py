@@ -13,9 +13,14 @@ from .kv import PagedKVCache
 
 def bytes_per_block(num_layers: int, block_size: int, num_kv_heads: int, head_dim: int,
                     dtype: torch.dtype) -> int:
-    """Bytes of one physical block across all layers, K + V (scheduler.py:351-362)."""
+    """Bytes of one physical block across all layers, K + V (scheduler.py:351-362).
+
+    An fp8 (e4m3) pool, which the reference does not have, also holds one fp32
+    scale per (layer, block, K | V): 8 bytes per layer.
+    """
     itemsize = torch.empty((), dtype=dtype).element_size()
-    return 2 * num_layers * block_size * num_kv_heads * head_dim * itemsize
+    scales = 8 * num_layers if dtype == getattr(torch, "float8_e4m3fn", None) else 0
+    return 2 * num_layers * block_size * num_kv_heads * head_dim * itemsize + scales
 
 
 def build_kv(model: Any, engine_cfg: EngineConfig, device: torch.device) -> PagedKVCache:

@@ -39,3 +39,12 @@ def test_workload_lengths_are_seeded_and_in_range():
     a, _ = bench.workload_lens(0)
     b, _ = bench.workload_lens(0)
     assert a == b and len(a) == bench.B and all(256 <= L <= 4096 for L in a)
+
+
+def test_replicas_are_distinct_context_draws_near_the_distribution_mean():
+    rl = bench.replica_lens(0)
+    assert len(rl) == bench.REPLICAS and rl[0] == bench.workload_lens(0)[0]
+    assert len({tuple(r) for r in rl}) == bench.REPLICAS
+    mean = sum(sum(r) for r in rl) / (bench.REPLICAS * bench.B)
+    # U[256, 4096] has mean 2176; 256 draws put the sample mean within ~6%
+    assert abs(mean - 2176) < 0.06 * 2176, mean

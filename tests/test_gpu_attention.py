@@ -337,3 +337,24 @@ def test_pieces_longer_than_the_block_id_window(cuda, d):
     q = torch.randn(B, C, Hq, d, generator=g).to(torch.bfloat16)
     out = verify_attention(q.to(cuda), gpu, 0, list(range(B)), lens, max(lens) + C)
     _bf16_check(out, ref_attn.extend_attention_dense(q, keys, values, lens, Hq))
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64)])
+def test_reading_unwritten_keys_is_reported(cuda, dtype, d):
+    """verify_attention over a chunk that was never appended (start + chunk
+    beyond the sequence's length, here also beyond its blocks, so a table slot
+    is unset) reads block 0 instead of faulting and raises IndexError at the
+    next metadata query; the flag is cleared by raising it. The MFMA path
+    (bf16) and the VALU path (fp32)."""
+    lens, C, Hq = [40, 20], 6, 4
+    gpu, keys, values = _dense_pool(cuda, lens, C, 2, d, 16, dtype, seed=5)
+    q = torch.randn(2, C, Hq, d).to(dtype).to(cuda)
+    ok = verify_attention(q, gpu, 0, [0, 1], lens, max(lens) + C)
+    assert gpu.seq_lengths == [L + C for L in lens]  # a correct call raises nothing
+    verify_attention(q, gpu, 0, [0, 1], [40, 40], 46)  # sequence 1 holds 26 keys in 2 blocks
+    torch.cuda.synchronize()
+    with pytest.raises(IndexError):
+        gpu.seq_lengths
+    assert gpu.seq_lengths == [L + C for L in lens]
+    again = verify_attention(q, gpu, 0, [0, 1], lens, max(lens) + C)
+    assert torch.equal(ok, again)

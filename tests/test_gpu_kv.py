@@ -486,3 +486,38 @@ def test_later_layers_write_without_allocating(cuda, exhaust):
                 want = torch.stack([torch.cat([cpu.k[layer, b] for b in cpu.block_tables[s]])[:n],
                                     torch.cat([cpu.v[layer, b] for b in cpu.block_tables[s]])[:n]])
                 assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("chunk,maxb", [(6, 3), (40, 12)])
+def test_table_width_caps_a_device_append_and_reports_it(cuda, chunk, maxb):
+    """A device-side append whose chunk needs more blocks than a table holds
+    gets the blocks that fit, writes only the tokens inside them, and the next
+    metadata query raises IndexError; the state equals the oracle's after the
+    same writes cut at max_blocks_per_seq * block_size. chunk 6 runs the
+    one-launch append, chunk 40 (11 blocks) the allocation + copy kernels."""
+    bs, cap, H, d = 4, 32, 2, 8
+    gpu = PagedKVCache(1, H, d, cap, bs, cuda, torch.float32, max_seqs=2, max_blocks_per_seq=maxb)
+    cpu = ref.PagedKVCache(1, H, d, cap, bs)
+    for s in (0, 1):
+        gpu.add_sequence(s)
+        cpu.add_sequence(s)
+    g = torch.Generator().manual_seed(chunk)
+    k = torch.randn(2, chunk, H, d, generator=g)
+    v = torch.randn(2, chunk, H, d, generator=g)
+    starts = [10, 0]  # sequence 0 overflows its table, sequence 1 fits
+    fit = maxb * bs - starts[0]
+    assert 0 < fit < chunk and starts[1] + chunk <= maxb * bs
+    gpu.write_block_device(0, torch.tensor([0, 1], dtype=torch.int32, device=cuda),
+                           torch.tensor(starts, dtype=torch.int32, device=cuda), k.to(cuda), v.to(cuda))
+    with pytest.raises(IndexError):
+        gpu.seq_lengths
+    cpu.write_block(0, [0], [starts[0]], k[:1, :fit], v[:1, :fit])
+    cpu.write_block(0, [1], [starts[1]], k[1:], v[1:])
+    _same_state(gpu, cpu)
+    assert gpu.seq_lengths == [maxb * bs, chunk]
+    for s in (0, 1):
+        n = gpu.seq_lengths[s]
+        got = gather_ctx(gpu, 0, s, n).cpu()
+        want = torch.stack((torch.cat([cpu.key_map(0, [p])[0] for p in cpu.block_tables[s]])[:n],
+                            torch.cat([cpu.value_map(0, [p])[0] for p in cpu.block_tables[s]])[:n]))
+        assert torch.equal(got[:, starts[s]:], want[:, starts[s]:])

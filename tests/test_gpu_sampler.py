@@ -12,8 +12,12 @@ Token ids, accept lengths and commit outputs must be identical (bit-exact):
 
 Probabilities computed from logits on the GPU differ from torch's CPU softmax in
 the last bits; a decision can only differ when ``u`` lies within ~1e-6 of
-``p/q`` or two race keys tie to ~1e-6. The workload test reports the smallest
-such margin and requires the ids to match.
+``p/q`` or two race keys tie to ~1e-6. The workload test computes the smallest
+such margin on the oracle's side, prints it, requires it above 1e-6 (so the
+seed does not sit on a rounding boundary), and requires the ids to match.
+With probabilities as inputs the arithmetic is exactly the reference's: crafted
+near-ties (race keys equal, or one fp32 ulp apart, at the residual and bonus
+rows) take the exact re-race and must return torch's own argmax.
 """
 
 from __future__ import annotations
@@ -109,11 +113,36 @@ def _proposals(draft, T, g):
     return torch.multinomial(q.reshape(-1, V), 1, generator=g).reshape(B, gamma)
 
 
+def _decision_margins(target, draft, x, u, noise, T):
+    """Smallest |u - a| over the examined positions and smallest relative gap
+    between the two best race keys over the sequences, as the oracle computes
+    them (T > 0)."""
+    p, q = S.logits_to_probs(target, T), S.logits_to_probs(draft, T)
+    B, gamma = x.shape
+    min_u, min_gap = float("inf"), float("inf")
+    for b in range(B):
+        k = gamma
+        for j in range(gamma):
+            a = S.acceptance_probability(p[b, j], q[b, j], int(x[b, j]))
+            min_u = min(min_u, abs(float(u[b, j]) - a))
+            if not float(u[b, j]) < a:
+                k = j
+                break
+        r = S.residual_distribution(p[b, k], q[b, k]) if k < gamma else p[b, gamma]
+        top = torch.topk(r / noise[b], 2).values
+        min_gap = min(min_gap, float((top[0] - top[1]) / top[0]))
+    return min_u, min_gap
+
+
 @pytest.mark.parametrize("T", [1.0, 0.0])
 def test_fused_sampler_workload(cuda, T):
     g, target, draft, u, noise = _workload(42 if T else 43)
     x = _proposals(draft, T, g)
     want = S.verify_from_logits(target, draft, x, u, noise, T)
+    if T > 0:
+        min_u, min_gap = _decision_margins(target, draft, x, u, noise, T)
+        print("decision margins: min |u - a| = {:.3e}, min race top-2 gap = {:.3e}".format(min_u, min_gap))
+        assert min_u > 1e-6 and min_gap > 1e-6, (min_u, min_gap)
     res = es.verify_sample(target.to(cuda), draft.to(cuda), x.to(cuda), u.to(cuda),
                            noise.to(cuda) if T > 0 else None, T)
     got = res.accepted_lists()
@@ -122,6 +151,59 @@ def test_fused_sampler_workload(cuda, T):
     assert lens == [len(w) - 1 for w in want]
     if T > 0:
         assert 0 < sum(lens) < 5 * 64  # both accepts and rejections occur
+
+
+def _tie_case(seed, V, reject_at, relation, gamma=3):
+    """One sequence whose race has two keys tied at fp32 level: ``relation`` 0
+    makes the keys of indices a < b equal (torch.argmax takes a), +1 puts b one
+    ulp above a, -1 one ulp below. ``reject_at`` < gamma races the residual of
+    that row (u = 1 rejects it), gamma races the bonus row (u = 0 accepts all)."""
+    g = torch.Generator().manual_seed(seed)
+    p = torch.softmax(torch.randn(gamma + 1, V, generator=g) * 2, -1)
+    q = torch.softmax(torch.randn(gamma, V, generator=g) * 2, -1)
+    x = torch.randint(0, V, (1, gamma), generator=g)
+    u = torch.zeros(1, gamma)
+    if reject_at < gamma:
+        u[0, reject_at] = 1.0
+    noise = torch.empty(V).exponential_(1, generator=g)
+    k = reject_at
+    cand = torch.randperm(V, generator=g)[:64].tolist()
+    a = min(cand[:2])
+    if k < gamma:
+        q[k, cand] = 0.0  # residual mass at every candidate index
+        r = S.residual_distribution(p[k], q[k])
+    else:
+        r = p[gamma]
+    noise[a] = r[a] * 1e-10  # a's key ~1e10: above every other key by far
+    key_a = r[a] / noise[a]
+    want = key_a if relation == 0 else torch.nextafter(key_a, key_a * (1 + relation))
+    for b in cand:
+        if b <= a:
+            continue
+        # E_b such that r_b / E_b is exactly `want` (not every quotient is reachable)
+        e_b = (r[b] / want).to(torch.float32)
+        for _ in range(16):
+            kb = r[b] / e_b
+            if kb == want:
+                break
+            e_b = torch.nextafter(e_b, e_b * (2.0 if kb > want else 0.5))
+        if r[b] / e_b == want:
+            noise[b] = e_b
+            break
+    else:
+        raise AssertionError("could not place the tie")
+    assert S.race_argmax(r, noise) == (b if relation > 0 else a)
+    return p.unsqueeze(0), q.unsqueeze(0), x.to(torch.int32), u, noise.unsqueeze(0)
+
+
+@pytest.mark.parametrize("reject_at", [0, 2, 3])
+@pytest.mark.parametrize("relation", [0, 1, -1])
+def test_near_tie_race_takes_the_exact_path(cuda, reject_at, relation):
+    p, q, x, u, noise = _tie_case(100 + 3 * reject_at + relation, 151936, reject_at, relation)
+    want = S.batch_accept_noise(p, q, x, u, noise)
+    res = es.verify_sample(p.to(cuda), q.to(cuda), x.to(cuda), u.to(cuda), noise.to(cuda), 1.0,
+                           is_probs=True)
+    assert res.accepted_lists() == want
 
 
 def test_fused_sampler_probs_mode_matches_batch_accept(cuda):
