@@ -195,7 +195,9 @@ def make_step(w):
     from engine.spec_scheduler import _new_result, verify_sample
 
     kv = w["kv"]
-    res = _new_result(B, GAMMA, kv.device)
+    # one result per replica: a rewind applies the lengths sampled against its
+    # own replica's start positions
+    results = [_new_result(B, GAMMA, kv.device) for _ in range(REPLICAS)]
 
     def append(r):
         kv.write_block_device(0, w["sids"][r], w["start"][r], w["k_new"], w["v_new"])
@@ -206,24 +208,21 @@ def make_step(w):
     def sample(t, r=0):
         target, draft, proposals = w["logits"][t]
         verify_sample(target, draft, proposals, w["u"], w["noise"], 1.0,
-                      start_pos=w["start"][r], result=res, validate=False)
+                      start_pos=w["start"][r], result=results[r], validate=False)
 
     def rewind(r):
-        # the new lengths were sampled against replica r's start positions
-        kv.rewind_device(w["sids"][r], res.new_len, res.finished)
+        kv.rewind_device(w["sids"][r], results[r].new_len, results[r].finished)
 
     def step(i, events=None):
         r, t = i % REPLICAS, i % LOGIT_SETS
         append(r)
         if events is not None:
-            events[0].record()
+            events.arm()
         attend(r)
-        if events is not None:
-            events[1].record()
         sample(t, r)
         rewind(r)
 
-    return step, {"append": append, "attend": attend, "sample": sample, "rewind": rewind}, res
+    return step, {"append": append, "attend": attend, "sample": sample, "rewind": rewind}, results[0]
 
 
 def graph_of(fn, reps, torch):
@@ -278,14 +277,51 @@ def sleep_cycles_per_ms(torch):
     return 2_000_000 / max(a.elapsed_time(b), 1e-3)
 
 
+class KernelEvents:
+    """A start / stop hipEvent pair for one attention call, armed through the
+    library's timing hook (spv_time_next_attention): the HIP runtime records
+    the kernel's own start and end timestamps into them, on the stream the
+    kernel runs on -- the interval rocprofv3 reports for the kernel."""
+
+    def __init__(self):
+        import ctypes
+
+        from engine import _hip
+
+        self.lib = _hip.lib()  # resolves the HIP runtime already in the process
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+        for e in self.ev:
+            if self.lib.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+
+    def arm(self):
+        self.lib.spv_time_next_attention(self.ev[0], self.ev[1])
+
+    def elapsed_ms(self):
+        import ctypes
+
+        ms = ctypes.c_float()
+        if self.lib.hipEventElapsedTime(ctypes.byref(ms), self.ev[0], self.ev[1]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def close(self):
+        for e in self.ev:
+            self.lib.hipEventDestroy(e)
+
+
 def timed_steps(step, steps, torch, host_us_per_step=400.0):
     """Exactly ``steps`` steps on the current stream, queued behind a bounded
     device-side delay long enough for the host to enqueue all of them, so the
-    GPU never waits on a launch. Events bracket the region and every attention
-    call. Returns (ms per step, per-call attention ms list)."""
+    GPU never waits on a launch. torch events bracket the region; every
+    attention call's kernel records its own start / end into a HIP event pair.
+    Returns (ms per step, per-call attention kernel ms list)."""
     rate = sleep_cycles_per_ms(torch)
     delay_ms = min(400.0, 5.0 + steps * host_us_per_step / 1000.0)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    ev = [KernelEvents() for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -299,7 +335,10 @@ def timed_steps(step, steps, torch, host_us_per_step=400.0):
     if queued_ms > delay_ms:
         print("bench: warning: the host took {:.1f} ms to queue the timed steps, more than the {:.1f} ms "
               "delay ahead of them".format(queued_ms, delay_ms), file=sys.stderr, flush=True)
-    return start.elapsed_time(end) / steps, [a.elapsed_time(b) for a, b in ev]
+    attn_ms = [e.elapsed_ms() for e in ev]
+    for e in ev:
+        e.close()
+    return start.elapsed_time(end) / steps, attn_ms
 
 
 def cpu_baseline(w, dev, budget_s=12.0):

@@ -200,6 +200,14 @@ int spv_verify_attn(void* out, const void* q, int q_dtype,
                     int32_t max_ctx, float scale, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Kernel timing hook (no counterpart in the reference; for measurement): the
+ * next spv_verify_attn / spv_verify_attn_static call made on this host thread
+ * records the start of its first kernel into start_event and the end of its
+ * last kernel into stop_event (hipEvent_t handles the caller created), from
+ * the kernels' own dispatch timestamps -- the interval a profiler reports,
+ * without the queue gaps around it. The arming ends with that call. */
+int spv_time_next_attention(void* start_event, void* stop_event);
+
 /* -------------------------------------------------------------- sampling */
 
 /* Workspace needed by spv_verify_sample. Its first SPV_SAMPLE_COUNTER_BYTES

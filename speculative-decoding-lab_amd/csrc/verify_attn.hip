@@ -26,6 +26,8 @@
 // a (sequence, kv head, row group, split) grid and its own merge kernel.
 #include <math.h>
 
+#include <hip/hip_ext.h>
+
 #include "spv_common.h"
 
 using namespace spv;
@@ -1200,22 +1202,39 @@ int persistent_wgs() {
   return cached[slot];
 }
 
+// Events armed by spv_time_next_attention for the next attention call made on
+// this host thread: the start of its first kernel and the end of its last are
+// recorded from the kernels' own dispatch timestamps.
+struct TimingArm {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+thread_local TimingArm g_arm;
+
+// One kernel of an attention call; `first` / `last` place the armed events.
+template <typename K>
+void launch_attn(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t s, bool first, bool last,
+                 const AttnParams& p) {
+  hipEvent_t e0 = first ? g_arm.start : nullptr, e1 = last ? g_arm.stop : nullptr;
+  if (e0 || e1) hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)smem, s, e0, e1, 0, p);
+  else hipLaunchKernelGGL(kernel, grid, block, smem, s, p);
+}
+
 template <int QT, int KT>
-void launch_valu(const AttnParams& p, dim3 grid, hipStream_t s) {
+void launch_valu(const AttnParams& p, dim3 grid, hipStream_t s, bool last) {
   const size_t smem = (size_t)(64 * p.d + 32 * p.d + 64 * 17 + 3 * 64) * sizeof(float);
   if (smem > 65536)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_valu_kernel<QT, KT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-  hipLaunchKernelGGL((attn_valu_kernel<QT, KT>), grid, dim3(kAttnThreads), smem, s, p);
+  launch_attn(attn_valu_kernel<QT, KT>, grid, dim3(kAttnThreads), smem, s, true, last, p);
 }
 
 template <int QT>
-int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s) {
+int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s, bool last) {
   switch (kv_dtype) {
-    case SPV_F32: launch_valu<QT, SPV_F32>(p, grid, s); break;
-    case SPV_BF16: launch_valu<QT, SPV_BF16>(p, grid, s); break;
-    case SPV_F16: launch_valu<QT, SPV_F16>(p, grid, s); break;
-    case SPV_FP8E4M3: launch_valu<QT, SPV_FP8E4M3>(p, grid, s); break;
+    case SPV_F32: launch_valu<QT, SPV_F32>(p, grid, s, last); break;
+    case SPV_BF16: launch_valu<QT, SPV_BF16>(p, grid, s, last); break;
+    case SPV_F16: launch_valu<QT, SPV_F16>(p, grid, s, last); break;
+    case SPV_FP8E4M3: launch_valu<QT, SPV_FP8E4M3>(p, grid, s, last); break;
     default: return SPV_ERR_ARG;
   }
   return SPV_OK;
@@ -1225,10 +1244,10 @@ template <int D, bool BAL, int KT>
 void launch_mfma_mode(const AttnParams& p, int nt, hipStream_t s, dim3 grid, size_t smem) {
   const dim3 blk(kMfmaThreads);
   switch (nt) {
-    case 1: hipLaunchKernelGGL((attn_mfma_kernel<1, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_mfma_kernel<2, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_mfma_kernel<3, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
-    default: hipLaunchKernelGGL((attn_mfma_kernel<4, D, SPV_BF16, BAL, KT>), grid, blk, smem, s, p); break;
+    case 1: launch_attn(attn_mfma_kernel<1, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
+    case 2: launch_attn(attn_mfma_kernel<2, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
+    case 3: launch_attn(attn_mfma_kernel<3, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
+    default: launch_attn(attn_mfma_kernel<4, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
   }
 }
 
@@ -1270,6 +1289,9 @@ int spv::verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_p
                      int32_t B, int32_t C, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int32_t layer, int32_t capacity, int32_t max_ctx, float scale,
                      void* workspace, size_t workspace_bytes, bool exact_layout, void* stream) {
+  struct Disarm {
+    ~Disarm() { g_arm = TimingArm{}; }
+  } disarm;  // armed timing events serve this call only, whatever its outcome
   if (!out || !q || !k_pool || !v_pool || !block_tables || !seq_ids || !start_pos) return SPV_ERR_ARG;
   if (q_dtype != SPV_F32 && q_dtype != SPV_BF16 && q_dtype != SPV_F16) return SPV_ERR_ARG;
   if (dtype_size(kv_dtype) == 0) return SPV_ERR_ARG;
@@ -1328,28 +1350,37 @@ int spv::verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_p
     return SPV_OK;
   }
   const dim3 grid(pl.max_splits, num_kv_heads * pl.nrg, B);
+  const bool merge = pl.max_splits > 1;
   int rc;
   switch (q_dtype) {
-    case SPV_F32: rc = launch_valu_q<SPV_F32>(p, kv_dtype, grid, s); break;
-    case SPV_BF16: rc = launch_valu_q<SPV_BF16>(p, kv_dtype, grid, s); break;
-    default: rc = launch_valu_q<SPV_F16>(p, kv_dtype, grid, s); break;
+    case SPV_F32: rc = launch_valu_q<SPV_F32>(p, kv_dtype, grid, s, !merge); break;
+    case SPV_BF16: rc = launch_valu_q<SPV_BF16>(p, kv_dtype, grid, s, !merge); break;
+    default: rc = launch_valu_q<SPV_F16>(p, kv_dtype, grid, s, !merge); break;
   }
   if (rc != SPV_OK) return rc;
   SPV_CHECK_LAUNCH();
-  if (pl.max_splits > 1) {
+  if (merge) {
     const int gx = (p.G * head_dim + kAttnThreads - 1) / kAttnThreads;
-    const dim3 mgrid(gx, num_kv_heads, B);
+    const dim3 mgrid(gx, num_kv_heads, B), mblk(kAttnThreads);
     switch (q_dtype) {
-      case SPV_F32: hipLaunchKernelGGL(attn_merge_kernel<SPV_F32>, mgrid, dim3(kAttnThreads), 0, s, p); break;
-      case SPV_BF16: hipLaunchKernelGGL(attn_merge_kernel<SPV_BF16>, mgrid, dim3(kAttnThreads), 0, s, p); break;
-      default: hipLaunchKernelGGL(attn_merge_kernel<SPV_F16>, mgrid, dim3(kAttnThreads), 0, s, p); break;
+      case SPV_F32: launch_attn(attn_merge_kernel<SPV_F32>, mgrid, mblk, 0, s, false, true, p); break;
+      case SPV_BF16: launch_attn(attn_merge_kernel<SPV_BF16>, mgrid, mblk, 0, s, false, true, p); break;
+      default: launch_attn(attn_merge_kernel<SPV_F16>, mgrid, mblk, 0, s, false, true, p); break;
     }
     SPV_CHECK_LAUNCH();
   }
   return SPV_OK;
 }
 
+
+
 extern "C" {
+
+int spv_time_next_attention(void* start_event, void* stop_event) {
+  g_arm.start = static_cast<hipEvent_t>(start_event);
+  g_arm.stop = static_cast<hipEvent_t>(stop_event);
+  return SPV_OK;
+}
 
 int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, const void* v_pool, int kv_dtype,
                     const float* kv_scales, const int32_t* block_tables, int32_t max_blocks_per_seq,

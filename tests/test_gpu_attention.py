@@ -358,3 +358,36 @@ def test_reading_unwritten_keys_is_reported(cuda, dtype, d):
     assert gpu.seq_lengths == [L + C for L in lens]
     again = verify_attention(q, gpu, 0, [0, 1], lens, max(lens) + C)
     assert torch.equal(ok, again)
+
+
+def test_timing_hook_records_the_kernel_and_changes_nothing(cuda):
+    """spv_time_next_attention: the next attention call records its kernels'
+    start and end into the caller's HIP events (a positive interval below the
+    whole call's wall time) and computes exactly what an untimed call does; the
+    arming serves one call only."""
+    import ctypes
+
+    from engine import _hip
+
+    lib = _hip.lib()
+    lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    lens, C, Hq = [300, 2000, 17], 6, 12
+    for dtype, d in ((torch.bfloat16, 128), (torch.float32, 64)):  # one kernel; two (split + merge)
+        gpu, keys, values = _dense_pool(cuda, lens, C, 2, d, 16, dtype, seed=8)
+        q = torch.randn(3, C, Hq, d).to(dtype).to(cuda)
+        plain = verify_attention(q, gpu, 0, [0, 1, 2], lens, max(lens) + C)
+        ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+        for e in ev:
+            assert lib.hipEventCreate(ctypes.byref(e)) == 0
+        assert lib.spv_time_next_attention(ev[0], ev[1]) == 0
+        timed = verify_attention(q, gpu, 0, [0, 1, 2], lens, max(lens) + C)
+        after = verify_attention(q, gpu, 0, [0, 1, 2], lens, max(lens) + C)  # not armed any more
+        torch.cuda.synchronize()
+        ms = ctypes.c_float()
+        assert lib.hipEventElapsedTime(ctypes.byref(ms), ev[0], ev[1]) == 0
+        assert 0.0 < ms.value < 50.0
+        assert torch.equal(plain, timed) and torch.equal(plain, after)
+        for e in ev:
+            lib.hipEventDestroy(e)
