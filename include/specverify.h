@@ -200,6 +200,29 @@ int spv_verify_attn(void* out, const void* q, int q_dtype,
                     int32_t max_ctx, float scale, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* spv_verify_attn with no allocation and no caller workspace. No counterpart
+ * in the reference: it serves callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The kernels keep their counters and partials in the library's
+ * own static device array of spv_verify_attn_static_max_bytes() bytes (24 MiB;
+ * one per GPU, held until the process ends); a call that needs more (see
+ * spv_verify_attn_workspace_bytes: the VALU path with long split contexts) is
+ * rejected with SPV_ERR_WORKSPACE before anything is enqueued. Every call on
+ * one GPU shares that array: calls that overlap on a GPU (other streams,
+ * other host threads) race and give wrong results; order them. Arguments and
+ * results are spv_verify_attn's. */
+size_t spv_verify_attn_static_max_bytes(void);
+int spv_verify_attn_static(void* out, const void* q, int q_dtype,
+                           const void* k_pool, const void* v_pool, int kv_dtype,
+                           const float* kv_scales, const int32_t* block_tables,
+                           int32_t max_blocks_per_seq, const int32_t* seq_ids,
+                           const int32_t* start_pos, const int32_t* seq_lens,
+                           int32_t* ctr, int32_t B, int32_t C,
+                           int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t block_size, int32_t layer,
+                           int32_t capacity, int32_t max_ctx, float scale,
+                           void* stream);
+
 /* Kernel timing hook (no counterpart in the reference; for measurement): the
  * next spv_verify_attn / spv_verify_attn_static call made on this host thread
  * records the start of its first kernel into start_event and the end of its

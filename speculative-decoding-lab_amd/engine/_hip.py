@@ -56,6 +56,8 @@ SIGNATURES = {
     "spv_verify_attn_workspace_bytes": (S, [I, I, I, I, I, I, I]),
     "spv_verify_attn": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P, S, P]),
     "spv_time_next_attention": (I, [P, P]),
+    "spv_verify_attn_static_max_bytes": (S, []),
+    "spv_verify_attn_static": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P]),
     "spv_verify_sample_workspace_bytes": (S, [I, I, I]),
     "spv_verify_sample": (I, [P, P, I, F, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, I, P, S, P]),
     "spv_logits_to_probs": (I, [P, P, I, I, F, P]),
