@@ -634,11 +634,39 @@ def draft_decode(dev, seed=0):
     gw = graph_of(lambda: [append(i) for i in range(n)], 1, torch)
     app_us = time_graph(gw, 5, torch) * 1000.0 / n
     nbytes = attention_bytes(lens, 1, hq, hkv, d, BS)
+    # Batched draft sampling of one step (B rows of V draft logits, T = 1) and
+    # one whole draft step at the draft model's depth as a captured graph:
+    # per layer the one-token append and decode attention (layers cycle over
+    # the replicas' pages, so each reads HBM), then the step's sampling.
+    from engine.spec_scheduler import draft_sample
+
+    logits = [torch.randn(B, VOCAB, generator=gd, device=dev) * 2.0 for _ in range(2)]
+    noise = [torch.empty(B, VOCAB, device=dev).exponential_(1, generator=gd) for _ in range(2)]
+    toks = torch.empty(B, dtype=torch.int32, device=dev)
+    samp = lambda i: draft_sample(logits[i % 2], 1.0, noise[i % 2], out=toks)
+    gs = graph_of(lambda: [samp(i) for i in range(n)], 1, torch)
+    samp_us = time_graph(gs, 5, torch) * 1000.0 / n
+    depth = 24
+
+    def draft_step(i):
+        for layer in range(depth):
+            r = (i * depth + layer) % reps
+            kv.write_block_device(0, sids[r], st, kn, vn, alloc=False)
+            verify_attention(q, kv, 0, sids[r], st, max_ctx, out=out)
+        samp(i)
+
+    gstep = graph_of(lambda: [draft_step(i) for i in range(2)], 1, torch)
+    step_us = time_graph(gstep, 5, torch) * 1000.0 / 2
     res = {"workload": "Qwen2.5-0.5B-shaped draft decode: batch 32, one query row, 14q/2kv heads, head_dim 64, "
-                       "block 16, bf16 KV, the verify workload's contexts (U[256,4096], seed 0); 8 replicas",
+                       "block 16, bf16 KV, the verify workload's contexts (U[256,4096], seed 0); 8 replicas; "
+                       "draft sampling of 32 rows over V=151936 at T=1; a draft step = 24 layers of append + "
+                       "decode attention, then the sampling, as one captured graph",
            "attn_us": round(attn_us, 2), "attn_gbs": round(nbytes / (attn_us * 1e-6) / 1e9, 1),
-           "attn_bytes_per_call": nbytes, "append_us": round(app_us, 2)}
-    del kv, ga, gw
+           "attn_bytes_per_call": nbytes, "append_us": round(app_us, 2),
+           "sample_us": round(samp_us, 2),
+           "sample_gbs": round(2 * B * VOCAB * 4 / (samp_us * 1e-6) / 1e9, 1),
+           "step_24_layers_us": round(step_us, 1)}
+    del kv, ga, gw, gs, gstep
     torch.cuda.empty_cache()
     return res
 

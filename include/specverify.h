@@ -271,6 +271,21 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs,
                       double* accept_prob, int32_t decide_only,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* One draft step of the draft loop (engine/spec_scheduler.py:243-252): for
+ * every row b of the draft logits (row b at logits + b * row_stride, V fp32
+ * entries), out_tokens[b * out_stride] = sample_token(logits_to_probs(row))
+ * (specdec/sampler.py:19-36, 59-69): argmax over i of q_i / exp_noise[b][i]
+ * (q = softmax(z / max(T, 1e-12)), caller-supplied Exp(1) rows, lowest index
+ * on ties), or, for temperature <= 0, the first-index argmax of the logits
+ * (exp_noise not read). One launch for the batch; the workspace's first
+ * SPV_SAMPLE_COUNTER_BYTES hold arrival counters that must be zero when it is
+ * first used and are zero after every call. V <= 4,194,304. */
+size_t spv_draft_sample_workspace_bytes(int32_t B, int32_t V);
+int spv_draft_sample(const float* logits, int64_t row_stride, float temperature,
+                     const float* exp_noise, int32_t B, int32_t V,
+                     int32_t* out_tokens, int32_t out_stride, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 /* logits_to_probs (specdec/sampler.py:19-36) on `rows` rows of V fp32 logits. */
 int spv_logits_to_probs(const float* logits, float* probs, int32_t rows, int32_t V,
                         float temperature, void* stream);

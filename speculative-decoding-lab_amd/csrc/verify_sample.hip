@@ -709,6 +709,230 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
   if (arrive_last(ws.cnt_race + b, nch, &s_last)) finalize_seq(a, cm, ws, b, info);
 }
 
+// ------------------------------------------------------ draft proposals
+// One draft step of the reference's draft loop (engine/spec_scheduler.py:
+// 243-252): for every row b, token[b] = sample_token(logits_to_probs(z_b))
+// (specdec/sampler.py:19-36, 59-69) = argmax(q_b / E_b) with the caller's
+// Exp(1) row E_b, or the first-index argmax of z_b when greedy. grid (chunks,
+// B): each chunk workgroup reads its slice of z_b and E_b once and keeps the
+// slice's max m_c, sum of exp(x - m_c) and the top two keys exp(x - m_c) / E
+// (x = z / T); the last workgroup of a row to arrive combines them (keys
+// rescaled by exp(m_c - M)) and, when the two best keys are within kTieRel or
+// a NaN is involved, re-races the row exactly with torch's arithmetic, q =
+// exp(x - M) / S, key = q / E. Greedy rows keep the slice's argmax instead.
+struct DraftPart {
+  float m, s, v1, v2;  // slice max, sum exp(x - m), best two keys (relative to m)
+  int i1, i2, pad0, pad1;
+};  // 32 bytes: two coherent 16-byte stores
+
+struct DraftArgs {
+  const float* logits;
+  const float* noise;
+  int32_t* out;
+  DraftPart* part;
+  int* cnt;
+  long long row_stride;
+  int B, V, out_stride, greedy;
+  float tf;
+};
+
+template <bool UNIT>
+__global__ __launch_bounds__(kThreads) void draft_race_kernel(DraftArgs a) {
+  const int c = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
+  const float* z = a.logits + (size_t)b * a.row_stride;
+  const float* e = a.noise + (size_t)b * a.V;
+  const int V = a.V;
+  const float rtf = 1.f / a.tf;
+  float m = -INFINITY, sum = 0.f;
+  Top2 t2;
+  t2.init();
+  int nan_i = 0x7fffffff;
+  if ((V & 3) == 0 && (a.row_stride & 3) == 0) {
+    const int n4 = V >> 2;
+    const uint32_t row_bytes = (uint32_t)V * 4u;
+    const __amdgpu_buffer_rsrc_t bz = span_rsrc(z, row_bytes), be = span_rsrc(e, row_bytes);
+    u32x4_t zv[kVecPerThread], ev[kVecPerThread];
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const uint32_t off = (uint32_t)vec_index(c, k) * 16u;
+      zv[k] = load_b128(bz, off);
+      if (!a.greedy) ev[k] = load_b128(be, off);
+    }
+    if (a.greedy) {
+      // first-index argmax of the raw logits (torch.argmax: NaN wins)
+#pragma unroll
+      for (int k = 0; k < kVecPerThread; ++k) {
+        const int i4 = vec_index(c, k);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float v = __uint_as_float(zv[k][t]);
+          if (i4 < n4 && better(v, 4 * i4 + t, t2.v1, t2.i1)) t2.v1 = v, t2.i1 = 4 * i4 + t;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kVecPerThread; ++k) {
+        const int i4 = vec_index(c, k);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float x = UNIT ? __uint_as_float(zv[k][t]) : __uint_as_float(zv[k][t]) * rtf;
+          if (i4 < n4) m = fmaxf(m, x);
+        }
+      }
+      // the slice max across the workgroup, so every thread's keys share it
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 8, 64));
+      m = fmaxf(m, __shfl_xor(m, 4, 64));
+      m = fmaxf(m, __shfl_xor(m, 2, 64));
+      m = fmaxf(m, __shfl_xor(m, 1, 64));
+      __shared__ float s_m[kWaves];
+      if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+      __syncthreads();
+      m = s_m[0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) m = fmaxf(m, s_m[w]);
+      const float ml = m == -INFINITY ? 0.f : m * kLog2e;
+#pragma unroll
+      for (int k = 0; k < kVecPerThread; ++k) {
+        const int i4 = vec_index(c, k);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int i = 4 * i4 + t;
+          const bool ok = i4 < n4;
+          const float x = UNIT ? __uint_as_float(zv[k][t]) : __uint_as_float(zv[k][t]) * rtf;
+          const float q = ok ? __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -ml)) : 0.f;
+          sum += q;
+          const float key = ok ? q * __builtin_amdgcn_rcpf(__uint_as_float(ev[k][t])) : -1.f;
+          const bool c1 = key > t2.v1, c2 = key > t2.v2;
+          t2.v2 = c1 ? t2.v1 : (c2 ? key : t2.v2);
+          t2.i2 = c1 ? t2.i1 : (c2 ? i : t2.i2);
+          t2.v1 = c1 ? key : t2.v1;
+          t2.i1 = c1 ? i : t2.i1;
+          nan_i = (key != key && nan_i == 0x7fffffff) ? i : nan_i;
+        }
+      }
+    }
+  } else {
+    // unaligned rows: element loads, two passes
+    const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
+    if (a.greedy) {
+      for (int i = i0 + threadIdx.x; i < i1; i += kThreads)
+        if (better(z[i], i, t2.v1, t2.i1)) t2.v1 = z[i], t2.i1 = i;
+    } else {
+      for (int i = i0 + threadIdx.x; i < i1; i += kThreads) m = fmaxf(m, UNIT ? z[i] : z[i] * rtf);
+      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      __shared__ float s_m2[kWaves];
+      if ((threadIdx.x & 63) == 0) s_m2[threadIdx.x >> 6] = m;
+      __syncthreads();
+      m = s_m2[0];
+      for (int w = 1; w < kWaves; ++w) m = fmaxf(m, s_m2[w]);
+      const float ml = m == -INFINITY ? 0.f : m * kLog2e;
+      for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
+        const float x = UNIT ? z[i] : z[i] * rtf;
+        const float q = __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -ml));
+        sum += q;
+        t2.push(q * __builtin_amdgcn_rcpf(e[i]), i);
+        if (q != q && nan_i == 0x7fffffff) nan_i = i;
+      }
+    }
+  }
+  if (nan_i != 0x7fffffff) {  // a NaN key leads the thread's list
+    t2.v2 = t2.v1;
+    t2.i2 = t2.i1;
+    t2.v1 = __uint_as_float(0x7fc00000u);
+    t2.i1 = nan_i;
+  }
+  t2.wave_reduce();
+  __shared__ float s_v1[kWaves], s_v2[kWaves];
+  __shared__ int s_i1[kWaves], s_i2[kWaves];
+  __shared__ float s_sum[kWaves];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_v1[w] = t2.v1;
+    s_v2[w] = t2.v2;
+    s_i1[w] = t2.i1;
+    s_i2[w] = t2.i2;
+    s_sum[w] = sum;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float st = 0.f;
+    for (int k = 1; k < kWaves; ++k) t2.merge(s_v1[k], s_i1[k], s_v2[k], s_i2[k]);
+    for (int k = 0; k < kWaves; ++k) st += s_sum[k];
+    const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(a.part);
+    const size_t o = ((size_t)b * nch + c) * sizeof(DraftPart);
+    store_coherent_b128(rp, o, u32x4_t{__float_as_uint(m), __float_as_uint(st), __float_as_uint(t2.v1),
+                                       __float_as_uint(t2.v2)});
+    store_coherent_b128(rp, o + 16, u32x4_t{(unsigned)t2.i1, (unsigned)t2.i2, 0u, 0u});
+  }
+  __shared__ int s_last;
+  if (!arrive_last(a.cnt + b, nch, &s_last)) return;
+
+  // The row's last workgroup: combine the slices (one wave), then the draw.
+  __shared__ int s_tok, s_exact;
+  __shared__ float s_M, s_S;
+  if (threadIdx.x < 64) {
+    const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(a.part);
+    float M = -INFINITY;
+    float pm[4], ps[4], pv1[4], pv2[4];
+    int pi1[4], pi2[4];
+    int np = 0;
+    for (int k = threadIdx.x; k < nch; k += 64, ++np) {  // nch <= 256 at V <= 4M
+      const size_t o = ((size_t)b * nch + k) * sizeof(DraftPart);
+      const u32x4_t lo = load_coherent_b128(rp, o), hi = load_coherent_b128(rp, o + 16);
+      pm[np] = __uint_as_float(lo.x);
+      ps[np] = __uint_as_float(lo.y);
+      pv1[np] = __uint_as_float(lo.z);
+      pv2[np] = __uint_as_float(lo.w);
+      pi1[np] = (int)hi.x;
+      pi2[np] = (int)hi.y;
+      M = fmaxf(M, pm[np]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    Top2 r2;
+    r2.init();
+    float S = 0.f;
+    for (int k = 0; k < np; ++k) {
+      if (a.greedy) {
+        r2.merge(pv1[k], pi1[k], -INFINITY, 0x7fffffff);
+      } else {
+        const float f = pm[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((pm[k] - M) * kLog2e);
+        S += ps[k] * f;
+        r2.merge(pv1[k] * f, pi1[k], pv2[k] * f, pi2[k]);
+      }
+    }
+    r2.wave_reduce();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) S += __shfl_xor(S, o, 64);
+    if (threadIdx.x == 0) {
+      s_tok = r2.i1;
+      s_M = M;
+      s_S = S;
+      s_exact = !a.greedy && (isnan(r2.v1) || !(r2.v1 - r2.v2 > kTieRel * r2.v1));
+    }
+  }
+  __syncthreads();
+  int token = s_tok;
+  if (s_exact) {
+    // torch's arithmetic: q = exp(x - M) / S, key = q / E, first max wins
+    const float M = s_M, S = s_S;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+      const float x = UNIT ? z[i] : z[i] / a.tf;
+      const float key = (expf(x - M) / S) / e[i];
+      if (better(key, i, bv, bi)) bv = key, bi = i;
+    }
+    block_argmax(bv, bi);
+    token = bi;
+  }
+  if (threadIdx.x == 0) a.out[(size_t)b * a.out_stride] = token;
+}
+
 // ------------------------------------------------------- single-row helpers
 __global__ __launch_bounds__(1024) void softmax_rows_kernel(const float* __restrict__ logits,
                                                             float* __restrict__ probs, int V, float tf,
@@ -908,6 +1132,42 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
     hipLaunchKernelGGL((race_kernel<true, false>), rgrid, dim3(kThreads), 0, s, a, cm, ws);
   else
     hipLaunchKernelGGL((race_kernel<false, false>), rgrid, dim3(kThreads), 0, s, a, cm, ws);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+size_t spv_draft_sample_workspace_bytes(int32_t B, int32_t V) {
+  if (B < 1 || B > 65535 || V < 1 || num_chunks(V) > 256) return 0;
+  return (size_t)SPV_SAMPLE_COUNTER_BYTES + (size_t)B * num_chunks(V) * sizeof(DraftPart);
+}
+
+int spv_draft_sample(const float* logits, int64_t row_stride, float temperature, const float* exp_noise,
+                     int32_t B, int32_t V, int32_t* out_tokens, int32_t out_stride, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  const bool greedy = !(temperature > 0.f);
+  if (!logits || !out_tokens || B < 0 || B > 65535 || V < 1 || row_stride < V || out_stride < 1 ||
+      num_chunks(V) > 256 || (!greedy && !exp_noise))
+    return SPV_ERR_ARG;
+  if ((size_t)V * 4 > 0x7fffffffu) return SPV_ERR_ARG;
+  if (B == 0) return SPV_OK;
+  if (!workspace || workspace_bytes < spv_draft_sample_workspace_bytes(B, V)) return SPV_ERR_WORKSPACE;
+  DraftArgs a{};
+  a.logits = logits;
+  a.noise = exp_noise;
+  a.out = out_tokens;
+  a.cnt = static_cast<int*>(workspace);
+  a.part = reinterpret_cast<DraftPart*>(static_cast<char*>(workspace) + SPV_SAMPLE_COUNTER_BYTES);
+  a.row_stride = row_stride;
+  a.B = B;
+  a.V = V;
+  a.out_stride = out_stride;
+  a.greedy = greedy ? 1 : 0;
+  a.tf = temperature_divisor(temperature);
+  const dim3 grid(num_chunks(V), B);
+  if (a.tf == 1.0f)
+    hipLaunchKernelGGL(draft_race_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(draft_race_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
   SPV_CHECK_LAUNCH();
   return SPV_OK;
 }

@@ -60,6 +60,8 @@ SIGNATURES = {
     "spv_verify_attn_static": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P]),
     "spv_verify_sample_workspace_bytes": (S, [I, I, I]),
     "spv_verify_sample": (I, [P, P, I, F, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, I, P, S, P]),
+    "spv_draft_sample_workspace_bytes": (S, [I, I]),
+    "spv_draft_sample": (I, [P, ctypes.c_int64, F, P, I, I, P, I, P, S, P]),
     "spv_logits_to_probs": (I, [P, P, I, I, F, P]),
     "spv_residual": (I, [P, P, P, I, P]),
     "spv_race_argmax": (I, [P, P, I, P, P]),
@@ -131,16 +133,35 @@ def i32(values, device: torch.device) -> torch.Tensor:
 
 
 class Workspace:
-    """Grow-only device scratch buffer owned by the caller of the library.
+    """Device scratch of one family of entry points, owned by the caller of the
+    library: one zero-filled, grow-only buffer per (device, stream).
 
-    Allocated zero-filled: the attention and sampling entry points keep arrival
-    counters at its head that must start at zero (and are zero again after
-    every call)."""
+    The attention and sampling entry points keep arrival counters at its head
+    that must start at zero (and are zero again after every call), and calls
+    that share a buffer must be ordered: giving each stream its own buffer
+    keeps calls on two streams from racing on counters and partials. A buffer
+    replaced by a larger one is kept alive for the life of the object, since a
+    HIP graph captured earlier may still point at it."""
 
     def __init__(self) -> None:
-        self._buf: Optional[torch.Tensor] = None
+        self._bufs: dict = {}
+        self._retired: list = []
+
+    @staticmethod
+    def _key(device: torch.device):
+        device = torch.device(device)
+        return device.index, torch.cuda.current_stream(device).cuda_stream
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
-        if self._buf is None or self._buf.numel() < nbytes or self._buf.device != device:
-            self._buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
-        return self._buf
+        key = self._key(device)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._retired.append(buf)
+            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+    def current(self, device: torch.device) -> Optional[torch.Tensor]:
+        """The buffer of the current stream on ``device`` (None before first use)."""
+        return self._bufs.get(self._key(device))

@@ -16,6 +16,13 @@ Drop-in for the verify part of the reference's engine/spec_scheduler.py:
   ``write_block`` + ``verify_attention``, then ``verify_sample`` on the
   round's logits and ``rewind_device`` of the KV pool with the device-computed
   lengths and finished flags (spec_scheduler.py:255-322 minus the model).
+* ``draft_sample``  -- one draft step's proposals (spec_scheduler.py:243-252:
+  ``logits_to_probs`` + ``sample_token`` per row) for the whole batch in one
+  launch, with caller-supplied ``Exp(1)`` rows; ``draft_sample_with_generator``
+  draws those rows from the reference's generator in its order.
+* ``DraftLoop``     -- the paged part of the gamma draft decode steps (per layer
+  one-token append + decode attention, engine/model.py:123-153) and each step's
+  sampling, with device-resident positions so the loop captures as one graph.
 """
 
 from __future__ import annotations
@@ -31,6 +38,7 @@ from .attention import verify_attention
 from .kv import PagedKVCache
 
 _workspace = _hip.Workspace()
+_draft_workspace = _hip.Workspace()
 
 
 def _draw_uniform(generator: torch.Generator) -> float:
@@ -240,3 +248,105 @@ class VerifyStep:
                             start_pos=st_t, remaining=rem_t, eos_id=self.eos_id, validate=False)
         self.kv.rewind_device(sid_t, res.new_len, res.finished)
         return res
+
+
+def draft_sample(logits: torch.Tensor, temperature: float, noise: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One draft step's proposals for every row in one launch (spec_scheduler.py:243-252).
+
+    ``logits`` (B, V) fp32 draft logits (rows may be strided, elements
+    contiguous); row b's token is ``sample_token(logits_to_probs(logits[b]))``
+    drawn as ``argmax(q / noise[b])`` with the caller's ``Exp(1)`` rows
+    ``noise`` (B, V), or the first-index argmax when ``temperature <= 0``
+    (``noise`` unused). ``out``: an int32 device view of B entries to write
+    (e.g. column s of the (B, gamma) proposals), else a new tensor. No host
+    synchronisation.
+    """
+    dev = _hip.require_gpu(logits.device)
+    if logits.dim() != 2 or logits.stride(1) != 1 or logits.dtype != torch.float32:
+        raise ValueError("logits must be a (B, V) float32 tensor with contiguous rows")
+    B, V = (int(x) for x in logits.shape)
+    greedy = not temperature > 0
+    if not greedy:
+        if noise is None or tuple(noise.shape) != (B, V) or noise.dtype != torch.float32 or not noise.is_contiguous():
+            raise ValueError("sampling needs contiguous float32 Exp(1) rows of shape (B, V)")
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=dev)
+    if out.dtype != torch.int32 or out.dim() != 1 or out.numel() != B or out.device != dev:
+        raise ValueError("out must be an int32 device vector of B entries")
+    ws_bytes = _hip.lib().spv_draft_sample_workspace_bytes(max(B, 1), V)
+    if ws_bytes == 0:
+        raise ValueError("unsupported draft-sampling shape B={} V={}".format(B, V))
+    ws = _draft_workspace.get(ws_bytes, dev)
+    call("spv_draft_sample", ptr(logits), int(logits.stride(0)), float(temperature),
+         None if greedy else ptr(noise), B, V, ptr(out), int(out.stride(0)), ptr(ws), int(ws_bytes),
+         _hip.stream_of(dev))
+    return out
+
+
+def draft_sample_with_generator(q_logits: torch.Tensor, sampling, generator: torch.Generator) -> List[int]:
+    """The reference's per-row loop of one draft step (spec_scheduler.py:246-251:
+    ``logits_to_probs`` then ``sample_token`` drawing from ``generator``) as one
+    launch: the B ``Exp(1)`` rows the B multinomial draws consume are drawn from
+    ``generator`` on the host in batch order (also when greedy, where the
+    reference's draw from a one-hot row still consumes them), then raced on the
+    device. Returns the B token ids; the generator ends where the reference's does."""
+    top_k = getattr(sampling, "top_k", 0)
+    top_p = getattr(sampling, "top_p", 1.0)
+    if (top_k and 0 < top_k < q_logits.shape[-1]) or 0.0 < top_p < 1.0:
+        raise NotImplementedError("draft_sample_with_generator takes unfiltered logits")
+    z = q_logits.detach().float().contiguous()
+    B, V = (int(x) for x in z.shape)
+    noise = torch.stack([torch.empty(V, dtype=torch.float32).exponential_(1, generator=generator)
+                         for _ in range(B)]) if B else torch.empty(0, V)
+    temperature = 0.0 if sampling.is_greedy else float(sampling.temperature)
+    return draft_sample(z, temperature, noise.to(z.device)).tolist()
+
+
+class DraftLoop:
+    """The paged part of the gamma draft decode steps and their sampling.
+
+    Per step s (positions ``ctx + s``, device-resident) and draft layer l: the
+    new token's K/V are written at ``ctx + s`` (allocating at layer 0, the
+    write-then-attend order of engine/model.py:123-153), then decode attention
+    of the step's query over positions ``0 .. ctx + s``; after the last layer
+    the step's proposals are drawn from its draft logits into column s of the
+    (B, gamma) proposals (spec_scheduler.py:243-252). Every launch goes to the
+    current stream and nothing synchronises with the host, so ``run`` can be
+    captured in a HIP graph; the draft model between the steps is the caller's.
+    """
+
+    def __init__(self, kv: PagedKVCache, gamma: int, temperature: float):
+        self.kv = kv
+        self.gamma = int(gamma)
+        self.temperature = float(temperature)
+
+    def run(self, seq_ids: torch.Tensor, ctx: torch.Tensor, max_ctx: int,
+            q_steps: Sequence[Sequence[torch.Tensor]], k_steps: Sequence[Sequence[torch.Tensor]],
+            v_steps: Sequence[Sequence[torch.Tensor]], logits_steps: Sequence[torch.Tensor],
+            noise_steps: Optional[Sequence[torch.Tensor]] = None,
+            proposals: Optional[torch.Tensor] = None,
+            attn_out: Optional[Sequence[Sequence[torch.Tensor]]] = None):
+        """``seq_ids``/``ctx`` (B,) int32 device: the sequences and their draft
+        cache lengths before the loop; ``max_ctx`` >= max(ctx) (host int).
+        ``q_steps[s][l]`` (B, 1, Hq, d), ``k_steps``/``v_steps[s][l]`` (B, 1,
+        Hkv, d), ``logits_steps[s]`` (B, V) fp32, ``noise_steps[s]`` (B, V)
+        Exp(1) rows (None when greedy). Returns (proposals (B, gamma) int32,
+        attention outputs [s][l])."""
+        kv = self.kv
+        dev = kv.device
+        B = int(seq_ids.numel())
+        if proposals is None:
+            proposals = torch.empty((B, self.gamma), dtype=torch.int32, device=dev)
+        outs = []
+        for s in range(self.gamma):
+            pos = ctx + s
+            outs_s = []
+            for layer in range(len(q_steps[s])):
+                kv.write_block_device(layer, seq_ids, pos, k_steps[s][layer], v_steps[s][layer], alloc=layer == 0)
+                o = None if attn_out is None else attn_out[s][layer]
+                outs_s.append(verify_attention(q_steps[s][layer], kv, layer, seq_ids, pos, max_ctx + s + 1, out=o))
+            outs.append(outs_s)
+            draft_sample(logits_steps[s], self.temperature, None if noise_steps is None else noise_steps[s],
+                         out=proposals[:, s])
+        return proposals, outs

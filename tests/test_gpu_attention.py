@@ -229,7 +229,7 @@ def test_repeated_calls_are_identical_and_leave_counters_zero(cuda):
     outs = [verify_attention(q, gpu, 0, list(range(32)), lens, max(lens) + 6).clone() for _ in range(3)]
     torch.cuda.synchronize()
     assert all(torch.equal(outs[0], o) for o in outs[1:])
-    counters = A._workspace._buf[: 1 << 18]
+    counters = A._workspace.current(cuda)[: 1 << 18]
     assert int(counters.count_nonzero()) == 0
     _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, 12))
 
@@ -271,7 +271,7 @@ def test_page_balanced_split_when_segments_outnumber_workgroups(cuda, B, C, Hq):
     outs = [verify_attention(q, gpu, 0, list(range(B)), lens, max(lens) + C).clone() for _ in range(2)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
-    assert int(torch.count_nonzero(A._workspace._buf[: 1 << 18])) == 0
+    assert int(torch.count_nonzero(A._workspace.current(cuda)[: 1 << 18])) == 0
     _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, Hq))
 
 
@@ -295,7 +295,7 @@ def test_balanced_split_with_piece_costs(cuda, n_short, n_long, d):
     outs = [verify_attention(q, gpu, 0, list(range(B)), lens, max(lens) + C).clone() for _ in range(2)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
-    assert int(torch.count_nonzero(A._workspace._buf[: 1 << 18])) == 0
+    assert int(torch.count_nonzero(A._workspace.current(cuda)[: 1 << 18])) == 0
     _bf16_check(outs[0], ref_attn.extend_attention_dense(q.cpu(), keys, values, lens, Hq))
 
 

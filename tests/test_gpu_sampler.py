@@ -266,7 +266,7 @@ def test_repeated_calls_are_identical_and_leave_counters_zero(cuda, T):
         assert res.accepted_lists() == want
         outs.append((res.accept_len.clone(), res.out_tokens.clone()))
         torch.cuda.synchronize()
-        assert int(torch.count_nonzero(es._workspace._buf[:SAMPLE_COUNTER_BYTES])) == 0
+        assert int(torch.count_nonzero(es._workspace.current(cuda)[:SAMPLE_COUNTER_BYTES])) == 0
     for a, o in outs[1:]:
         assert torch.equal(a, outs[0][0]) and torch.equal(o, outs[0][1])
 
