@@ -671,6 +671,54 @@ def draft_decode(dev, seed=0):
     return res
 
 
+# Prefill: Qwen2.5-3B-shaped prompts (16 q / 2 kv heads, head_dim 128, bf16).
+PF_B, PF_HQ, PF_HKV, PF_D = 4, 16, 2, 128
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def prefill_flops(lengths, hq=PF_HQ, d=PF_D):
+    """Algorithmic FLOPs of causal prefill: per row of L positions, query i
+    meets i + 1 keys in q.k and in p.v (2 flops per multiply-add)."""
+    return sum(hq * 4 * d * L * (L + 1) // 2 for L in lengths)
+
+
+def prefill(dev, seed=0):
+    """Causal chunk prefill attention at the Qwen2.5-3B shape: 4 prompts with
+    lengths log-uniform in [512, 8192] (seeded) in one padded chunk, timed as
+    a captured graph of back-to-back calls; TFLOP/s of the algorithmic causal
+    FLOPs against MI355X's dense bf16 peak."""
+    import torch
+
+    from engine.attention import prefill_attention
+
+    g = torch.Generator().manual_seed(seed + 17)
+    lengths = [int(math.exp(math.log(512) + (math.log(8192) - math.log(512)) * float(u)))
+               for u in torch.rand(PF_B, generator=g)]
+    Lc = max(lengths)
+    gd = torch.Generator(device=dev).manual_seed(seed + 17)
+    q = torch.randn(PF_B, Lc, PF_HQ, PF_D, generator=gd, device=dev).to(torch.bfloat16)
+    k = torch.randn(PF_B, Lc, PF_HKV, PF_D, generator=gd, device=dev).to(torch.bfloat16)
+    v = torch.randn(PF_B, Lc, PF_HKV, PF_D, generator=gd, device=dev).to(torch.bfloat16)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    call = lambda: prefill_attention(q, k, v, lens, out=out)
+    call()
+    torch.cuda.synchronize()
+    n = 4
+    gr = graph_of(lambda: [call() for _ in range(n)], 1, torch)
+    us = time_graph(gr, 5, torch) * 1000.0 / n
+    flops = prefill_flops(lengths)
+    tf = flops / (us * 1e-6) / 1e12
+    del gr, q, k, v, out
+    torch.cuda.empty_cache()
+    return {"workload": "Qwen2.5-3B-shaped causal prefill chunk: {} prompts of {} tokens in one chunk of {}, "
+                        "16q/2kv heads, head_dim 128, bf16".format(PF_B, lengths, Lc),
+            "us": round(us, 1), "tflops": round(tf, 1), "flops_per_call": flops,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)},
+            "us_per_token": round(us / sum(lengths), 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -784,6 +832,8 @@ def main() -> int:
     if not args.no_long_context:
         print("bench: draft decode", file=sys.stderr, flush=True)
         line["draft_decode"] = draft_decode(dev, args.seed)
+        print("bench: prefill", file=sys.stderr, flush=True)
+        line["prefill"] = prefill(dev, args.seed)
     if args.full_depth_rounds > 0:
         del g_step, g_att, g_smp, g_ar, step, parts, res, w
         torch.cuda.synchronize()

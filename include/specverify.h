@@ -231,6 +231,20 @@ int spv_verify_attn_static(void* out, const void* q, int q_dtype,
  * without the queue gaps around it. The arming ends with that call. */
 int spv_time_next_attention(void* start_event, void* stop_event);
 
+/* paged_attention_prefill_chunk (engine/attention.py:121-167): causal
+ * attention of a freshly prefilled prompt chunk over itself. q (B, Lc, Hq, d),
+ * k / v (B, Lc, Hkv, d) and out (B, Lc, Hq, d) are dense, in dtype (f32, bf16
+ * or f16); lengths (device int32, B entries) holds the valid positions of each
+ * row (clamped to [0, Lc]). Position j < lengths[b], q head h attends keys
+ * 0 .. j of kv head h / (Hq/Hkv) with softmax(scale * q.k); positions >=
+ * lengths[b] are written as zeros and none of them enters a result (the
+ * padding may hold anything). bf16 with head_dim 64 or 128 takes the MFMA
+ * path, other cases an fp32 VALU path. No workspace. */
+int spv_prefill_attn(void* out, const void* q, const void* k, const void* v,
+                     int dtype, const int32_t* lengths, int32_t B, int32_t Lc,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                     float scale, void* stream);
+
 /* -------------------------------------------------------------- sampling */
 
 /* Workspace needed by spv_verify_sample. Its first SPV_SAMPLE_COUNTER_BYTES

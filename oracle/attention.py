@@ -9,6 +9,9 @@ Follows engine/attention.py of the reference:
 * ``full_attention``         -- attention.py:66-93 (unmasked SDPA)
 * ``paged_attention_extend`` -- attention.py:170-216 (boolean causal mask
                                 ``mask[j, i] = i <= start + j``, one SDPA per sequence)
+* ``paged_attention_prefill_chunk`` -- attention.py:121-167 (causal SDPA over each
+                                row's first ``chunk_query_lengths[b]`` positions of
+                                the dense chunk, zeros for the padded tail)
 
 ``extend_attention_dense`` runs the same per-sequence mask + SDPA on dense
 per-sequence K/V (what ``gather_ctx`` would return), so large synthetic
@@ -17,7 +20,11 @@ workloads need not be materialised in the reference pool layout first.
 Pinned by tests/test_oracle_attention.py: the reference's GQA mapping test
 (tests/test_attention.py:73-81), extend == per-row prefix ``full_attention``
 (tests/test_paged_attention_extend.py:56-77, 1e-5), and an independent float64
-brute-force softmax(QK^T/sqrt(d))V written with explicit loops.
+brute-force softmax(QK^T/sqrt(d))V written with explicit loops; the prefill
+chunk by the reference's prefill tests (tests/test_attention.py:144-175: the
+symmetric q = k = v case against causal SDPA at 1e-5, an exactly zero padded
+tail, finite outputs), the same float64 brute force with a causal mask, and
+its agreement with ``paged_attention_extend`` at start 0 over the same keys.
 """
 
 from __future__ import annotations
@@ -106,4 +113,22 @@ def extend_attention_dense(query_3d: torch.Tensor, keys: Sequence[torch.Tensor],
         outs.append(_extend_one(query_3d[b].to(compute_dtype),
                                 keys[b][:n].to(compute_dtype),
                                 values[b][:n].to(compute_dtype), start, num_q_heads))
+    return torch.stack(outs, 0)
+
+
+def paged_attention_prefill_chunk(query_3d: torch.Tensor, key_3d: torch.Tensor, value_3d: torch.Tensor,
+                                  num_q_heads: int, chunk_query_lengths: Sequence[int]) -> torch.Tensor:
+    """``(B, chunk, Hq, d)``: row ``b`` position ``j < L_b`` attends ``0 .. j`` of
+    its own chunk (GQA expanded), positions ``>= L_b`` are zeros."""
+    B, chunk = query_3d.shape[:2]
+    outs = []
+    for b in range(B):
+        n = int(chunk_query_lengths[b])
+        q4 = query_3d[b][:n].transpose(0, 1).unsqueeze(0)
+        k4 = expand_to_q_heads(key_3d[b][:n], num_q_heads).transpose(0, 1).unsqueeze(0)
+        v4 = expand_to_q_heads(value_3d[b][:n], num_q_heads).transpose(0, 1).unsqueeze(0)
+        out = F.scaled_dot_product_attention(q4, k4, v4, is_causal=True)[0].transpose(0, 1)
+        if chunk > n:
+            out = torch.cat((out, torch.zeros((chunk - n,) + tuple(out.shape[1:]), dtype=out.dtype)), 0)
+        outs.append(out)
     return torch.stack(outs, 0)

@@ -1,0 +1,476 @@
+// Causal attention over a freshly prefilled prompt chunk on gfx950.
+//
+// Semantics (engine/attention.py:121-167 of the reference,
+// paged_attention_prefill_chunk): q (B, Lc, Hq, d), k / v (B, Lc, Hkv, d),
+// dense; sequence b has L_b = lengths[b] valid positions (the rest of the
+// chunk is tail padding). Position i < L_b, q head h attends keys 0..i of kv
+// head h / (Hq/Hkv) with softmax(scale * q.k); positions i >= L_b are written
+// as zeros. Nothing beyond L_b is read into a result (padding may hold
+// anything, NaN included).
+//
+// MFMA path (bf16, head_dim 64 or 128): one workgroup of 8 waves takes a block
+// of BM consecutive positions and every q head of one kv head -- rows (position
+// p, head k) in the order p * ratio + k, 16 rows per MFMA tile, NT tiles per
+// wave -- so every K/V tile staged in LDS serves all heads of the group. Key
+// tiles of 64 are double-buffered in LDS (K row-major, V transposed), one
+// barrier per tile. Per 16-key part of a tile and query tile:
+//   S^T = K Q^T    v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims (LDS),
+//                  B = Q^T fragments held in registers for the whole walk;
+//   O^T += V^T P^T v_mfma_f32_16x16x32_bf16, A = {V^T, V^T} (LDS), B =
+//                  {P_hi, P_lo}: P split into two bf16 halves, so P V carries
+//                  ~16 significant bits of P, not 8.
+// The accumulator layout of S^T is the operand layout of P^T (lane l: keys
+// 4 (l / 16) .. + 3 of query column l % 16), so the softmax moves no data.
+// Online softmax with a per-column reference maximum that scores may exceed by
+// kSlack (log2 units) before O is rescaled; masks only on diagonal tiles.
+// Workgroups take position blocks from the last (longest key range) to the
+// first, so the long blocks start first.
+//
+// VALU path (fp32 / fp16 / other head dims): one workgroup per (sequence, q
+// head, 64 positions), key tiles of 16 in LDS, fp32 online softmax.
+#include <math.h>
+
+#include "spv_common.h"
+
+using namespace spv;
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kSlack = 8.f;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBK = 64;  // keys per LDS tile
+
+struct PrefillParams {
+  void* out;
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* lengths;
+  int B, Lc, Hq, Hkv, ratio, d;
+  int BM;     // positions per workgroup (MFMA path)
+  int nblk;   // position blocks per (sequence, kv head)
+  float scale_log2;
+};
+
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+template <int NT, int D>
+__global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams p) {
+  constexpr int KS = D / 32;          // 32-dim k-steps of S^T
+  constexpr int MT = D / 16;          // 16-dim tiles of O^T
+  constexpr int KP = D + 8;           // bf16 pitch of a K row in LDS (16 bytes of padding)
+  constexpr int VP = kBK + 4;         // bf16 pitch of a V^T row in LDS (8 bytes of padding)
+  constexpr int kKElems = kBK * KP, kVElems = D * VP;
+  __shared__ __align__(16) uint16_t sK[2][kKElems];
+  __shared__ __align__(16) uint16_t sV[2][kVElems];
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i16 = lane & 15, g = lane >> 4;
+  const int hk = blockIdx.y, b = blockIdx.z;
+  const int blk = p.nblk - 1 - (int)blockIdx.x;  // longest key ranges first
+  const int p0 = blk * p.BM;
+  const int L = min(max(p.lengths[b], 0), p.Lc);  // never a key beyond the chunk
+  const int ratio = p.ratio, Hq = p.Hq, Hkv = p.Hkv, Lc = p.Lc;
+  const uint16_t* qb = static_cast<const uint16_t*>(p.q);
+  const uint16_t* kb = static_cast<const uint16_t*>(p.k);
+  const uint16_t* vb = static_cast<const uint16_t*>(p.v);
+  uint16_t* ob = static_cast<uint16_t*>(p.out);
+
+  // This lane's query column of each tile: WG row R = (w * NT + nt) * 16 + i16,
+  // position p0 + R / ratio, q head hk * ratio + R % ratio.
+  int cpos[NT], chead[NT];
+  bool cvalid[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int R = (w * NT + nt) * 16 + i16;
+    const int pl = R / ratio;
+    cpos[nt] = p0 + pl;
+    chead[nt] = hk * ratio + (R - pl * ratio);
+    cvalid[nt] = pl < p.BM && cpos[nt] < L;
+  }
+  const int rows_end = min(L, p0 + p.BM);  // positions of this block that exist
+  if (rows_end <= p0) {
+    // no valid position in the block: its rows are padding, written as zeros
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int R = (w * NT + nt) * 16 + i16;
+      if (R / ratio >= p.BM || cpos[nt] >= Lc) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        *reinterpret_cast<uint2*>(ob + (((size_t)b * Lc + cpos[nt]) * Hq + chead[nt]) * D + 16 * mt + 4 * g) =
+            make_uint2(0u, 0u);
+    }
+    return;
+  }
+  const int kend = rows_end;  // keys 0 .. kend - 1 are attended by some row
+  const int ntiles = (kend + kBK - 1) / kBK;
+
+  // Q^T fragments for the whole walk (B operand: dims 32 ks + 8 g .. + 7 of column i16).
+  uint4 qf[NT][KS];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[nt][ks] = cvalid[nt] ? *reinterpret_cast<const uint4*>(
+                                    qb + (((size_t)b * Lc + cpos[nt]) * Hq + chead[nt]) * D + 32 * ks + 8 * g)
+                              : make_uint4(0u, 0u, 0u, 0u);
+
+  // Staging: K tile as 16-byte chunks (key, 8 dims); V tile as (key pair, 8
+  // dims) items written transposed, one 32-bit word (two keys) per dim.
+  constexpr int kKChunks = kBK * D / 8, kKPer = (kKChunks + kThreads - 1) / kThreads;
+  constexpr int kVItems = kBK / 2 * D / 8, kVPer = (kVItems + kThreads - 1) / kThreads;
+  uint4 kreg[kKPer], vreg[kVPer][2];
+  auto load_tile = [&](int t) {
+    const int t0 = t * kBK;
+#pragma unroll
+    for (int i = 0; i < kKPer; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      const int key = c / (D / 8), col = c % (D / 8);
+      kreg[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (c < kKChunks && t0 + key < kend)
+        kreg[i] = *reinterpret_cast<const uint4*>(kb + (((size_t)b * Lc + t0 + key) * Hkv + hk) * D + 8 * col);
+    }
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      const int pair = c / (D / 8), col = c % (D / 8);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        vreg[i][e] = make_uint4(0u, 0u, 0u, 0u);  // keys beyond the range stay zero (never NaN)
+        if (c < kVItems && t0 + 2 * pair + e < kend)
+          vreg[i][e] = *reinterpret_cast<const uint4*>(vb + (((size_t)b * Lc + t0 + 2 * pair + e) * Hkv + hk) * D +
+                                                       8 * col);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kKPer; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      if (c < kKChunks) {
+        const int key = c / (D / 8), col = c % (D / 8);
+        *reinterpret_cast<uint4*>(&sK[buf][key * KP + 8 * col]) = kreg[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      if (c < kVItems) {
+        const int pair = c / (D / 8), col = c % (D / 8);
+        const uint32_t a[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
+        const uint32_t bb[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // dims 8 col + 2 e (low halves) and + 1 (high halves): keys 2 pair, 2 pair + 1
+          const uint32_t lo = (a[e] & 0xffffu) | (bb[e] << 16);
+          const uint32_t hi = (a[e] >> 16) | (bb[e] & 0xffff0000u);
+          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e) * VP + 2 * pair]) = lo;
+          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e + 1) * VP + 2 * pair]) = hi;
+        }
+      }
+    }
+  };
+
+  f32x4_t o[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m[NT], l[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m[nt] = -INFINITY;
+    l[nt] = 0.f;
+  }
+  const float sl2 = p.scale_log2;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);  // in flight while this tile is computed
+    const int t0 = t * kBK;
+    const bool need_mask = t0 + kBK - 1 > p0;  // some key beyond the block's first position
+    const uint16_t* K = sK[buf];
+    const uint16_t* Vt = sV[buf];
+    // S^T for the four 16-key parts of the tile
+    f32x4_t sc[4][NT];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) sc[kt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(&K[(16 * kt + i16) * KP + 32 * ks + 8 * g]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          sc[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                               __builtin_bit_cast(bf16x8_t, qf[nt][ks]), sc[kt][nt], 0,
+                                                               0, 0);
+      }
+    }
+    // scores in log2 units, masks, and the growth test against the reference m
+    bool grow = false;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          float x = sc[kt][nt][jj] * sl2;
+          if (need_mask && t0 + 16 * kt + 4 * g + jj > cpos[nt]) x = -INFINITY;
+          sc[kt][nt][jj] = x;
+          grow |= x > m[nt] + kSlack;
+        }
+    if (__any(grow)) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          mx = fmaxf(mx, fmaxf(fmaxf(sc[kt][nt][0], sc[kt][nt][1]), fmaxf(sc[kt][nt][2], sc[kt][nt][3])));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m[nt], mx);
+        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[nt] - m_new);
+        l[nt] *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o[mt][nt] *= alpha;
+        m[nt] = m_new;
+      }
+    }
+    // P = 2^(x - m) as hi + lo bf16 halves; row sums take P itself
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      bf16x8_t pf[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
+        float e[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(sc[kt][nt][jj] - mu);
+        l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
+        const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
+        const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
+        const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
+        const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
+        pf[nt] = __builtin_bit_cast(
+            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
+                                 pack2_bf16(r01[0], r01[1]), pack2_bf16(r23[0], r23[1])));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        // V^T rows (dim 16 mt + i16), keys 16 kt + 4 g .. + 3, in both halves of the k-slots
+        const uint2 vv = *reinterpret_cast<const uint2*>(&Vt[(16 * mt + i16) * VP + 16 * kt + 4 * g]);
+        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(vv.x, vv.y, vv.x, vv.y));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[nt], o[mt][nt], 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);  // that buffer's readers finished before the last barrier
+    __syncthreads();
+  }
+
+  // Row sums over the four lane groups, then the normalised rows.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    l[nt] += __shfl_xor(l[nt], 16, 64);
+    l[nt] += __shfl_xor(l[nt], 32, 64);
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int R = (w * NT + nt) * 16 + i16;
+    if (R / ratio >= p.BM || cpos[nt] >= Lc) continue;
+    const float inv = cvalid[nt] ? 1.f / l[nt] : 0.f;  // padded positions: zeros
+    uint16_t* orow = ob + (((size_t)b * Lc + cpos[nt]) * Hq + chead[nt]) * D;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const f32x4_t v = o[mt][nt] * inv;
+      *reinterpret_cast<uint2*>(orow + 16 * mt + 4 * g) = make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ VALU path
+constexpr int kValuThreads = 256;
+constexpr int kValuRows = 64;
+
+template <int DT>
+__global__ __launch_bounds__(kValuThreads) void prefill_valu_kernel(PrefillParams p) {
+  extern __shared__ float smem[];
+  const int d = p.d;
+  const int hq = blockIdx.y, b = blockIdx.z, hk = hq / p.ratio;
+  const int p0 = blockIdx.x * kValuRows;
+  const int L = min(max(p.lengths[b], 0), p.Lc);  // never a key beyond the chunk
+  const int nr = min(kValuRows, p.Lc - p0);  // rows of this block that exist in the chunk
+  float* Qs = smem;                  // [64][d], pre-scaled (log2 units)
+  float* Ks = Qs + kValuRows * d;    // [16][d]
+  float* Vs = Ks + 16 * d;           // [16][d]
+  float* Ps = Vs + 16 * d;           // [64][17]
+  float* Ms = Ps + kValuRows * 17;   // [64]
+  float* Ls = Ms + kValuRows;        // [64]
+  float* As = Ls + kValuRows;        // [64]
+  for (int idx = threadIdx.x; idx < nr * d; idx += blockDim.x) {
+    const int rr = idx / d, e = idx - rr * d;
+    const int pos = p0 + rr;
+    Qs[rr * d + e] = pos < L ? load_elem<DT>(p.q, (((size_t)b * p.Lc + pos) * p.Hq + hq) * d + e) * p.scale_log2 : 0.f;
+  }
+  if (threadIdx.x < kValuRows) {
+    Ms[threadIdx.x] = -INFINITY;
+    Ls[threadIdx.x] = 0.f;
+  }
+  constexpr int kMaxO = kValuRows * 256 / kValuThreads;  // rows * head_dim <= 64 * 256
+  float o[kMaxO];
+#pragma unroll
+  for (int k = 0; k < kMaxO; ++k) o[k] = 0.f;
+  __syncthreads();
+  const int kend = min(L, p0 + nr);  // keys attended by some valid row of the block
+  for (int t0 = 0; t0 < kend; t0 += 16) {
+    const int nt = min(16, kend - t0);
+    for (int idx = threadIdx.x; idx < nt * d; idx += blockDim.x) {
+      const int tt = idx / d, e = idx - tt * d;
+      const size_t src = (((size_t)b * p.Lc + t0 + tt) * p.Hkv + hk) * d + e;
+      Ks[tt * d + e] = load_elem<DT>(p.k, src);
+      Vs[tt * d + e] = load_elem<DT>(p.v, src);
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nr * 16; idx += blockDim.x) {
+      const int rr = idx >> 4, tt = idx & 15;
+      float sc = -INFINITY;
+      if (tt < nt && t0 + tt <= p0 + rr && p0 + rr < L) {
+        float acc = 0.f;
+        for (int e = 0; e < d; ++e) acc = fmaf(Qs[rr * d + e], Ks[tt * d + e], acc);
+        sc = acc;
+      }
+      Ps[rr * 17 + tt] = sc;
+    }
+    __syncthreads();
+    if (threadIdx.x < nr) {
+      const int rr = threadIdx.x;
+      float mx = -INFINITY;
+      for (int tt = 0; tt < 16; ++tt) mx = fmaxf(mx, Ps[rr * 17 + tt]);
+      const float m_old = Ms[rr];
+      const float m_new = fmaxf(m_old, mx);
+      float alpha = 1.f, sum = 0.f;
+      if (m_new != -INFINITY) {
+        alpha = exp2f(m_old - m_new);
+        for (int tt = 0; tt < 16; ++tt) {
+          const float x = Ps[rr * 17 + tt];
+          const float e = x == -INFINITY ? 0.f : exp2f(x - m_new);
+          Ps[rr * 17 + tt] = e;
+          sum += e;
+        }
+      } else {
+        for (int tt = 0; tt < 16; ++tt) Ps[rr * 17 + tt] = 0.f;
+      }
+      Ls[rr] = Ls[rr] * alpha + sum;
+      Ms[rr] = m_new;
+      As[rr] = alpha;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kMaxO; ++k) {
+      const int el = threadIdx.x + k * kValuThreads;
+      if (el < nr * d) {
+        const int rr = el / d, e = el - rr * d;
+        float acc = o[k] * As[rr];
+        for (int tt = 0; tt < nt; ++tt) acc = fmaf(Ps[rr * 17 + tt], Vs[tt * d + e], acc);
+        o[k] = acc;
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxO; ++k) {
+    const int el = threadIdx.x + k * kValuThreads;
+    if (el < nr * d) {
+      const int rr = el / d, e = el - rr * d;
+      const int pos = p0 + rr;
+      const float val = pos < L ? o[k] / Ls[rr] : 0.f;  // padded positions: zeros
+      store_elem<DT>(p.out, (((size_t)b * p.Lc + pos) * p.Hq + hq) * d + e, val);
+    }
+  }
+}
+
+template <int NT, int D>
+void launch_prefill_mfma(PrefillParams p, hipStream_t s) {
+  const int rows = kWaves * NT * 16;
+  p.BM = rows / p.ratio;
+  p.nblk = (p.Lc + p.BM - 1) / p.BM;
+  hipLaunchKernelGGL((prefill_mfma_kernel<NT, D>), dim3(p.nblk, p.Hkv, p.B), dim3(kThreads), 0, s, p);
+}
+
+}  // namespace
+
+extern "C" {
+
+int spv_prefill_attn(void* out, const void* q, const void* k, const void* v, int dtype, const int32_t* lengths,
+                     int32_t B, int32_t Lc, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                     void* stream) {
+  if (!out || !q || !k || !v || !lengths) return SPV_ERR_ARG;
+  if (dtype != SPV_F32 && dtype != SPV_BF16 && dtype != SPV_F16) return SPV_ERR_ARG;
+  if (B < 0 || B > 65535 || Lc < 1 || num_kv_heads < 1 || num_q_heads < num_kv_heads ||
+      num_q_heads % num_kv_heads || head_dim < 1 || head_dim > 256)
+    return SPV_ERR_ARG;
+  if (B == 0) return SPV_OK;
+  if ((long long)B * Lc * num_q_heads * head_dim >= (1LL << 40)) return SPV_ERR_ARG;
+  PrefillParams p{};
+  p.out = out;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.lengths = lengths;
+  p.B = B;
+  p.Lc = Lc;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.ratio = num_q_heads / num_kv_heads;
+  p.d = head_dim;
+  p.scale_log2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  // The MFMA path holds 256 rows (positions x heads of a kv head) per
+  // workgroup: at least one position, i.e. up to 256 q heads per kv head.
+  if (dtype == SPV_BF16 && (head_dim == 128 || head_dim == 64) && p.ratio <= 256) {
+    if (head_dim == 128) launch_prefill_mfma<2, 128>(p, s);
+    else launch_prefill_mfma<2, 64>(p, s);
+    SPV_CHECK_LAUNCH();
+    return SPV_OK;
+  }
+  const size_t smem = (size_t)(kValuRows * head_dim + 32 * head_dim + kValuRows * 17 + 3 * kValuRows) * sizeof(float);
+  const dim3 grid((Lc + kValuRows - 1) / kValuRows, num_q_heads, B), blk(kValuThreads);
+  switch (dtype) {
+    case SPV_F32:
+      if (smem > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_valu_kernel<SPV_F32>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      hipLaunchKernelGGL(prefill_valu_kernel<SPV_F32>, grid, blk, smem, s, p);
+      break;
+    case SPV_BF16:
+      if (smem > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_valu_kernel<SPV_BF16>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      hipLaunchKernelGGL(prefill_valu_kernel<SPV_BF16>, grid, blk, smem, s, p);
+      break;
+    default:
+      if (smem > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_valu_kernel<SPV_F16>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      hipLaunchKernelGGL(prefill_valu_kernel<SPV_F16>, grid, blk, smem, s, p);
+      break;
+  }
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+}  // extern "C"

@@ -55,6 +55,7 @@ SIGNATURES = {
     "spv_kv_read_blocks": (I, [P, I, I, P, I, I, I, I, I, I, P, P]),
     "spv_verify_attn_workspace_bytes": (S, [I, I, I, I, I, I, I]),
     "spv_verify_attn": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P, S, P]),
+    "spv_prefill_attn": (I, [P, P, P, P, I, P, I, I, I, I, I, F, P]),
     "spv_time_next_attention": (I, [P, P]),
     "spv_verify_attn_static_max_bytes": (S, []),
     "spv_verify_attn_static": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P]),

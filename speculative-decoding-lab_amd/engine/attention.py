@@ -7,6 +7,9 @@ Drop-in for the reference's engine/attention.py on the verify path:
                                 (plus a merge launch when contexts are split)
 * ``paged_attention_decode`` -- attention.py:96-118 as the one-row case of extend
                                 (``start = length - 1``, chunk 1)
+* ``paged_attention_prefill_chunk`` -- attention.py:121-167, one causal prefill
+                                launch over the dense chunk (``prefill_attention``
+                                takes the lengths as a device tensor)
 * ``_expand_to_q_heads``     -- attention.py:32-38 (kept for API parity; the
                                 kernels never materialise the expansion: kv head
                                 ``h // (Hq/Hkv)`` is indexed directly)
@@ -127,3 +130,46 @@ def paged_attention_decode(query_2d: torch.Tensor, kv: PagedKVCache, layer: int,
     q3 = query_2d.unsqueeze(1)
     out = paged_attention_extend(q3, kv, layer, seq_ids, [x - 1 for x in lengths], num_q_heads)
     return out.squeeze(1)
+
+
+def prefill_attention(query_3d: torch.Tensor, key_3d: torch.Tensor, value_3d: torch.Tensor,
+                      lengths: Union[Sequence[int], torch.Tensor], scale: Optional[float] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Device-argument form of ``paged_attention_prefill_chunk``: ``lengths`` may
+    be an int32 device tensor (no host sync); values above the chunk length are
+    clamped to it."""
+    B, chunk, hq, d = query_3d.shape
+    if tuple(key_3d.shape[:2]) != (B, chunk) or key_3d.shape != value_3d.shape or key_3d.shape[3] != d \
+            or hq % key_3d.shape[2]:
+        raise ValueError("query (B, chunk, Hq, d) and key / value (B, chunk, Hkv, d) do not match")
+    dev = _hip.require_gpu(query_3d.device)
+    if key_3d.device != dev or value_3d.device != dev or key_3d.dtype != query_3d.dtype or \
+            value_3d.dtype != query_3d.dtype:
+        raise ValueError("query, key and value must share a device and dtype")
+    q, k, v = query_3d.contiguous(), key_3d.contiguous(), value_3d.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    if B == 0:
+        return out
+    lens = _hip.i32(lengths, dev)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    call("spv_prefill_attn", ptr(out), ptr(q), ptr(k), ptr(v), _hip.dtype_code(q.dtype), ptr(lens), B, chunk,
+         hq, int(key_3d.shape[2]), d, scale, _hip.stream_of(dev))
+    return out
+
+
+def paged_attention_prefill_chunk(query_3d: torch.Tensor, key_3d: torch.Tensor, value_3d: torch.Tensor,
+                                  num_q_heads: int, chunk_query_lengths: Sequence[int]) -> torch.Tensor:
+    """Causal attention over a freshly prefilled prompt chunk (attention.py:121-167).
+
+    ``query_3d`` (B, chunk, Hq, d), ``key_3d``/``value_3d`` (B, chunk, Hkv, d);
+    row ``b`` position ``j < chunk_query_lengths[b]`` attends ``0 .. j``; the
+    padded tail is zeros. Returns (B, chunk, Hq, d).
+    """
+    B, chunk = int(query_3d.shape[0]), int(query_3d.shape[1])
+    if int(query_3d.shape[2]) != int(num_q_heads):
+        raise ValueError("query has {} heads, expected {}".format(query_3d.shape[2], num_q_heads))
+    lengths = [int(x) for x in chunk_query_lengths]
+    if len(lengths) != B or any(not 0 <= n <= chunk for n in lengths):
+        raise ValueError("one length in [0, chunk] per batch row")
+    return prefill_attention(query_3d, key_3d, value_3d, lengths)

@@ -107,3 +107,92 @@ def test_brute_force_catches_wrong_head_mapping():
     q_mod = q[:, :, [0, 2, 1, 3]]
     bad = brute_force_extend(q_mod, swapped, values, [7], 4)[:, :, [0, 2, 1, 3]]
     assert not torch.allclose(good, bad, atol=1e-3)
+
+
+# ------------------------------------------------------------ prefill chunk
+from oracle.attention import paged_attention_prefill_chunk  # noqa: E402
+
+
+def brute_force_prefill(q, k, v, lengths, num_q_heads):
+    """float64 loops: position j < L_b attends keys 0..j; zeros beyond L_b."""
+    B, C, Hq, d = q.shape
+    ratio = num_q_heads // k.shape[2]
+    out = torch.zeros((B, C, Hq, d), dtype=torch.float64)
+    for b in range(B):
+        for j in range(int(lengths[b])):
+            for h in range(Hq):
+                kh = h // ratio
+                qv = q[b, j, h].double()
+                scores = [float(torch.dot(qv, k[b, t, kh].double())) / math.sqrt(d) for t in range(j + 1)]
+                m = max(scores)
+                w = [math.exp(s - m) for s in scores]
+                tot = sum(w)
+                acc = torch.zeros(d, dtype=torch.float64)
+                for t in range(j + 1):
+                    acc += (w[t] / tot) * v[b, t, kh].double()
+                out[b, j, h] = acc
+    return out
+
+
+def test_prefill_matches_causal_sdpa_on_the_reference_test_shape():
+    # reference tests/test_attention.py:144-164: q = k = v, lengths [4, 6], chunk 6
+    torch.manual_seed(0)
+    Hq, d = 4, 8
+    query = torch.randn(2, 6, Hq, d)
+    out = paged_attention_prefill_chunk(query, query, query, Hq, [4, 6])
+    for index, length in enumerate([4, 6]):
+        block = query[index][:length].transpose(0, 1)[None]
+        want = torch.nn.functional.scaled_dot_product_attention(block, block, block, is_causal=True)[0]
+        assert torch.allclose(out[index][:length], want.transpose(0, 1), atol=1e-5, rtol=1e-5)
+        assert torch.equal(out[index][length:], torch.zeros_like(out[index][length:]))
+
+
+def test_prefill_padding_is_exactly_zero_and_finite():
+    # reference tests/test_attention.py:167-175
+    torch.manual_seed(1)
+    query = torch.randn(2, 5, 4, 8)
+    out = paged_attention_prefill_chunk(query, query, query, 4, [2, 5])
+    assert torch.equal(out[0][2:], torch.zeros_like(out[0][2:]))
+    assert bool(torch.isfinite(out).all())
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(4, 2), (6, 2), (2, 2)])
+def test_prefill_matches_float64_brute_force(Hq, Hkv):
+    g = torch.Generator().manual_seed(Hq * 10 + Hkv)
+    B, C, d = 3, 7, 16
+    q = torch.randn(B, C, Hq, d, generator=g)
+    k = torch.randn(B, C, Hkv, d, generator=g)
+    v = torch.randn(B, C, Hkv, d, generator=g)
+    lengths = [7, 1, 4]
+    out = paged_attention_prefill_chunk(q, k, v, Hq, lengths)
+    want = brute_force_prefill(q, k, v, lengths, Hq)
+    assert torch.allclose(out.double(), want, atol=1e-5, rtol=1e-5)
+
+
+def test_brute_force_prefill_catches_a_shifted_causal_bound():
+    # a mask one key too wide (j + 2 instead of j + 1) must fail the comparison
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(1, 5, 2, 8, generator=g) for _ in range(3))
+    out = paged_attention_prefill_chunk(q, k, v, 2, [5])
+    wrong = torch.zeros_like(out)
+    for j in range(5):
+        n = min(j + 2, 5)
+        s = torch.einsum("hd,thd->ht", q[0, j], k[0, :n]) / math.sqrt(8)
+        wrong[0, j] = torch.einsum("ht,thd->hd", torch.softmax(s, -1), v[0, :n])
+    assert not torch.allclose(out, wrong, atol=1e-3)
+
+
+def test_prefill_equals_extend_from_position_zero():
+    # the chunk attends itself causally: the same as extend with start 0 over
+    # a pool holding the chunk's keys
+    g = torch.Generator().manual_seed(9)
+    Hq, Hkv, d, bs, n = 4, 2, 16, 4, 11
+    q = torch.randn(1, n, Hq, d, generator=g)
+    k = torch.randn(1, n, Hkv, d, generator=g)
+    v = torch.randn(1, n, Hkv, d, generator=g)
+    kv = PagedKVCache(1, Hkv, d, 8, bs)
+    kv.add_sequence(0)
+    kv.write_block(0, [0], [0], k, v)
+    ext = paged_attention_extend(q, kv, 0, [0], [0], Hq)
+    pre = paged_attention_prefill_chunk(q, k, v, Hq, [n])
+    assert torch.allclose(ext, pre, atol=1e-6, rtol=1e-5)
