@@ -773,6 +773,18 @@ def main() -> int:
     g_ar = graph_of(lambda: [(parts["append"](i % REPLICAS), parts["rewind"](i % REPLICAS)) for i in range(reps)],
                     1, torch)
     part_us["append_rewind"] = time_graph(g_ar, 5, torch) * 1000.0 / reps
+    # the same sampling with top-k / top-p filtering of both sides' logits
+    from engine.spec_scheduler import _new_result, verify_sample
+
+    fres = _new_result(B, GAMMA, dev)
+    for name, tk, tp in (("sample_top_k50", 50, 1.0), ("sample_top_p0.9", 0, 0.9)):
+        def filtered(i, tk=tk, tp=tp):
+            target, draft, proposals = w["logits"][i % LOGIT_SETS]
+            verify_sample(target, draft, proposals, w["u"], w["noise"], 1.0, start_pos=w["start"][0], result=fres,
+                          validate=False, top_k=tk, top_p=tp)
+        g_f = graph_of(lambda: [filtered(i) for i in range(4)], 1, torch)
+        part_us[name] = time_graph(g_f, 3, torch) * 1000.0 / 4
+        del g_f
     torch.cuda.synchronize()
     print("bench: timings done", file=sys.stderr, flush=True)
 

@@ -300,6 +300,22 @@ int spv_draft_sample(const float* logits, int64_t row_stride, float temperature,
                      int32_t* out_tokens, int32_t out_stride, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* The top-k / top-p part of logits_to_probs (specdec/sampler.py:19-56) for
+ * `rows` rows of V fp32 logits (row r at logits + r * in_stride, written at
+ * out + r * out_stride): x = z / max(T, 1e-12), then apply_top_k (values below
+ * the k-th largest become -inf, ties at it stay; 0 < top_k < V, else off),
+ * then apply_top_p on what remains (descending order, a value stays while the
+ * softmax mass before it is below top_p; 0 < top_p < 1, else off). out holds
+ * x where it stays and -inf elsewhere: softmax(out) is logits_to_probs, and
+ * out is what spv_verify_sample / spv_draft_sample take at temperature 1.
+ * Masses are summed in fp64; equal values at the nucleus boundary stay in
+ * ascending index order. temperature must be > 0 (greedy rows are not
+ * filtered). One workgroup per row; out may equal logits (same strides). */
+int spv_filter_logits(const float* logits, int64_t in_stride, float* out,
+                      int64_t out_stride, int32_t rows, int32_t V,
+                      float temperature, int32_t top_k, float top_p,
+                      void* stream);
+
 /* logits_to_probs (specdec/sampler.py:19-36) on `rows` rows of V fp32 logits. */
 int spv_logits_to_probs(const float* logits, float* probs, int32_t rows, int32_t V,
                         float temperature, void* stream);

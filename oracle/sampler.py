@@ -2,10 +2,15 @@
 
 Follows the reference:
 
-* ``logits_to_probs``        -- specdec/sampler.py:19-36 with the engine defaults
-                                top_k=0 / top_p=1.0 (specdec/config.py:27-29), i.e.
-                                greedy one-hot at ``argmax`` for T <= 0, else
-                                ``softmax(logits.float() / max(T, 1e-12))``
+* ``logits_to_probs``        -- specdec/sampler.py:19-36: greedy one-hot at
+                                ``argmax`` for T <= 0, else the softmax of
+                                ``logits.float() / max(T, 1e-12)`` after
+                                ``apply_top_k`` then ``apply_top_p`` (no-ops at the
+                                defaults top_k=0 / top_p=1.0, specdec/config.py:27-29)
+* ``apply_top_k``            -- specdec/sampler.py:39-44 (values below the k-th
+                                largest become -inf; ties at it stay)
+* ``apply_top_p``            -- specdec/sampler.py:47-56 (descending sort, cumulative
+                                softmax, the shifted mask ``cum - p >= top_p``)
 * ``acceptance_probability`` -- specdec/sampler.py:86-92 (fp32 -> Python float,
                                 both 1e-12 branches, ``min(1, p/q)`` in float64)
 * ``residual_distribution``  -- specdec/sampler.py:72-83
@@ -18,6 +23,12 @@ Follows the reference:
                                 exponential rows it consumed)
 * ``batch_accept_noise``     -- the same rule with caller-supplied ``u[b][j]`` and
                                 one ``E[b]`` row per sequence
+
+The top-k / top-p filters are pinned by the reference's own filter tests
+(tests/test_sampler.py:34-49, 76-78) and by a brute force that keeps each value
+by counting larger values (top-k) or summing the mass of larger values in
+float64 (top-p), on rows without ties; equal values at the nucleus boundary
+are ordered by torch's (unstable) sort, so which of them stays is unpinned.
 
 Pinned by tests/test_oracle_sampler.py: the reference's one-hot cases
 (tests/test_spec_accept.py:29-73), its sampler properties (tests/test_sampler.py:
@@ -37,13 +48,37 @@ import torch
 EPS = 1e-12  # specdec/sampler.py:16
 
 
-def logits_to_probs(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+def apply_top_k(logits: torch.Tensor, top_k: int) -> torch.Tensor:
+    if top_k <= 0 or top_k >= logits.shape[-1]:
+        return logits
+    kth_value = torch.topk(logits, top_k, dim=-1).values[..., -1, None]
+    return torch.where(logits < kth_value, torch.full_like(logits, float("-inf")), logits)
+
+
+def apply_top_p(logits: torch.Tensor, top_p: float) -> torch.Tensor:
+    if top_p >= 1.0 or top_p <= 0.0:
+        return logits
+    sorted_logits, sorted_index = torch.sort(logits, descending=True, dim=-1)
+    probs = torch.softmax(sorted_logits, dim=-1)
+    mask = torch.cumsum(probs, dim=-1) - probs >= top_p
+    sorted_logits = sorted_logits.masked_fill(mask, float("-inf"))
+    return sorted_logits.scatter(-1, sorted_index, sorted_logits)
+
+
+def logits_to_probs(logits: torch.Tensor, temperature: float, top_k: int = 0,
+                    top_p: float = 1.0) -> torch.Tensor:
     logits = logits.float()
     if temperature <= 0.0:
         probs = torch.zeros_like(logits)
         probs.scatter_(-1, logits.argmax(dim=-1, keepdim=True), 1.0)
         return probs
-    return torch.softmax(logits / max(temperature, EPS), dim=-1)
+    scaled = logits / max(temperature, EPS)
+    return torch.softmax(apply_top_p(apply_top_k(scaled, top_k), top_p), dim=-1)
+
+
+def filter_logits(logits: torch.Tensor, temperature: float, top_k: int = 0, top_p: float = 1.0) -> torch.Tensor:
+    """The scaled, filtered logits whose softmax ``logits_to_probs`` returns (T > 0)."""
+    return apply_top_p(apply_top_k(logits.float() / max(temperature, EPS), top_k), top_p)
 
 
 def acceptance_probability(p: torch.Tensor, q: torch.Tensor, token_id: int) -> float:
@@ -134,10 +169,10 @@ def batch_accept_noise(p: torch.Tensor, q: torch.Tensor, proposals: torch.Tensor
 
 def verify_from_logits(target_logits: torch.Tensor, draft_logits: torch.Tensor,
                        proposals: torch.Tensor, u: torch.Tensor, noise: torch.Tensor,
-                       temperature: float) -> List[List[int]]:
+                       temperature: float, top_k: int = 0, top_p: float = 1.0) -> List[List[int]]:
     """logits_to_probs on every row (spec_scheduler.py:249, 261-263), then accept."""
-    p = logits_to_probs(target_logits, temperature)
-    q = logits_to_probs(draft_logits, temperature)
+    p = logits_to_probs(target_logits, temperature, top_k, top_p)
+    q = logits_to_probs(draft_logits, temperature, top_k, top_p)
     return batch_accept_noise(p, q, proposals, u, noise)
 
 

@@ -63,6 +63,7 @@ SIGNATURES = {
     "spv_verify_sample": (I, [P, P, I, F, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, I, P, S, P]),
     "spv_draft_sample_workspace_bytes": (S, [I, I]),
     "spv_draft_sample": (I, [P, ctypes.c_int64, F, P, I, I, P, I, P, S, P]),
+    "spv_filter_logits": (I, [P, ctypes.c_int64, P, ctypes.c_int64, I, I, F, I, F, P]),
     "spv_logits_to_probs": (I, [P, P, I, I, F, P]),
     "spv_residual": (I, [P, P, P, I, P]),
     "spv_race_argmax": (I, [P, P, I, P, P]),
@@ -124,6 +125,23 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
+
+
+def filtering(top_k: int, top_p: float, vocab: int) -> bool:
+    """Whether top-k / top-p change a row of ``vocab`` logits."""
+    return (0 < int(top_k) < int(vocab)) or (0.0 < float(top_p) < 1.0)
+
+
+def filter_rows(z: torch.Tensor, temperature: float, top_k: int, top_p: float) -> torch.Tensor:
+    """``spv_filter_logits`` over the rows of a float32 (..., V) tensor: the
+    scaled logits with what top-k / top-p drop set to -inf (a new tensor)."""
+    z = z.float().contiguous()
+    V = int(z.shape[-1])
+    rows = z.numel() // V if V else 0
+    out = torch.empty_like(z)
+    call("spv_filter_logits", ptr(z), V, ptr(out), V, rows, V, float(temperature), int(top_k), float(top_p),
+         stream_of(z.device))
+    return out
 
 
 def i32(values, device: torch.device) -> torch.Tensor:

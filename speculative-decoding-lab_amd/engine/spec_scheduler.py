@@ -93,12 +93,16 @@ def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Te
                   u: torch.Tensor, noise: Optional[torch.Tensor], temperature: float,
                   start_pos: Optional[torch.Tensor] = None, remaining: Optional[torch.Tensor] = None,
                   eos_id: Optional[int] = None, is_probs: bool = False,
-                  result: Optional[VerifyResult] = None, validate: bool = True) -> VerifyResult:
+                  result: Optional[VerifyResult] = None, validate: bool = True,
+                  top_k: int = 0, top_p: float = 1.0) -> VerifyResult:
     """Fused accept / resample / bonus / commit cut of one round (device in, device out).
 
     ``target`` (B, gamma+1, V) and ``draft`` (B, gamma, V) are fp32 logits (or
     probabilities with ``is_probs``); ``proposals`` (B, gamma); ``u`` (B, gamma)
     uniforms; ``noise`` (B, V) ``Exp(1)`` rows (unused for greedy logits).
+    ``top_k``/``top_p`` filter both sides' logits first (logits_to_probs,
+    specdec/sampler.py:19-56; sampling mode only): every row is scaled and
+    filtered in one launch, then sampled at temperature 1.
     ``validate=False`` skips the proposal-range check (a host synchronisation).
     """
     dev = _hip.require_gpu(target.device)
@@ -114,6 +118,10 @@ def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Te
         raise ValueError("sampling needs the Exp(1) noise rows")
     t = target.float().contiguous()
     d = draft.float().contiguous()
+    if not greedy and not is_probs and _hip.filtering(top_k, top_p, V):
+        t = _hip.filter_rows(t, temperature, top_k, top_p)
+        d = _hip.filter_rows(d, temperature, top_k, top_p)
+        temperature = 1.0
     x = _hip.i32(proposals, dev)
     if validate and (int(x.min().item()) < 0 or int(x.max().item()) >= V):
         raise IndexError("proposal token ids must lie in [0, V)")
@@ -251,7 +259,7 @@ class VerifyStep:
 
 
 def draft_sample(logits: torch.Tensor, temperature: float, noise: Optional[torch.Tensor] = None,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, top_k: int = 0, top_p: float = 1.0) -> torch.Tensor:
     """One draft step's proposals for every row in one launch (spec_scheduler.py:243-252).
 
     ``logits`` (B, V) fp32 draft logits (rows may be strided, elements
@@ -259,14 +267,17 @@ def draft_sample(logits: torch.Tensor, temperature: float, noise: Optional[torch
     drawn as ``argmax(q / noise[b])`` with the caller's ``Exp(1)`` rows
     ``noise`` (B, V), or the first-index argmax when ``temperature <= 0``
     (``noise`` unused). ``out``: an int32 device view of B entries to write
-    (e.g. column s of the (B, gamma) proposals), else a new tensor. No host
-    synchronisation.
+    (e.g. column s of the (B, gamma) proposals), else a new tensor. ``top_k``
+    / ``top_p`` filter the rows first (sampling mode). No host synchronisation.
     """
     dev = _hip.require_gpu(logits.device)
     if logits.dim() != 2 or logits.stride(1) != 1 or logits.dtype != torch.float32:
         raise ValueError("logits must be a (B, V) float32 tensor with contiguous rows")
     B, V = (int(x) for x in logits.shape)
     greedy = not temperature > 0
+    if not greedy and _hip.filtering(top_k, top_p, V):
+        logits = _hip.filter_rows(logits, temperature, top_k, top_p)
+        temperature = 1.0
     if not greedy:
         if noise is None or tuple(noise.shape) != (B, V) or noise.dtype != torch.float32 or not noise.is_contiguous():
             raise ValueError("sampling needs contiguous float32 Exp(1) rows of shape (B, V)")
@@ -291,16 +302,14 @@ def draft_sample_with_generator(q_logits: torch.Tensor, sampling, generator: tor
     ``generator`` on the host in batch order (also when greedy, where the
     reference's draw from a one-hot row still consumes them), then raced on the
     device. Returns the B token ids; the generator ends where the reference's does."""
-    top_k = getattr(sampling, "top_k", 0)
-    top_p = getattr(sampling, "top_p", 1.0)
-    if (top_k and 0 < top_k < q_logits.shape[-1]) or 0.0 < top_p < 1.0:
-        raise NotImplementedError("draft_sample_with_generator takes unfiltered logits")
+    top_k = int(getattr(sampling, "top_k", 0) or 0)
+    top_p = float(getattr(sampling, "top_p", 1.0))
     z = q_logits.detach().float().contiguous()
     B, V = (int(x) for x in z.shape)
     noise = torch.stack([torch.empty(V, dtype=torch.float32).exponential_(1, generator=generator)
                          for _ in range(B)]) if B else torch.empty(0, V)
     temperature = 0.0 if sampling.is_greedy else float(sampling.temperature)
-    return draft_sample(z, temperature, noise.to(z.device)).tolist()
+    return draft_sample(z, temperature, noise.to(z.device), top_k=top_k, top_p=top_p).tolist()
 
 
 class DraftLoop:

@@ -29,18 +29,34 @@ def _rows(x: torch.Tensor) -> torch.Tensor:
 
 
 def logits_to_probs(logits: torch.Tensor, sampling: SamplingConfig) -> torch.Tensor:
-    """Greedy one-hot (T <= 0) or ``softmax(logits / max(T, 1e-12))`` over the last dim."""
-    top_k = getattr(sampling, "top_k", 0)
-    top_p = getattr(sampling, "top_p", 1.0)
-    if (top_k and 0 < top_k < logits.shape[-1]) or 0.0 < top_p < 1.0:
-        raise NotImplementedError("top-k / top-p filtering is not part of the verify kernels")
+    """Greedy one-hot (T <= 0), else ``softmax`` of ``logits / max(T, 1e-12)``
+    after top-k then top-p filtering (specdec/sampler.py:19-56)."""
+    top_k = int(getattr(sampling, "top_k", 0) or 0)
+    top_p = float(getattr(sampling, "top_p", 1.0))
     z = _rows(logits)
     V = int(z.shape[-1])
     out = torch.empty_like(z)
     rows = z.numel() // V if V else 0
     temperature = 0.0 if sampling.is_greedy else float(sampling.temperature)
+    if temperature > 0 and _hip.filtering(top_k, top_p, V):
+        z = _hip.filter_rows(z, temperature, top_k, top_p)  # scaled and filtered: softmax at T = 1
+        temperature = 1.0
     call("spv_logits_to_probs", ptr(z), ptr(out), rows, V, temperature, _hip.stream_of(z.device))
     return out
+
+
+def apply_top_k(logits: torch.Tensor, top_k: int) -> torch.Tensor:
+    """Values below the k-th largest become -inf (specdec/sampler.py:39-44)."""
+    z = _rows(logits)
+    return _hip.filter_rows(z, 1.0, int(top_k), 1.0).reshape(logits.shape) if _hip.filtering(top_k, 1.0, z.shape[-1]) \
+        else z.reshape(logits.shape)
+
+
+def apply_top_p(logits: torch.Tensor, top_p: float) -> torch.Tensor:
+    """Nucleus filtering (specdec/sampler.py:47-56)."""
+    z = _rows(logits)
+    return _hip.filter_rows(z, 1.0, 0, float(top_p)).reshape(logits.shape) if _hip.filtering(0, top_p, z.shape[-1]) \
+        else z.reshape(logits.shape)
 
 
 def draw_race_noise(vocab: int, generator: Optional[torch.Generator] = None) -> torch.Tensor:

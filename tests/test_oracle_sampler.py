@@ -164,3 +164,63 @@ def test_accept_rule_sampled_chi_square():
     expected = p[0, 0] * N
     chi2 = float(((counts - expected) ** 2 / expected).sum())
     assert chi2 < 24.3  # chi^2_{7} at p = 0.001
+
+
+# ------------------------------------------------------------- top-k / top-p
+def test_top_k_keeps_exactly_k_tokens():
+    # reference tests/test_sampler.py:34-39
+    filtered = S.apply_top_k(torch.tensor([[5.0, 4.0, 3.0, 2.0, 1.0]]), 2)
+    assert torch.isfinite(filtered).sum().item() == 2 and float(filtered[0, 0]) == 5.0
+
+
+def test_top_p_truncates_tail():
+    # reference tests/test_sampler.py:42-48
+    filtered = S.apply_top_p(torch.log(torch.tensor([[0.5, 0.3, 0.15, 0.05]])), 0.8)
+    probs = torch.softmax(filtered, dim=-1)
+    assert float(probs[0, 3]) == 0.0 and float(probs.sum()) >= 0.8 - 1e-6
+
+
+def test_top_p_ignored_when_one():
+    # reference tests/test_sampler.py:76-78
+    logits = torch.randn(1, 8)
+    assert torch.allclose(S.apply_top_p(logits, 1.0), logits)
+
+
+def _brute_keep(x, top_k, top_p):
+    """float64 brute force on a row without ties: top-k keeps a value when
+    fewer than k values are larger; top-p (on what top-k kept) keeps a value
+    when the mass of the kept values larger than it is below p times their
+    total mass."""
+    x = x.double()
+    keep = torch.ones_like(x, dtype=torch.bool)
+    if 0 < top_k < x.numel():
+        for i in range(x.numel()):
+            keep[i] = int((x > x[i]).sum()) < top_k
+    if 0.0 < top_p < 1.0:
+        w = torch.where(keep, torch.exp(x - x[keep].max()), torch.zeros_like(x))
+        tot = float(w.sum())
+        keep2 = keep.clone()
+        for i in range(x.numel()):
+            if keep[i]:
+                keep2[i] = float(w[(x > x[i]) & keep].sum()) < top_p * tot
+        keep = keep2
+    return keep
+
+
+@pytest.mark.parametrize("top_k,top_p", [(5, 1.0), (0, 0.9), (40, 0.5), (3, 0.99), (0, 0.05)])
+def test_filters_match_the_brute_force(top_k, top_p):
+    g = torch.Generator().manual_seed(top_k + int(100 * top_p))
+    for _ in range(3):
+        x = torch.randn(200, generator=g) * 2
+        got = torch.isfinite(S.filter_logits(x, 1.0, top_k, top_p))
+        assert torch.equal(got, _brute_keep(x, top_k, top_p))
+
+
+def test_brute_force_catches_an_unshifted_nucleus_mask():
+    # dropping the value that crosses p (mask cum >= p instead of cum - p >= p)
+    # keeps one value fewer
+    x = torch.log(torch.tensor([0.5, 0.3, 0.15, 0.05]))
+    keep = _brute_keep(x, 0, 0.6)
+    assert keep.tolist() == [True, True, False, False]
+    sorted_p = torch.softmax(x, -1)
+    assert (torch.cumsum(sorted_p, -1) < 0.6).tolist() == [True, False, False, False]
