@@ -20,7 +20,9 @@
  *   rewinds, [3] blocks pushed by the last rewind, [4] last single alloc, [5]
  *   arrival count (zero between calls), [6] sticky 1 + batch index whose
  *   allocation the table width (max_blocks_per_seq) capped, [7] sticky 1 +
- *   batch index of a forbidden attention read (see spv_verify_attn).
+ *   batch index of a forbidden attention read (see spv_verify_attn), [8] sticky
+ *   1 + batch index whose draft cache was shorter than the round's start (see
+ *   spv_kv_draft_align); [9..15] zero.
  *
  * Reference interfaces replaced (paths relative to the reference repository):
  *   engine/kv.py, engine/attention.py, engine/spec_scheduler.py,
@@ -42,7 +44,7 @@ extern "C" {
 #define SPV_ERR_WORKSPACE (-3)
 #define SPV_ERR_UNSUPPORTED (-4)
 
-#define SPV_CTR_WORDS 8
+#define SPV_CTR_WORDS 16
 
 /* element types */
 #define SPV_F32 0
@@ -145,6 +147,50 @@ int spv_kv_rewind(int32_t* block_tables, int32_t max_blocks_per_seq,
                   const int32_t* seq_ids, const int32_t* new_len,
                   const int32_t* finished, int32_t n, int32_t capacity,
                   int32_t block_size, int32_t shrink_only, void* stream);
+
+/* Draft-cache alignment after a verify round (engine/spec_scheduler.py:296-322:
+ * the draft truncate / catch-up / clear of the commit loop, on the draft pool).
+ * Entry i: sequence seq_ids[i] started the round at start_pos[i] = L and
+ * committed n_commit[i] = k tokens, so the target keeps keep = L + k. If k > 0
+ * and the draft cache holds d > keep tokens it is truncated to keep
+ * (PagedKVCache.truncate, engine/kv.py:150-162); if d < keep, positions
+ * d .. keep-1 are caught up: their blocks are allocated as the reference's
+ * draft decode writes would allocate them (engine/kv.py:119-122) and the
+ * length becomes keep; catch_n[i] = keep - d, catch_pos[i] = d and
+ * catch_tok[i][j] = chunk_tokens[i][d - L + j] (the round's chunk row: the
+ * pending token, then the proposals) name the tokens the caller's draft model
+ * must decode there, without allocating (the rest of catch_tok[i] is -1). A
+ * finished sequence (finished[i] != 0) is then cleared (engine/kv.py:164-171)
+ * and gets catch_n = 0. Pops and frees follow the reference's per-sequence
+ * order exactly. d < L (tokens from before the round needed) skips the
+ * catch-up and sets ctr[8] = 1 + i; an exhausted pool sets ctr[1] = 1 + i
+ * and leaves later entries untouched, as the reference's exception does; a
+ * table too narrow sets ctr[6]. kv_scales (fp8 pools, NULL otherwise) get
+ * zero scales for allocated blocks in all num_layers layers. chunk_tokens,
+ * catch_tok: (n, C) int32. 1 <= n <= 1024, seq_ids distinct. One workgroup. */
+int spv_kv_draft_align(int32_t* block_tables, int32_t max_blocks_per_seq,
+                       int32_t* num_blocks, int32_t* seq_lens,
+                       int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                       float* kv_scales, int32_t num_layers,
+                       const int32_t* seq_ids, const int32_t* start_pos,
+                       const int32_t* n_commit, const int32_t* finished,
+                       const int32_t* chunk_tokens, int32_t C,
+                       int32_t* catch_n, int32_t* catch_pos, int32_t* catch_tok,
+                       int32_t n, int32_t capacity, int32_t block_size,
+                       void* stream);
+
+/* One round's record of the scheduler metrics (engine/spec_scheduler.py:200-205
+ * over PagedKVCache.num_allocated_blocks / logical_tokens / kv_stats,
+ * engine/kv.py:186-224), computed on the device so the round needs no host
+ * read: record[0] allocated blocks (capacity - ctr[0]), [1] logical tokens (sum
+ * of seq_lens[0..rows)), [2] longest sequence, [3] B, [4] sum of n_commit[0..B),
+ * [5] count of finished[0..B) != 0 (n_commit / finished may be NULL: 0);
+ * peak (NULL to skip) = max(peak, allocated blocks), i.e. kv_peak_blocks.
+ * record: 6 int64, peak: 1 int64. */
+int spv_pool_metrics(const int32_t* ctr, const int32_t* seq_lens, int32_t rows,
+                     int32_t capacity, const int32_t* n_commit,
+                     const int32_t* finished, int32_t B, int64_t* record,
+                     int64_t* peak, void* stream);
 
 /* gather_ctx (engine/attention.py:41-63): out = (2, length, Hkv, d) in kv_dtype
  * (fp8 pools are dequantised to fp32 with kv_scales, see spv_verify_attn). */

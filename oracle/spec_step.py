@@ -9,8 +9,13 @@ Follows engine/spec_scheduler.py:269-322 of the reference, per sequence in
 3. ``k == 0`` finishes without a truncate (:292-295); otherwise extend
    ``generated``, finish when the budget is reached, and truncate the target
    cache to ``prompt_len + len(generated) - 1`` (:296-303);
-4. align the draft cache: truncate when it is longer than that length (:305-307;
-   the catch-up decode of :308-319 is model work and not part of this path);
+4. align the draft cache (:305-319): truncate when it is longer than that
+   length; when it is shorter, decode the missing positions ``d .. keep - 1``
+   one at a time. The decode itself is model work; what it does to the pool is
+   the write of each position (kv.py:125-147): blocks allocated lazily in
+   logical order (kv.py:119-122) and the length raised to the position + 1.
+   ``catch_up`` restates exactly that and records the positions and tokens
+   (``generated[p - prompt_len]``) the draft model decodes;
 5. finished -> ``clear`` both caches (:320-322).
 
 Under the cache invariant ``seq_len == prompt_len + len(generated) - 1`` the
@@ -49,10 +54,35 @@ def cut_accepted(acc: Sequence[int], remaining: int, eos: Optional[int]) -> Tupl
     return acc, False
 
 
+@dataclass
+class CatchUp:
+    """Draft positions ``pos .. pos + len(tokens) - 1`` decoded to align sequence ``sid``."""
+    sid: int
+    pos: int
+    tokens: List[int]
+    finished: bool = False   # the sequence finished this round (its draft cache is then cleared)
+
+
+def catch_up(draft_kv: PagedKVCache, s: SeqState, keep: int) -> CatchUp:
+    """The pool side of the draft catch-up loop (spec_scheduler.py:308-319):
+    one write per position, in order, as the draft decode's per-layer writes
+    make them (the first layer's write allocates, kv.py:119-122, and raises
+    the length, kv.py:146-147)."""
+    d = draft_kv.seq_lengths[s.sid]
+    toks = []
+    for p in range(d, keep):
+        toks.append(s.generated[p - s.prompt_len])
+        draft_kv._ensure_blocks_up_to(s.sid, p // draft_kv.block_size)
+        if draft_kv.seq_lengths[s.sid] <= p:
+            draft_kv.seq_lengths[s.sid] = p + 1
+    return CatchUp(s.sid, d, toks)
+
+
 def commit_round(running: Sequence[SeqState], accepted_by: Dict[int, List[int]],
                  kv: PagedKVCache, draft_kv: Optional[PagedKVCache] = None,
-                 eos: Optional[int] = None) -> List[int]:
-    """Apply one round's commit to ``kv`` (and ``draft_kv``); returns k per sequence."""
+                 eos: Optional[int] = None, catchups: Optional[List[CatchUp]] = None) -> List[int]:
+    """Apply one round's commit to ``kv`` (and ``draft_kv``); returns k per sequence.
+    Draft catch-ups are appended to ``catchups`` when it is given."""
     ks = []
     for s in running:
         acc, eos_hit = cut_accepted(accepted_by[s.sid], s.max_new_tokens - len(s.generated), eos)
@@ -69,8 +99,15 @@ def commit_round(running: Sequence[SeqState], accepted_by: Dict[int, List[int]],
                 s.finished = True
             keep = s.prompt_len + len(s.generated) - 1
             kv.truncate(s.sid, keep)
-            if draft_kv is not None and draft_kv.seq_lengths[s.sid] > keep:
-                draft_kv.truncate(s.sid, keep)
+            if draft_kv is not None:
+                d_len = draft_kv.seq_lengths[s.sid]
+                if d_len > keep:
+                    draft_kv.truncate(s.sid, keep)
+                elif d_len < keep:
+                    c = catch_up(draft_kv, s, keep)
+                    c.finished = s.finished
+                    if catchups is not None:
+                        catchups.append(c)
         if s.finished:
             kv.clear(s.sid)
             if draft_kv is not None:

@@ -763,6 +763,315 @@ __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
   ctr[CTR_SLOWPATH] += 1;
 }
 
+// ------------------------------------------------------------------ draft alignment
+//
+// After a verify round the draft cache follows the target's commit
+// (spec_scheduler.py:296-322). Sequence i of the batch started the round at
+// L = start_pos[i] and committed k = n_commit[i] tokens; the target keeps
+// keep = L + k. When k > 0 a draft cache of d tokens is truncated to keep
+// (d > keep; kv.py:150-162) or caught up to it (d < keep): the draft model
+// decodes positions d .. keep - 1, and their writes allocate blocks lazily
+// (kv.py:119-122, popping the free stack). A finished sequence's draft cache
+// is then cleared (kv.py:164-171). The reference does this sequence by
+// sequence in batch order, so the free stack sees each sequence's pops and
+// pushes in turn. The kernel replays that order exactly: the batch is cut at
+// the sequences whose catch-up needs new blocks; each run of sequences
+// between cuts frees its blocks in parallel (push_run), and each cut sequence
+// pops its blocks from the top in between. Catch-up positions receive their
+// blocks and the length keep here; the caller's draft decode then writes
+// their keys and values without allocating.
+
+struct RunLds {
+  int scan[kPoolThreads / 64];
+  int off[kPoolThreads], cnt[kPoolThreads], ft[kPoolThreads], nb[kPoolThreads], sid[kPoolThreads];
+  int nbf[kPoolThreads], lenf[kPoolThreads];
+  short owner[kRewindItems];
+};
+
+// Block k of run entry o: its truncated tail first (tail-first), then its
+// remaining blocks in forward order.
+__device__ __forceinline__ int run_block(const RunLds& S, int o, int k, const int32_t* __restrict__ tables, int maxb) {
+  const size_t row = (size_t)S.sid[o] * maxb;
+  return tables[row + (k < S.ft[o] ? S.nb[o] - 1 - k : k - S.ft[o])];
+}
+
+// Frees of one run of entries (thread i holds entry i, `act` when it is in
+// the run), in the order the sequential calls make them: entry i's blocks go
+// to top + (blocks of the run's entries before i) + k. Windows of
+// kRewindItems blocks spread the blocks over the threads. Every block is
+// marked pending (+2 on its flag) first; a block already free, listed twice
+// or outside the pool undoes the marks and returns -1 (nothing changed), and
+// the caller replays the run one block at a time. Otherwise returns the new
+// stack height. Every thread calls it.
+__device__ int push_run(RunLds& S, bool act, const RewindEntry& e, int top, const int32_t* __restrict__ tables,
+                        int maxb, int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag, int cap) {
+  const int i = threadIdx.x;
+  const int cnt = act ? e.ft + e.fc : 0;
+  int total;
+  const int off = block_exclusive_scan(cnt, S.scan, &total);
+  S.off[i] = off;
+  S.cnt[i] = cnt;
+  S.ft[i] = e.ft;
+  S.nb[i] = e.nb;
+  S.sid[i] = e.sid;
+  S.nbf[i] = e.nb_final;
+  S.lenf[i] = e.len_final;
+  // pass 0 marks, pass 1 places (or undoes the marks)
+  bool dup = false;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int w0 = 0; w0 < total; w0 += kRewindItems) {
+      const int wn = min(kRewindItems, total - w0);
+      __syncthreads();  // the previous window's readers of `owner` are done
+      if (cnt > 0) {
+        const int k1 = min(cnt, w0 + wn - off);
+        for (int k = max(0, w0 - off); k < k1; ++k) S.owner[off + k - w0] = (short)i;
+      }
+      __syncthreads();
+      int ids[kRewindRounds];
+#pragma unroll
+      for (int j = 0; j < kRewindRounds; ++j) {
+        const int t = i + j * kPoolThreads;
+        ids[j] = -1;
+        if (t < wn) {
+          const int o = S.owner[t];
+          ids[j] = run_block(S, o, w0 + t - S.off[o], tables, maxb);
+        }
+      }
+      if (pass == 0) {
+        int old[kRewindRounds];
+#pragma unroll
+        for (int j = 0; j < kRewindRounds; ++j) {
+          old[j] = 0;
+          if (i + j * kPoolThreads < wn) {
+            if ((unsigned)ids[j] >= (unsigned)cap) dup = true;
+            else old[j] = atomicAdd(&free_flag[ids[j]], 2);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kRewindRounds; ++j) dup |= old[j] != 0;
+      } else {
+#pragma unroll
+        for (int j = 0; j < kRewindRounds; ++j) {
+          const int t = i + j * kPoolThreads;
+          if (t >= wn) continue;
+          if (!dup) {
+            free_stack[top + w0 + t] = ids[j];
+            free_flag[ids[j]] = 1;
+          } else if ((unsigned)ids[j] < (unsigned)cap) {
+            atomicSub(&free_flag[ids[j]], 2);
+          }
+        }
+      }
+    }
+    if (pass == 0) dup = __syncthreads_or(dup);
+  }
+  __syncthreads();
+  return dup ? -1 : top + total;
+}
+
+__global__ __launch_bounds__(kPoolThreads) void kv_align_kernel(
+    int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks, int32_t* __restrict__ seq_lens,
+    int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
+    float* __restrict__ scales, int32_t num_layers, const int32_t* __restrict__ seq_ids,
+    const int32_t* __restrict__ start_pos, const int32_t* __restrict__ n_commit,
+    const int32_t* __restrict__ finished, const int32_t* __restrict__ chunk_tokens, int32_t C,
+    int32_t* __restrict__ catch_n, int32_t* __restrict__ catch_pos, int32_t* __restrict__ catch_tok, int32_t n,
+    int32_t bs, int32_t cap) {
+  __shared__ RunLds S;
+  __shared__ int s_top, s_next, s_stop, s_slow, s_pushed, s_ovf, s_behind;
+  const int i = threadIdx.x;
+  const bool act = i < n;
+  if (i == 0) {
+    s_top = ctr[CTR_TOP];
+    s_stop = s_slow = s_pushed = 0;
+    s_ovf = s_behind = n;
+  }
+  __syncthreads();
+  int sid = 0, d = 0, nb = 0, keep = 0, need = 0;
+  bool fin = false, trunc = false, catchup = false;
+  if (act) {
+    sid = seq_ids[i];
+    const int L = start_pos[i], k = n_commit[i];
+    fin = finished[i] != 0;
+    d = seq_lens[sid];
+    nb = nblocks[sid];
+    keep = L + k;
+    int cn = 0;
+    if (k > 0 && d > keep) {
+      trunc = true;
+    } else if (k > 0 && d < keep) {
+      if (d < L) {
+        atomicMin(&s_behind, i);  // the catch-up would need tokens from before the round
+      } else {
+        catchup = true;
+        const int want = max(0, (keep + bs - 1) / bs - nb);
+        need = min(want, max(0, maxb - nb));
+        if (need < want) atomicMin(&s_ovf, i);
+        // (positions beyond the chunk's tokens are not caught up: k <= C)
+        cn = fin ? 0 : max(0, min(min(keep, (nb + need) * bs) - d, C - (d - L)));
+      }
+    }
+    // Position p of the catch-up holds the chunk's token p - L (the pending
+    // token, then the accepted proposals): d - L + j <= k - 1 <= C - 1.
+    catch_n[i] = cn;
+    catch_pos[i] = d;
+    const size_t row = (size_t)i * C;
+    for (int j = 0; j < C; ++j) catch_tok[row + j] = j < cn ? chunk_tokens[row + (d - L) + j] : -1;
+  }
+  bool pending = need > 0;  // pops not yet made
+  int lo = 0;
+  while (lo < n) {
+    if (i == 0) s_next = n;
+    __syncthreads();
+    if (act && i >= lo && pending) atomicMin(&s_next, i);
+    __syncthreads();
+    const int p = s_next;
+    if (p == lo) {
+      // Entry p pops its catch-up blocks (kv.py:62-68 through kv.py:119-122).
+      if (i == p) {
+        int top = s_top, got = 0;
+        const size_t row = (size_t)sid * maxb;
+        for (; got < need && top > 0; ++got) {
+          const int id = free_stack[--top];
+          free_flag[id] = 0;
+          tables[row + nb + got] = id;
+          if (scales)  // an fp8 pool: the block starts with zero scales in every layer
+            for (int l = 0; l < num_layers; ++l)
+              *reinterpret_cast<float2*>(&scales[((size_t)l * cap + id) * 2]) = make_float2(0.f, 0.f);
+        }
+        nb += got;
+        nblocks[sid] = nb;
+        if (got < need) {
+          // The reference raises at the first position without a block: the
+          // positions before it were written, later sequences are not touched.
+          seq_lens[sid] = max(d, min(keep, nb * bs));
+          ctr[CTR_EXHAUSTED] = p + 1;
+          s_stop = 1;
+        }
+        s_top = top;
+        pending = false;
+      }
+      __syncthreads();
+      if (s_stop) break;
+      continue;  // entry p's own frees (a clear) open the next run
+    }
+    // Frees of entries [lo, p): truncations and clears.
+    const bool in_run = act && i >= lo && i < p;
+    RewindEntry e{};
+    if (in_run) {
+      e.sid = sid;
+      e.nb = nb;
+      int nb1 = nb, len1 = d;
+      if (trunc) {
+        e.ft = max(0, nb - (keep + bs - 1) / bs);
+        nb1 = nb - e.ft;
+        len1 = keep;
+      } else if (catchup) {
+        len1 = min(keep, nb * bs);
+      }
+      e.fc = fin ? nb1 : 0;
+      e.nb_final = fin ? 0 : nb1;
+      e.len_final = fin ? 0 : len1;
+    }
+    const int top = s_top;
+    const int nt = push_run(S, in_run, e, top, tables, maxb, free_stack, free_flag, cap);
+    if (nt >= 0) {
+      if (in_run) {
+        nblocks[sid] = e.nb_final;
+        seq_lens[sid] = e.len_final;
+      }
+      if (i == 0) {
+        s_pushed += nt - top;
+        s_top = nt;
+      }
+    } else if (i == 0) {
+      // The reference's rule `if block in free_list: return` (kv.py:73-74),
+      // one block at a time.
+      int t = top;
+      for (int o = lo; o < p; ++o) {
+        for (int k = 0; k < S.cnt[o]; ++k) {
+          const int id = run_block(S, o, k, tables, maxb);
+          if ((unsigned)id < (unsigned)cap && t < cap && atomicOr(&free_flag[id], 0) == 0) {
+            free_stack[t++] = id;
+            atomicExch(&free_flag[id], 1);
+          }
+        }
+        nblocks[S.sid[o]] = S.nbf[o];
+        seq_lens[S.sid[o]] = S.lenf[o];
+      }
+      s_pushed += t - top;
+      s_top = t;
+      s_slow = 1;
+    }
+    __syncthreads();
+    lo = p;
+  }
+  __syncthreads();
+  if (i == 0) {
+    ctr[CTR_TOP] = s_top;
+    ctr[CTR_PUSHED] = s_pushed;
+    if (s_slow) ctr[CTR_SLOWPATH] += 1;
+    if (s_ovf < n) ctr[CTR_OVERFLOW] = s_ovf + 1;
+    if (s_behind < n) ctr[CTR_ALIGN] = s_behind + 1;
+  }
+}
+
+// ------------------------------------------------------------------ metrics
+//
+// One round's record of the scheduler metrics (spec_scheduler.py:200-205 over
+// kv.py:186-224): record[0] allocated blocks (capacity - free count), [1]
+// logical tokens (sum of the sequence lengths), [2] longest sequence, [3]
+// batch entries, [4] tokens committed (sum of n_commit), [5] sequences
+// finished; peak[0] = max(peak[0], allocated blocks).
+__global__ __launch_bounds__(kPoolThreads) void pool_metrics_kernel(
+    const int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_lens, int32_t rows, int32_t cap,
+    const int32_t* __restrict__ n_commit, const int32_t* __restrict__ finished, int32_t B,
+    long long* __restrict__ record, long long* __restrict__ peak) {
+  __shared__ long long s_sum[kPoolThreads / 64][3];
+  __shared__ int s_max[kPoolThreads / 64];
+  long long tok = 0, com = 0, fin = 0;
+  int mx = 0;
+  for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+    const int len = seq_lens[r];
+    tok += len;
+    mx = max(mx, len);
+  }
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    if (n_commit) com += n_commit[b];
+    if (finished) fin += finished[b] != 0;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    tok += __shfl_xor(tok, o, 64);
+    com += __shfl_xor(com, o, 64);
+    fin += __shfl_xor(fin, o, 64);
+    mx = max(mx, __shfl_xor(mx, o, 64));
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_sum[w][0] = tok;
+    s_sum[w][1] = com;
+    s_sum[w][2] = fin;
+    s_max[w] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < (int)(blockDim.x >> 6); ++k) {
+      tok += s_sum[k][0];
+      com += s_sum[k][1];
+      fin += s_sum[k][2];
+      mx = max(mx, s_max[k]);
+    }
+    const long long alloc = (long long)cap - ctr[CTR_TOP];
+    record[0] = alloc;
+    record[1] = tok;
+    record[2] = mx;
+    record[3] = B;
+    record[4] = com;
+    record[5] = fin;
+    if (peak && alloc > peak[0]) peak[0] = alloc;
+  }
+}
+
 // gather_ctx: out[0][p][h][e] = K, out[1][p][h][e] = V for p < length.
 template <int DT, bool DEQ>
 __global__ void kv_gather_kernel(const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
@@ -973,6 +1282,37 @@ int spv_kv_rewind(int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* nu
   hipLaunchKernelGGL(kv_rewind_kernel, dim3(1), dim3(kPoolThreads), 0, (hipStream_t)stream, block_tables,
                      max_blocks_per_seq, num_blocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len,
                      finished, n, block_size, shrink_only, capacity);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_kv_draft_align(int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
+                       int32_t* free_stack, int32_t* free_flag, int32_t* ctr, float* kv_scales, int32_t num_layers,
+                       const int32_t* seq_ids, const int32_t* start_pos, const int32_t* n_commit,
+                       const int32_t* finished, const int32_t* chunk_tokens, int32_t C, int32_t* catch_n,
+                       int32_t* catch_pos, int32_t* catch_tok, int32_t n, int32_t capacity, int32_t block_size,
+                       void* stream) {
+  if (!block_tables || !num_blocks || !seq_lens || !free_stack || !free_flag || !ctr || !seq_ids || !start_pos ||
+      !n_commit || !finished || !chunk_tokens || !catch_n || !catch_pos || !catch_tok || n < 0 ||
+      n > kPoolThreads || C < 1 || capacity < 1 || block_size < 1 || max_blocks_per_seq < 1 ||
+      (kv_scales && num_layers < 1))
+    return SPV_ERR_ARG;
+  if (n == 0) return SPV_OK;
+  hipLaunchKernelGGL(kv_align_kernel, dim3(1), dim3(kPoolThreads), 0, (hipStream_t)stream, block_tables,
+                     max_blocks_per_seq, num_blocks, seq_lens, free_stack, free_flag, ctr, kv_scales, num_layers,
+                     seq_ids, start_pos, n_commit, finished, chunk_tokens, C, catch_n, catch_pos, catch_tok, n,
+                     block_size, capacity);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_pool_metrics(const int32_t* ctr, const int32_t* seq_lens, int32_t rows, int32_t capacity,
+                     const int32_t* n_commit, const int32_t* finished, int32_t B, int64_t* record, int64_t* peak,
+                     void* stream) {
+  if (!ctr || (!seq_lens && rows > 0) || rows < 0 || capacity < 1 || B < 0 || !record) return SPV_ERR_ARG;
+  hipLaunchKernelGGL(pool_metrics_kernel, dim3(1), dim3(kPoolThreads), 0, (hipStream_t)stream, ctr, seq_lens, rows,
+                     capacity, n_commit, finished, B, reinterpret_cast<long long*>(record),
+                     reinterpret_cast<long long*>(peak));
   SPV_CHECK_LAUNCH();
   return SPV_OK;
 }

@@ -29,6 +29,7 @@ enum : int {
   CTR_ARRIVE = 5,     // arrival count of the one-launch append (zero between launches)
   CTR_OVERFLOW = 6,   // sticky: 1 + batch index of a sequence whose table width capped an allocation
   CTR_BAD_READ = 7,   // sticky: 1 + batch index of an attention row over an unwritten / out-of-pool page
+  CTR_ALIGN = 8,      // sticky: 1 + batch index whose draft cache is shorter than the round's start
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) {

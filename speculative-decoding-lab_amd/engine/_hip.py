@@ -21,9 +21,9 @@ SPV_ERR_ARG = -1
 SPV_ERR_LAUNCH = -2
 SPV_ERR_WORKSPACE = -3
 SPV_ERR_UNSUPPORTED = -4
-SPV_CTR_WORDS = 8
+SPV_CTR_WORDS = 16
 CTR_TOP, CTR_EXHAUSTED, CTR_SLOWPATH, CTR_PUSHED = 0, 1, 2, 3
-CTR_OVERFLOW, CTR_BAD_READ = 6, 7  # sticky error words (see include/specverify.h)
+CTR_OVERFLOW, CTR_BAD_READ, CTR_ALIGN = 6, 7, 8  # sticky error words (see include/specverify.h)
 
 SPV_F32, SPV_BF16, SPV_F16, SPV_FP8E4M3 = 0, 1, 2, 3
 _DTYPE_CODE = {torch.float32: SPV_F32, torch.bfloat16: SPV_BF16, torch.float16: SPV_F16}
@@ -51,6 +51,8 @@ SIGNATURES = {
     "spv_kv_append": (I, [P, P, I, P, P, P, I, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
     "spv_kv_append_fp8": (I, [P, P, P, I, P, P, P, I, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "spv_kv_rewind": (I, [P, I, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "spv_kv_draft_align": (I, [P, I, P, P, P, P, P, P, I, P, P, P, P, P, I, P, P, P, I, I, I, P]),
+    "spv_pool_metrics": (I, [P, P, I, I, P, P, I, P, P, P]),
     "spv_kv_gather": (I, [P, P, I, P, P, I, I, I, I, I, I, I, I, P, P]),
     "spv_kv_read_blocks": (I, [P, I, I, P, I, I, I, I, I, I, P, P]),
     "spv_verify_attn_workspace_bytes": (S, [I, I, I, I, I, I, I]),

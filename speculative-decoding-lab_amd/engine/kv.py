@@ -194,7 +194,7 @@ class PagedKVCache:
             self.allocator._refresh()
             self._stale = False
             ctr = self.allocator.ctr.tolist()
-            words = (_hip.CTR_EXHAUSTED, _hip.CTR_OVERFLOW, _hip.CTR_BAD_READ)
+            words = (_hip.CTR_EXHAUSTED, _hip.CTR_OVERFLOW, _hip.CTR_BAD_READ, _hip.CTR_ALIGN)
             if not any(ctr[w] for w in words):
                 return
             # One error is raised; the others set since the last query follow
@@ -209,9 +209,12 @@ class PagedKVCache:
                 raise IndexError("batch entry {}: the chunk needs more than max_blocks_per_seq={} blocks; "
                                  "its table was filled and the tokens beyond it were not written".format(
                                      ctr[_hip.CTR_OVERFLOW] - 1, self._maxb))
-            raise IndexError("batch entry {}: verify attention read positions that were never written "
-                             "(or a block id outside the pool, or beyond max_ctx)".format(
-                                 ctr[_hip.CTR_BAD_READ] - 1))
+            if ctr[_hip.CTR_BAD_READ]:
+                raise IndexError("batch entry {}: verify attention read positions that were never written "
+                                 "(or a block id outside the pool, or beyond max_ctx)".format(
+                                     ctr[_hip.CTR_BAD_READ] - 1))
+            raise ValueError("batch entry {}: the draft cache is shorter than the round's start position; "
+                             "its catch-up needs tokens from before the round".format(ctr[_hip.CTR_ALIGN] - 1))
 
     def _grow_rows(self, n: int) -> None:
         if n <= self._max_seqs:
@@ -442,6 +445,45 @@ class PagedKVCache:
              self.allocator.capacity, self.block_size, 1 if shrink_only else 0, self._stream())
         self._stale = True
         self.allocator._stale = True
+
+    def align_device(self, seq_ids: torch.Tensor, start_pos: torch.Tensor, n_commit: torch.Tensor,
+                     finished: torch.Tensor, chunk_tokens: torch.Tensor, catch_n: torch.Tensor,
+                     catch_pos: torch.Tensor, catch_tok: torch.Tensor, max_len: Optional[int] = None) -> None:
+        """Align this (draft) cache with a round's commit on the device
+        (engine/spec_scheduler.py:296-322): truncate to ``start + n_commit``,
+        or allocate and lengthen for the catch-up positions (reported in
+        ``catch_*`` for the draft model to decode), then clear the finished
+        sequences -- in the reference's per-sequence order. ``max_len`` (a bound
+        on ``start + n_commit``) widens the tables beforehand; without it a
+        catch-up beyond the table width is capped and reported. No host
+        synchronisation."""
+        n = int(seq_ids.numel())
+        if n == 0:
+            return
+        if n > 1024:
+            raise ValueError("draft alignment takes at most 1024 sequences per call")
+        C = int(chunk_tokens.shape[1])
+        if max_len is not None:
+            self._grow_width(-(-int(max_len) // self.block_size))
+        call("spv_kv_draft_align", ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
+             ptr(self.allocator.free_stack), ptr(self.allocator.free_flag), ptr(self.allocator.ctr), ptr(self.scales),
+             self.num_layers, ptr(seq_ids), ptr(start_pos), ptr(n_commit), ptr(finished), ptr(chunk_tokens), C,
+             ptr(catch_n), ptr(catch_pos), ptr(catch_tok), n, self.allocator.capacity, self.block_size,
+             self._stream())
+        self._stale = True
+        self.allocator._stale = True
+
+    def metrics_device(self, record: torch.Tensor, peak: Optional[torch.Tensor] = None,
+                       n_commit: Optional[torch.Tensor] = None, finished: Optional[torch.Tensor] = None,
+                       batch: int = 0) -> None:
+        """Write one round's metrics record on the device (no host read):
+        ``record`` (6 int64) = allocated blocks, logical tokens, longest
+        sequence, ``batch``, sum of ``n_commit``, finished count; ``peak`` (1
+        int64) tracks the most blocks allocated (engine/spec_scheduler.py:200-205,
+        engine/kv.py:186-224)."""
+        rows = len(self._nb)
+        call("spv_pool_metrics", ptr(self.allocator.ctr), ptr(self.lens_dev), rows, self.allocator.capacity,
+             ptr(n_commit), ptr(finished), int(batch), ptr(record), ptr(peak), self._stream())
 
     def truncate(self, seq_id: int, new_len: int) -> None:
         """Rewind to ``new_len`` positions, freeing the table tail tail-first (kv.py:150-162)."""

@@ -23,6 +23,9 @@ Drop-in for the verify part of the reference's engine/spec_scheduler.py:
 * ``DraftLoop``     -- the paged part of the gamma draft decode steps (per layer
   one-token append + decode attention, engine/model.py:123-153) and each step's
   sampling, with device-resident positions so the loop captures as one graph.
+* ``align_draft``   -- the draft cache's side of the commit
+  (spec_scheduler.py:296-322: truncate, catch-up allocation, clear) in one
+  launch on the device, reporting the catch-up tokens the draft model decodes.
 """
 
 from __future__ import annotations
@@ -82,6 +85,43 @@ def _launch_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.T
          ptr(r.n_commit) if r else None, ptr(r.finished) if r else None,
          ptr(r.new_len) if r else None, ptr(accept_prob), 1 if decide_only else 0,
          ptr(ws), int(ws_bytes), _hip.stream_of(dev))
+
+
+@dataclass
+class DraftCatchUp:
+    """Device int32 outputs of a draft alignment: sequence b's draft model
+    decodes ``tokens[b, :count[b]]`` at positions ``pos[b], pos[b] + 1, ...``
+    (blocks and length are already in place; ``tokens`` is -1 padded)."""
+
+    count: torch.Tensor    # (B,)
+    pos: torch.Tensor      # (B,)
+    tokens: torch.Tensor   # (B, gamma+1)
+
+
+def align_draft(draft_kv: PagedKVCache, seq_ids: torch.Tensor, start_pos: torch.Tensor, result: VerifyResult,
+                chunk_tokens: torch.Tensor, out: Optional[DraftCatchUp] = None) -> DraftCatchUp:
+    """Align the draft cache with a verify round's commit (spec_scheduler.py:296-322).
+
+    ``seq_ids``/``start_pos`` (B,) int32 device: the round's sequences and their
+    start positions; ``result``: the round's ``VerifyResult`` (``n_commit``,
+    ``finished``); ``chunk_tokens`` (B, gamma+1) int32 device: the verify
+    chunk's tokens (the pending token, then the proposals). Per sequence, in
+    batch order: the draft cache is truncated to ``start + n_commit`` when
+    longer; when shorter, the missing positions get their blocks (in the
+    reference's allocation order) and the returned catch-up names the tokens
+    to decode there; finished sequences are cleared. No host synchronisation.
+    """
+    dev = draft_kv.device
+    B = int(seq_ids.numel())
+    C = int(chunk_tokens.shape[1]) if chunk_tokens.dim() == 2 else 0
+    if chunk_tokens.shape[0] != B or chunk_tokens.dtype != torch.int32 or not chunk_tokens.is_contiguous():
+        raise ValueError("chunk_tokens must be a contiguous (B, gamma+1) int32 tensor")
+    if out is None:
+        out = DraftCatchUp(torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int32, device=dev),
+                           torch.empty((B, C), dtype=torch.int32, device=dev))
+    draft_kv.align_device(seq_ids, start_pos, result.n_commit, result.finished, chunk_tokens,
+                          out.count, out.pos, out.tokens)
+    return out
 
 
 def _new_result(B: int, gamma: int, dev: torch.device) -> VerifyResult:

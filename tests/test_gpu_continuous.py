@@ -79,6 +79,115 @@ def test_continuous_batching_matches_oracle(cuda, eos):
     assert res.kv_peak_blocks <= cap
 
 
+@pytest.mark.parametrize("temperature,eos", [(1.0, None), (1.0, 5), (0.0, None)])
+def test_continuous_with_draft_side_matches_oracle(cuda, temperature, eos):
+    """The whole round with a draft pool: gamma draft steps (append + decode
+    attention per draft layer, batched sampling), verify, commit, the device
+    draft alignment and its catch-up decode, replayed by the oracle; both pools
+    identical after every round, and the device metrics equal to the mirror's
+    counts at every record point."""
+    L, Hq, Hkv, d, bs, V, gamma, max_batch, cap = 2, 4, 2, 16, 4, 24, 3, 5, 40
+    DL, dHq, dHkv, dd = 2, 2, 1, 16
+    model = SyntheticVerifyModel(L, Hq, Hkv, d, V, gamma, max_batch, cuda, torch.float32, seed=7,
+                                 draft_sigma=0.3, prompt_cap=48, n_sets=3, temperature=max(temperature, 1e-3),
+                                 draft_layers=DL, draft_heads=(dHq, dHkv, dd))
+    gpu = PagedKVCache(L, Hkv, d, cap, bs, cuda, torch.float32)
+    gpu_d = PagedKVCache(DL, dHkv, dd, cap, bs, cuda, torch.float32)
+    cpu = ref.PagedKVCache(L, Hkv, d, cap, bs)
+    cpu_d = ref.PagedKVCache(DL, dHkv, dd, cap, bs)
+    reqs = poisson_requests(12, 2.0, 3, 30, 2, 14, seed=9)
+    by_sid = {r.sid: r for r in reqs}
+    drv = SpecContinuousDriver(gpu, model, gamma, max_batch, temperature=temperature, eos_id=eos, draft_kv=gpu_d)
+    mirror = {}
+    seen = {"rounds": 0, "catch_ups": 0, "catch_up_rounds": 0, "records": []}
+
+    record = drv._record
+
+    def checked_record(result):
+        record(result)
+        seen["records"].append((gpu.num_allocated_blocks, gpu.logical_tokens, gpu_d.num_allocated_blocks))
+
+    drv._record = checked_record
+
+    def on_round(info):
+        for sid in info.sids:
+            if sid not in mirror:
+                r = by_sid[sid]
+                cpu.add_sequence(sid)
+                cpu_d.add_sequence(sid)
+                k, v = model.prompt_kv(r.prompt_len)
+                for layer in range(L):
+                    cpu.write_block(layer, [sid], [0], k.cpu(), v.cpu())
+                dk, dv = model.draft_prompt_kv(r.prompt_len)
+                for layer in range(DL):
+                    cpu_d.write_block(layer, [sid], [0], dk.cpu(), dv.cpu())
+                mirror[sid] = SeqState(sid, r.prompt_len, r.max_new_tokens, [0])
+        running = [mirror[s] for s in info.sids]
+        inp = info.inputs
+        assert info.starts == [cpu_d.seq_lengths[s] for s in info.sids]
+        # the gamma draft steps
+        props = inp["proposals"].cpu()
+        for j in range(gamma):
+            pos = [st + j for st in info.starts]
+            for layer in range(DL):
+                cpu_d.write_block(layer, info.sids, pos, inp["dk"][j][layer].cpu(), inp["dv"][j][layer].cpu())
+                want = ref_attn.paged_attention_extend(inp["dq"][j][layer].cpu(), cpu_d, layer, info.sids, pos, dHq)
+                torch.testing.assert_close(info.draft_outputs[j][layer].cpu(), want, atol=1e-5, rtol=1e-5)
+            for b in range(len(info.sids)):
+                q = S.logits_to_probs(inp["draft"][b, j].cpu(), temperature)
+                tok = S.race_argmax(q, inp["draft_noise"][j][b].cpu()) if temperature > 0 else int(q.argmax())
+                assert int(props[b, j]) == tok, (b, j)
+        # verify
+        for layer in range(L):
+            cpu.write_block(layer, info.sids, info.starts, inp["k"][layer].cpu(), inp["v"][layer].cpu())
+            want = ref_attn.paged_attention_extend(inp["q"][layer].cpu(), cpu, layer, info.sids, info.starts, Hq)
+            torch.testing.assert_close(info.outputs[layer].cpu(), want, atol=1e-5, rtol=1e-5)
+        acc = S.verify_from_logits(inp["target"].cpu(), inp["draft"].cpu(), props, inp["u"].cpu(),
+                                   inp["noise"].cpu(), temperature)
+        assert info.result.accepted_lists() == acc
+        catchups = []
+        ks = commit_round(running, dict(zip(info.sids, acc)), cpu, cpu_d, eos=eos, catchups=catchups)
+        assert info.result.n_commit.tolist() == ks
+        # the catch-up: positions, tokens and its decode
+        count, cpos, ctok = (x.tolist() for x in (info.catch_up.count, info.catch_up.pos, info.catch_up.tokens))
+        live = {c.sid: c for c in catchups if not c.finished}
+        for b, sid in enumerate(info.sids):
+            c = live.get(sid)
+            assert count[b] == (len(c.tokens) if c else 0), b
+            if c:
+                assert cpos[b] == c.pos and ctok[b][: count[b]] == c.tokens
+        rows = info.catch_up_rows or []
+        assert rows == [b for b in range(len(info.sids)) if count[b]]
+        for layer in range(DL):
+            for b in rows:
+                cpu_d.write(layer, info.sids[b], cpos[b], inp["dk"][0][layer][b, 0].cpu(), inp["dv"][0][layer][b, 0].cpu())
+            if rows:
+                sids_r = [info.sids[b] for b in rows]
+                want = ref_attn.paged_attention_extend(inp["dq"][0][layer][rows].cpu(), cpu_d, layer, sids_r,
+                                                       [cpos[b] for b in rows], dHq)
+                torch.testing.assert_close(info.catch_up_outputs[layer].cpu(), want, atol=1e-5, rtol=1e-5)
+        seen["catch_ups"] += len(rows)
+        seen["catch_up_rounds"] += 1 if rows else 0
+        for g, c in ((gpu, cpu), (gpu_d, cpu_d)):
+            assert g.block_tables == c.block_tables
+            assert g.seq_lengths == c.seq_lengths
+            assert g.allocator.free_list() == c.allocator.free_list
+        seen["rounds"] += 1
+
+    res = drv.run(reqs, max_steps=400, on_round=on_round)
+    assert res.admitted == res.finished == len(reqs)
+    assert seen["rounds"] == res.rounds > 5
+    assert seen["catch_ups"] > 0, "no round accepted every proposal"
+    assert res.draft_forward_calls == gamma * res.rounds + seen["catch_up_rounds"]
+    assert gpu.allocator.num_free == cap and gpu_d.allocator.num_free == cap
+    # device metrics == the mirror's counts at every record point
+    assert len(res.block_util_hist) == len(res.batch_hist) == len(seen["records"]) == res.steps
+    for u, (alloc, tok, _) in zip(res.block_util_hist, seen["records"]):
+        assert u == (tok / (alloc * bs) if alloc else 0.0)
+    assert res.kv_peak_blocks == max(r[0] for r in seen["records"])
+    assert res.draft_kv_peak_blocks == max(r[2] for r in seen["records"])
+
+
 def test_admission_reserves_lifetimes(cuda):
     """No round can exhaust the pool: every admitted request's whole lifetime fits."""
     L, Hq, Hkv, d, bs, V, gamma = 1, 2, 1, 16, 4, 16, 5

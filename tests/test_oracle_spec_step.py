@@ -53,12 +53,47 @@ def test_commit_round_eos_first_finishes_without_truncate():
     assert kv.block_tables[0] == []
 
 
-def test_draft_alignment_is_shrink_only():
+def test_draft_alignment_truncates_or_catches_up():
+    # prompt 5, generated [7]: start 5. Seq 0 commits 2 -> keep 7 < draft 9:
+    # truncate. Seq 1 commits 4 (all 3 drafts + bonus) -> keep 9 > draft 8
+    # (start + gamma): position 8 is decoded, token generated[8 - 5] = 3.
     kv = _pool(2, [9, 9])
-    draft = _pool(2, [9, 3])
+    draft = _pool(2, [9, 8])
     seqs = [SeqState(0, 5, 10, [7]), SeqState(1, 5, 10, [7])]
-    commit_round(seqs, {0: [1, 2], 1: [1, 2, 3, 4]}, kv, draft)
-    assert draft.seq_lengths == [7, 3]               # seq 1 shorter than keep: untouched
+    cu = []
+    commit_round(seqs, {0: [1, 2], 1: [1, 2, 3, 4]}, kv, draft, catchups=cu)
+    assert draft.seq_lengths == [7, 9]
+    assert [(c.sid, c.pos, c.tokens, c.finished) for c in cu] == [(1, 8, [3], False)]
+    # block size 4: position 8 opens block 2, popped from the free list tail,
+    # which is block 61, freed a moment earlier by seq 0's truncation (the
+    # draft pool handed out 63, 62, 61 to seq 0 and 60, 59 to seq 1)
+    assert draft.block_tables[0] == [63, 62] and draft.block_tables[1] == [60, 59, 61]
+
+
+def test_catch_up_pops_blocks_freed_earlier_in_the_round():
+    # Seq 0 commits all 4 tokens and reaches its budget of 5: its catch-up
+    # pops block 59 (draft blocks were 63, 62 | 61, 60), then its clear frees
+    # 63, 62, 59 in forward order; seq 1's catch-up then pops 59 again: the
+    # reference's per-sequence order, which the device align must replay.
+    kv = _pool(2, [9, 9])
+    draft = _pool(2, [8, 8])
+    seqs = [SeqState(0, 5, 5, [7]), SeqState(1, 5, 10, [7])]
+    cu = []
+    commit_round(seqs, {0: [1, 2, 3, 4], 1: [1, 2, 3, 4]}, kv, draft, catchups=cu)
+    assert seqs[0].finished and draft.block_tables[0] == []
+    assert draft.block_tables[1] == [61, 60, 59]
+    assert draft.allocator.free_list[-2:] == [63, 62]
+    assert [(c.sid, c.pos, c.tokens, c.finished) for c in cu] == [(0, 8, [3], True), (1, 8, [3], False)]
+
+
+def test_catch_up_of_several_positions():
+    kv = _pool(1, [12])
+    draft = _pool(1, [6])
+    seqs = [SeqState(0, 5, 20, [7])]
+    cu = []
+    commit_round(seqs, {0: [1, 2, 3, 4, 5]}, kv, draft, catchups=cu)
+    assert draft.seq_lengths == [10] and len(draft.block_tables[0]) == 3
+    assert [(c.pos, c.tokens) for c in cu] == [(6, [1, 2, 3, 4])]
 
 
 def test_keep_equals_start_plus_k_under_invariant():
