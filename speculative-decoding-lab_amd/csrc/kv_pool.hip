@@ -271,15 +271,19 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
   const int vec = (d * ES) >> 4;  // 16-byte pieces of one K row
   const int nk = C * vec, nv = C * d;
   // The chunk's new keys and values (round trip 1, independent of the state).
-  uint4 kreg[kWriteItems];
-  T vreg[kWriteItems];
-#pragma unroll
-  for (int k = 0; k < kWriteItems; ++k) {
+  // Item k of this thread: K piece / V element threadIdx.x + k * kFusedThreads
+  // (named registers: as an array they were kept in scratch memory).
+  static_assert(kWriteItems == 4, "four named items");
+  auto load_k = [&](int k) {
     const int ik = min((int)threadIdx.x + k * kFusedThreads, nk - 1);
-    kreg[k] = reinterpret_cast<const uint4*>(knew + (((size_t)b * C + ik / vec) * row_elems + (size_t)h * d) * ES)[ik % vec];
+    return reinterpret_cast<const uint4*>(knew + (((size_t)b * C + ik / vec) * row_elems + (size_t)h * d) * ES)[ik % vec];
+  };
+  auto load_v = [&](int k) {
     const int iv = min((int)threadIdx.x + k * kFusedThreads, nv - 1);
-    vreg[k] = reinterpret_cast<const T*>(vnew)[((size_t)b * C + iv / d) * row_elems + (size_t)h * d + iv % d];
-  }
+    return reinterpret_cast<const T*>(vnew)[((size_t)b * C + iv / d) * row_elems + (size_t)h * d + iv % d];
+  };
+  const uint4 k0 = load_k(0), k1 = load_k(1), k2 = load_k(2), k3 = load_k(3);
+  const T v0 = load_v(0), v1 = load_v(1), v2 = load_v(2), v3 = load_v(3);
   const int top = ctr[CTR_TOP];
   const int sid = seq_ids[b], s0 = start[b];
   const int e0 = min((int)threadIdx.x, B - 1);
@@ -348,36 +352,31 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
   const int n = (b > lim || s0 < 0) ? 0 : min(C, nb_new * bs - s0);
   if (n > 0) {
     if (h == 0 && threadIdx.x == 0 && seq_lens[sid] < s0 + n) seq_lens[sid] = s0 + n;
-    for (int base = 0; base < max(nk, nv); base += kWriteItems * kFusedThreads) {
-      if (base > 0) {
-#pragma unroll
-        for (int k = 0; k < kWriteItems; ++k) {
-          const int ik = min(base + (int)threadIdx.x + k * kFusedThreads, nk - 1);
-          kreg[k] = reinterpret_cast<const uint4*>(knew + (((size_t)b * C + ik / vec) * row_elems + (size_t)h * d) * ES)[ik % vec];
-          const int iv = min(base + (int)threadIdx.x + k * kFusedThreads, nv - 1);
-          vreg[k] = reinterpret_cast<const T*>(vnew)[((size_t)b * C + iv / d) * row_elems + (size_t)h * d + iv % d];
+    // One pass (the host launches this kernel only when the chunk's K pieces
+    // and V elements fit kWriteItems per thread), fully unrolled so that the
+    // loaded rows stay in registers.
+    auto store = [&](int k, const uint4& kv, T vv) {
+      const int ik = (int)threadIdx.x + k * kFusedThreads;
+      if (ik < nk && ik / vec < n) {
+        const int p = s0 + ik / vec, phys = s_phys[p / bs - blk0];
+        if ((unsigned)phys < (unsigned)cap) {
+          uint8_t* kdst = kpool + ((((size_t)layer * cap + phys) * hkv + h) * bs + p % bs) * (size_t)(d * ES);
+          reinterpret_cast<uint4*>(kdst)[ik % vec] = kv;
         }
       }
-#pragma unroll
-      for (int k = 0; k < kWriteItems; ++k) {
-        const int ik = base + (int)threadIdx.x + k * kFusedThreads;
-        if (ik < nk && ik / vec < n) {
-          const int p = s0 + ik / vec, phys = s_phys[p / bs - blk0];
-          if ((unsigned)phys < (unsigned)cap) {
-            uint8_t* kdst = kpool + ((((size_t)layer * cap + phys) * hkv + h) * bs + p % bs) * (size_t)(d * ES);
-            reinterpret_cast<uint4*>(kdst)[ik % vec] = kreg[k];
-          }
-        }
-        const int iv = base + (int)threadIdx.x + k * kFusedThreads;
-        if (iv < nv && iv / d < n) {
-          const int p = s0 + iv / d, phys = s_phys[p / bs - blk0];
-          if ((unsigned)phys < (unsigned)cap) {
-            T* vdst = reinterpret_cast<T*>(vpool) + (((size_t)layer * cap + phys) * hkv + h) * (size_t)d * bs;
-            vdst[(size_t)(iv % d) * bs + p % bs] = vreg[k];
-          }
+      const int iv = (int)threadIdx.x + k * kFusedThreads;
+      if (iv < nv && iv / d < n) {
+        const int p = s0 + iv / d, phys = s_phys[p / bs - blk0];
+        if ((unsigned)phys < (unsigned)cap) {
+          T* vdst = reinterpret_cast<T*>(vpool) + (((size_t)layer * cap + phys) * hkv + h) * (size_t)d * bs;
+          vdst[(size_t)(iv % d) * bs + p % bs] = vv;
         }
       }
-    }
+    };
+    store(0, k0, v0);
+    store(1, k1, v1);
+    store(2, k2, v2);
+    store(3, k3, v3);
   }
   // The last workgroup to arrive publishes the counts and the stack height.
   if (threadIdx.x == 0) s_flag = arrived + 1 == (int)gridDim.x;
@@ -575,6 +574,35 @@ __device__ __forceinline__ int rewind_block(const RewindEntry& e, int k, const i
 // already free or listed twice sends the call to the exact sequential replay.
 constexpr int kRewindItems = 8192;
 constexpr int kRewindRounds = kRewindItems / kPoolThreads;
+// Tail blocks per entry loaded with the block counts (the short-truncation path).
+constexpr int kSpecTail = 4;
+
+// The exact sequential replay (one thread) with the reference's rule
+// `if block in free_list: return` (kv.py:73-74), from stack height `top`.
+__device__ void rewind_replay(const int32_t* __restrict__ tables, int maxb, int32_t* __restrict__ nblocks,
+                              int32_t* __restrict__ seq_lens, int32_t* __restrict__ free_stack,
+                              int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
+                              const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ new_len,
+                              const int32_t* __restrict__ finished, int n, int bs, int shrink_only, int cap, int top) {
+  int t = top, pushed = 0;
+  for (int q = 0; q < n; ++q) {
+    // Entries see the effects of earlier ones (distinct sids, so only the flags matter).
+    const RewindEntry eq = rewind_entry(q, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+    for (int k = 0; k < eq.ft + eq.fc; ++k) {
+      const int id = rewind_block(eq, k, tables, maxb);
+      if ((unsigned)id < (unsigned)cap && t < cap && atomicOr(&free_flag[id], 0) == 0) {
+        free_stack[t++] = id;
+        atomicExch(&free_flag[id], 1);
+        ++pushed;
+      }
+    }
+    nblocks[eq.sid] = eq.nb_final;
+    seq_lens[eq.sid] = eq.len_final;
+  }
+  ctr[CTR_TOP] = t;
+  ctr[CTR_PUSHED] = pushed;
+  ctr[CTR_SLOWPATH] += 1;
+}
 
 __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
     const int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
@@ -588,10 +616,62 @@ __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
   if (n <= (int)blockDim.x) {
     const int i = threadIdx.x;
     const int top = ctr[CTR_TOP];
-    RewindEntry e = rewind_entry(min(i, n - 1), seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
+    // The table entries from the new length's first dropped block on, loaded
+    // with the block counts: when every entry only truncates (no clear) at
+    // most kSpecTail blocks -- a spec round's rewind -- they are the blocks to
+    // free and the call saves the round trip of the table loads.
+    const int ii = min(i, n - 1);
+    const int nl_i = new_len ? new_len[ii] : -1;
+    const int kb = nl_i <= 0 ? 0 : (nl_i + bs - 1) / bs;
+    const int32_t* trow = tables + (size_t)seq_ids[ii] * maxb;
+    int spec[kSpecTail];
+#pragma unroll
+    for (int j = 0; j < kSpecTail; ++j) spec[j] = trow[min(kb + j, maxb - 1)];
+    RewindEntry e = rewind_entry(ii, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
     const int cnt = i < n ? e.ft + e.fc : 0;
     int total;
     const int off = block_exclusive_scan(cnt, s_scan, &total);
+    if (__syncthreads_and(i >= n || (e.fc == 0 && e.ft <= kSpecTail))) {
+      // Entry i frees table[nb - 1 - k] = spec[ft - 1 - k] to top + off + k.
+      bool mydup = false;
+      int old[kSpecTail];
+#pragma unroll
+      for (int j = 0; j < kSpecTail; ++j) {
+        old[j] = 0;
+        if (j < cnt) {
+          if ((unsigned)spec[j] >= (unsigned)cap) mydup = true;
+          else old[j] = atomicAdd(&free_flag[spec[j]], 2);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kSpecTail; ++j) mydup |= old[j] != 0;
+      if (!__syncthreads_or(mydup)) {
+#pragma unroll
+        for (int j = 0; j < kSpecTail; ++j) {
+          if (j < cnt) {
+            free_stack[top + off + (cnt - 1 - j)] = spec[j];
+            free_flag[spec[j]] = 1;
+          }
+        }
+        if (i < n) {
+          nblocks[e.sid] = e.nb_final;
+          seq_lens[e.sid] = e.len_final;
+        }
+        if (i == 0) {
+          ctr[CTR_TOP] = top + total;
+          ctr[CTR_PUSHED] = total;
+        }
+        return;
+      }
+#pragma unroll
+      for (int j = 0; j < kSpecTail; ++j)
+        if (j < cnt && (unsigned)spec[j] < (unsigned)cap) atomicSub(&free_flag[spec[j]], 2);
+      __syncthreads();
+      if (i == 0)
+        rewind_replay(tables, maxb, nblocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len, finished, n,
+                      bs, shrink_only, cap, top);
+      return;
+    }
     if (total <= kRewindItems) {
       if (i < n) {
         s_off[i] = off;
@@ -648,24 +728,9 @@ __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
       for (int j = 0; j < kRewindRounds; ++j)
         if (i + j * (int)blockDim.x < total && (unsigned)ids[j] < (unsigned)cap) atomicSub(&free_flag[ids[j]], 2);
       __syncthreads();
-      if (i != 0) return;
-      int t = top, pushed = 0;
-      for (int q = 0; q < n; ++q) {
-        const RewindEntry eq = rewind_entry(q, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
-        for (int k = 0; k < eq.ft + eq.fc; ++k) {
-          const int id = rewind_block(eq, k, tables, maxb);
-          if ((unsigned)id < (unsigned)cap && t < cap && atomicOr(&free_flag[id], 0) == 0) {
-            free_stack[t++] = id;
-            atomicExch(&free_flag[id], 1);
-            ++pushed;
-          }
-        }
-        nblocks[eq.sid] = eq.nb_final;
-        seq_lens[eq.sid] = eq.len_final;
-      }
-      ctr[CTR_TOP] = t;
-      ctr[CTR_PUSHED] = pushed;
-      ctr[CTR_SLOWPATH] += 1;
+      if (i == 0)
+        rewind_replay(tables, maxb, nblocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len, finished, n,
+                      bs, shrink_only, cap, top);
       return;
     }
     __syncthreads();
@@ -742,25 +807,9 @@ __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
     }
   }
   __syncthreads();
-  if (threadIdx.x != 0) return;
-  int t = top, pushed = 0;
-  for (int i = 0; i < n; ++i) {
-    // Entries see the effects of earlier ones (distinct sids, so only the flags matter).
-    const RewindEntry e = rewind_entry(i, seq_ids, new_len, finished, nblocks, seq_lens, bs, shrink_only);
-    for (int k = 0; k < e.ft + e.fc; ++k) {
-      const int id = rewind_block(e, k, tables, maxb);
-      if ((unsigned)id < (unsigned)cap && t < cap && atomicOr(&free_flag[id], 0) == 0) {
-        free_stack[t++] = id;
-        atomicExch(&free_flag[id], 1);
-        ++pushed;
-      }
-    }
-    nblocks[e.sid] = e.nb_final;
-    seq_lens[e.sid] = e.len_final;
-  }
-  ctr[CTR_TOP] = t;
-  ctr[CTR_PUSHED] = pushed;
-  ctr[CTR_SLOWPATH] += 1;
+  if (threadIdx.x == 0)
+    rewind_replay(tables, maxb, nblocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len, finished, n, bs,
+                  shrink_only, cap, top);
 }
 
 // ------------------------------------------------------------------ draft alignment
@@ -1184,7 +1233,8 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
   hipStream_t s = (hipStream_t)stream;
   const bool vec16 = (head_dim * es) % 16 == 0;
   if (may_alloc && !alloc_only && vec16 && B <= kFusedMaxB &&
-      (C + block_size - 1) / block_size + 1 <= kFusedMaxBlocks) {
+      (C + block_size - 1) / block_size + 1 <= kFusedMaxBlocks &&
+      C * head_dim <= kWriteItems * kFusedThreads && C * (head_dim * es / 16) <= kWriteItems * kFusedThreads) {
     if (!free_stack || !free_flag || !ctr) return SPV_ERR_ARG;
     auto* kp = static_cast<uint8_t*>(k_pool);
     auto* vp = static_cast<uint8_t*>(v_pool);

@@ -297,6 +297,35 @@ def test_already_free_block_takes_exact_slow_path(cuda):
     assert int(gpu.allocator.ctr[2].item()) == 1  # one call took the sequential path
 
 
+def test_already_free_block_in_a_short_truncation_takes_exact_slow_path(cuda):
+    # truncations only, a few blocks each: the path that frees the tail blocks
+    # loaded with the block counts must detect the already-free one too
+    gpu = PagedKVCache(1, 1, 2, 12, 2, cuda, torch.float32)
+    cpu = ref.PagedKVCache(1, 1, 2, 12, 2, store=False)
+    for kv in (gpu, cpu):
+        kv.add_sequence(0)
+        kv.add_sequence(1)
+    k = torch.zeros(2, 6, 1, 2, device=cuda)
+    gpu.write_block(0, [0, 1], [0, 0], k, k)
+    cpu.write_block(0, [0, 1], [0, 0], None, None, chunk=6)
+    victim = cpu.block_tables[0][2]
+    gpu.allocator.free(victim)
+    cpu.allocator.free(victim)
+    gpu.rewind([0, 1], [1, 3], [0, 0])
+    cpu.truncate(0, 1)
+    cpu.truncate(1, 3)
+    gpu._sync_pushes()
+    _same_state(gpu, cpu)
+    assert int(gpu.allocator.ctr[2].item()) == 1
+    # and without the victim the same rewind takes the fast path
+    gpu.rewind([0, 1], [0, 1], [0, 0])
+    cpu.truncate(0, 0)
+    cpu.truncate(1, 1)
+    gpu._sync_pushes()
+    _same_state(gpu, cpu)
+    assert int(gpu.allocator.ctr[2].item()) == 1
+
+
 def _qwen15_pool(seed=0, B=32, cap=65536, bs=16, C=6):
     """Random-permutation tables over a 64k-block pool, lengths U[256, 4096]."""
     g = torch.Generator().manual_seed(seed)
