@@ -7,10 +7,13 @@ tables are a random permutation of a 65,536-block pool; the rest of the pool is
 the free list. One step =
 
   1. append the 6 verify tokens of every sequence (device allocation + copy),
-  2. verify attention of the 6 rows x 12 heads over the paged context,
-  3. fused rejection sampling of the round over a 151,936-entry vocabulary
+  2. the round's attention plan (``VerifyPlan``: the split of the batch over
+     the workgroups and their first block ids, made once per round and shared
+     by the round's layers),
+  3. verify attention of the 6 rows x 12 heads over the paged context,
+  4. fused rejection sampling of the round over a 151,936-entry vocabulary
      (target logits N(0, 2^2), draft = target + N(0, 1), T = 1, caller noise),
-  4. rewind of the pool to start + n_commit with the sampled lengths.
+  5. rewind of the pool to start + n_commit with the sampled lengths.
 
 All inputs are resident in HBM before timing. The batch exists in 8 replicas on
 disjoint random pages of the pool, each with its own draw of the context
@@ -23,8 +26,10 @@ The timed region is exactly ``--steps`` steps, launched back to back on the
 current stream behind a bounded device-side delay (so the host has queued
 them all before the GPU reaches the first), with HIP events around the whole
 region and around every attention call. The headline ``value`` is the
-verify-attention HBM bandwidth: algorithmic bytes of the timed calls / their
-summed event-measured durations. ``spec_step_us_per_seq`` is the whole step
+verify-attention HBM bandwidth: algorithmic bytes of the timed calls / (their
+summed kernel durations + each call's share of its round's plan, the plan's
+time over the 28 layers of Qwen2.5-1.5B that share it); ``roofline`` rates
+the attention kernel alone. ``spec_step_us_per_seq`` is the whole step
 per sequence over the same region; ``graph_ms_per_step`` is the same step as a
 captured graph replay (outside the timed region). ``cpu_baseline`` times the
 CPU oracle's whole step (per-token write loop, gather + repeat_interleave +
@@ -60,6 +65,8 @@ C = GAMMA + 1
 # finds its data in the 256 MB last-level cache left by the previous one:
 # every call reads HBM, as one layer of a deep model does.
 REPLICAS, LOGIT_SETS = 8, 2
+# Layers of Qwen2.5-1.5B: the attention calls of one verify round that share its plan.
+LAYERS_PER_ROUND = 28
 
 
 def attention_bytes(lens, chunk=C, hq=HQ, hkv=HKV, d=D, bs=BS):
@@ -191,19 +198,24 @@ def build_workload(dev, seed=0):
 def make_step(w):
     """Closures of one verify step for replica r / logits set t: append the
     verify tokens, attention, fused sampling, rewind."""
-    from engine.attention import verify_attention
+    from engine.attention import VerifyPlan, verify_attention
     from engine.spec_scheduler import _new_result, verify_sample
 
     kv = w["kv"]
     # one result per replica: a rewind applies the lengths sampled against its
     # own replica's start positions
     results = [_new_result(B, GAMMA, kv.device) for _ in range(REPLICAS)]
+    plans = [VerifyPlan(kv, w["sids"][r], w["start"][r], C, HQ, w["max_ctx"][r]) for r in range(REPLICAS)]
 
     def append(r):
         kv.write_block_device(0, w["sids"][r], w["start"][r], w["k_new"], w["v_new"])
 
+    def plan(r):  # once the round's blocks exist (after its first append); into the replica's buffer
+        plans[r] = VerifyPlan(kv, w["sids"][r], w["start"][r], C, HQ, w["max_ctx"][r], buf=plans[r].buf)
+
     def attend(r):
-        verify_attention(w["q"], kv, 0, w["sids"][r], w["start"][r], w["max_ctx"][r], out=w["attn_out"])
+        verify_attention(w["q"], kv, 0, w["sids"][r], w["start"][r], w["max_ctx"][r], out=w["attn_out"],
+                         plan=plans[r])
 
     def sample(t, r=0):
         target, draft, proposals = w["logits"][t]
@@ -216,13 +228,15 @@ def make_step(w):
     def step(i, events=None):
         r, t = i % REPLICAS, i % LOGIT_SETS
         append(r)
+        plan(r)
         if events is not None:
             events.arm()
         attend(r)
         sample(t, r)
         rewind(r)
 
-    return step, {"append": append, "attend": attend, "sample": sample, "rewind": rewind}, results[0]
+    return step, {"append": append, "plan": plan, "attend": attend, "sample": sample, "rewind": rewind}, \
+        results[0]
 
 
 def graph_of(fn, reps, torch):
@@ -534,7 +548,7 @@ def long_context(dev, seed=0):
     calls cycle over, so no call finds its pages in the last-level cache."""
     import torch
 
-    from engine.attention import verify_attention
+    from engine.attention import VerifyPlan, verify_attention
     from engine.kv import PagedKVCache
 
     chunk = LC_GAMMA + 1
@@ -564,7 +578,9 @@ def long_context(dev, seed=0):
         for layer in range(LC_REPLICAS):  # the verify chunk, written before it is attended
             kv.write_block(layer, list(range(LC_B)), lens, kn, vn)
         o = torch.empty_like(q)
-        attend = lambda i: verify_attention(q, kv, i % LC_REPLICAS, sid, st, LC_CTX + chunk, out=o)
+        # every layer of the round reads the same tables: one plan serves all calls
+        pl = VerifyPlan(kv, sid, st, chunk, LC_HQ, LC_CTX + chunk)
+        attend = lambda i: verify_attention(q, kv, i % LC_REPLICAS, sid, st, LC_CTX + chunk, out=o, plan=pl)
         for i in range(LC_REPLICAS):
             attend(i)
         torch.cuda.synchronize()
@@ -594,7 +610,7 @@ def draft_decode(dev, seed=0):
     replicas on disjoint pages."""
     import torch
 
-    from engine.attention import verify_attention
+    from engine.attention import VerifyPlan, verify_attention
     from engine.kv import PagedKVCache
 
     hq, hkv, d, reps = 14, 2, 64, 8
@@ -623,7 +639,9 @@ def draft_decode(dev, seed=0):
     max_ctx = max(lens) + 1
     for r in range(reps):  # the new token's blocks exist from here on
         kv.write_block_device(0, sids[r], st, kn, vn)
-    attend = lambda i: verify_attention(q, kv, 0, sids[i % reps], st, max_ctx, out=out)
+    # one plan per replica (a draft step's layers share their step's plan)
+    plans = [VerifyPlan(kv, sids[r], st, 1, hq, max_ctx) for r in range(reps)]
+    attend = lambda i: verify_attention(q, kv, 0, sids[i % reps], st, max_ctx, out=out, plan=plans[i % reps])
     append = lambda i: kv.write_block_device(0, sids[i % reps], st, kn, vn, alloc=False)
     n = 3 * reps
     for i in range(reps):
@@ -652,15 +670,17 @@ def draft_decode(dev, seed=0):
         for layer in range(depth):
             r = (i * depth + layer) % reps
             kv.write_block_device(0, sids[r], st, kn, vn, alloc=False)
-            verify_attention(q, kv, 0, sids[r], st, max_ctx, out=out)
+            if layer == 0:  # the step's plan, made once its blocks exist
+                plans[r] = VerifyPlan(kv, sids[r], st, 1, hq, max_ctx, buf=plans[r].buf)
+            verify_attention(q, kv, 0, sids[r], st, max_ctx, out=out, plan=plans[r])
         samp(i)
 
     gstep = graph_of(lambda: [draft_step(i) for i in range(2)], 1, torch)
     step_us = time_graph(gstep, 5, torch) * 1000.0 / 2
     res = {"workload": "Qwen2.5-0.5B-shaped draft decode: batch 32, one query row, 14q/2kv heads, head_dim 64, "
                        "block 16, bf16 KV, the verify workload's contexts (U[256,4096], seed 0); 8 replicas; "
-                       "draft sampling of 32 rows over V=151936 at T=1; a draft step = 24 layers of append + "
-                       "decode attention, then the sampling, as one captured graph",
+                       "draft sampling of 32 rows over V=151936 at T=1; a draft step = the step's attention plan, 24 layers "
+                       "of append + decode attention, then the sampling, as one captured graph",
            "attn_us": round(attn_us, 2), "attn_gbs": round(nbytes / (attn_us * 1e-6) / 1e9, 1),
            "attn_bytes_per_call": nbytes, "append_us": round(app_us, 2),
            "sample_us": round(samp_us, 2),
@@ -755,7 +775,7 @@ def main() -> int:
     rl = w["rlens"]
     attn_bytes_timed = sum(attention_bytes(rl[i % REPLICAS]) for i in range(args.steps))
     attn_us = 1000.0 * sum(attn_ms) / len(attn_ms)
-    attn_gbs = attn_bytes_timed / (sum(attn_ms) * 1e-3) / 1e9
+    kernel_gbs = attn_bytes_timed / (sum(attn_ms) * 1e-3) / 1e9
 
     # Outside the timed region: the step as a captured graph (one replay runs
     # REPLICAS steps), and per-part graphs of back-to-back calls cycling over
@@ -768,6 +788,9 @@ def main() -> int:
     part_us = {}
     g_att = graph_of(lambda: [parts["attend"](i % REPLICAS) for i in range(reps)], 1, torch)
     part_us["attend"] = time_graph(g_att, 5, torch) * 1000.0 / reps
+    g_plan = graph_of(lambda: [parts["plan"](i % REPLICAS) for i in range(reps)], 1, torch)
+    part_us["plan"] = time_graph(g_plan, 5, torch) * 1000.0 / reps
+    del g_plan
     g_smp = graph_of(lambda: [parts["sample"](i % LOGIT_SETS, i % REPLICAS) for i in range(reps)], 1, torch)
     part_us["sample"] = time_graph(g_smp, 5, torch) * 1000.0 / reps
     g_ar = graph_of(lambda: [(parts["append"](i % REPLICAS), parts["rewind"](i % REPLICAS)) for i in range(reps)],
@@ -788,6 +811,9 @@ def main() -> int:
     torch.cuda.synchronize()
     print("bench: timings done", file=sys.stderr, flush=True)
 
+    # each call's share of its round's plan (LAYERS_PER_ROUND calls share one)
+    plan_share_us = part_us["plan"] / LAYERS_PER_ROUND
+    attn_gbs = attn_bytes_timed / ((sum(attn_ms) + args.steps * plan_share_us * 1e-3) * 1e-3) / 1e9
     copy_gbs = copy_bandwidth(dev)
     lens = w["lens"]
     all_lens = [L for r in rl for L in r]
@@ -820,6 +846,10 @@ def main() -> int:
         "pct_of_peak": round(100.0 * attn_gbs / HBM_PEAK_GBS, 2),
         "copy_gbs": round(copy_gbs, 1),
         "attn_us": round(attn_us, 2),
+        "plan_us": round(part_us["plan"], 2),
+        "layers_per_round": LAYERS_PER_ROUND,
+        "attn_us_with_plan_share": round(attn_us + plan_share_us, 2),
+        "attn_kernel_gbs": round(kernel_gbs, 1),
         "attn_bytes_per_call": round(attn_bytes_timed / args.steps),
         "spec_step_us_per_seq": round(ms_per_step * 1000.0 / B, 3),
         "graph_ms_per_step": round(graph_ms_per_step, 4),
@@ -830,10 +860,10 @@ def main() -> int:
         "mean_accepted_drafts": round(accept, 3),
         "roofline": {
             "bound": "hbm",
-            "achieved": round(attn_gbs, 1),
+            "achieved": round(kernel_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
         },
         "cpu_baseline": None,

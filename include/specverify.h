@@ -246,6 +246,41 @@ int spv_verify_attn(void* out, const void* q, int q_dtype,
                     int32_t max_ctx, float scale, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* The plan of a round's paged_attention_extend calls. The reference calls it
+ * once per layer with the same seq_ids / start_positions
+ * (engine/model.py:182-190 under spec_scheduler.py:255-259); what those calls
+ * share -- the split of the batch over the persistent grid and the block id
+ * of each workgroup's first pages -- is computed here once, after the round's
+ * blocks are allocated, into `plan` (spv_verify_attn_plan_bytes(B) bytes,
+ * caller-owned). The sequence-length check of spv_verify_attn (ctr[7]) is made
+ * here, once. Shapes off the MFMA path need no plan: the call then does
+ * nothing. */
+size_t spv_verify_attn_plan_bytes(int32_t B);
+int spv_verify_attn_plan(const int32_t* block_tables, int32_t max_blocks_per_seq,
+                         const int32_t* seq_ids, const int32_t* start_pos,
+                         const int32_t* seq_lens, int32_t* ctr, int32_t B,
+                         int32_t C, int32_t num_q_heads, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t block_size, int32_t kv_dtype,
+                         int32_t capacity, int32_t max_ctx, void* plan,
+                         size_t plan_bytes, void* stream);
+
+/* spv_verify_attn reading a plan made by spv_verify_attn_plan with the same
+ * block_tables contents, seq_ids, start_pos, B, C, heads, head_dim,
+ * block_size, kv_dtype, capacity and max_ctx (any layer): the MFMA path skips
+ * its prologue and starts the page walk one round trip after launch. Same
+ * results as spv_verify_attn; other shapes run spv_verify_attn. */
+int spv_verify_attn_planned(void* out, const void* q, int q_dtype,
+                            const void* k_pool, const void* v_pool, int kv_dtype,
+                            const float* kv_scales, const int32_t* block_tables,
+                            int32_t max_blocks_per_seq, const int32_t* seq_ids,
+                            const int32_t* start_pos, const int32_t* seq_lens,
+                            int32_t* ctr, int32_t B, int32_t C,
+                            int32_t num_q_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t block_size, int32_t layer,
+                            int32_t capacity, int32_t max_ctx, float scale,
+                            const void* plan, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* spv_verify_attn with no allocation and no caller workspace. No counterpart
  * in the reference: it serves callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid

@@ -198,7 +198,7 @@ int verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_pool, 
                      const int32_t* seq_ids, const int32_t* start_pos, const int32_t* seq_lens, int32_t* ctr,
                      int32_t B, int32_t C, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int32_t layer, int32_t capacity, int32_t max_ctx, float scale,
-                     void* workspace, size_t workspace_bytes, bool exact_layout, void* stream);
+                     const void* plan, void* workspace, size_t workspace_bytes, bool exact_layout, void* stream);
 
 }  // namespace spv
 

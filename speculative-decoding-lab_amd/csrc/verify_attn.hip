@@ -64,6 +64,7 @@ struct AttnParams {
   int pages_per_split, max_splits, nrg, rows_per_group;
   int max_pages;     // ceil(max_ctx / block_size): no table entry beyond it is read
   float scale_log2;  // softmax scale * log2(e)
+  int* plan;         // MFMA path: the round's plan (written by attn_plan_kernel, read by planned calls)
 };
 
 // Pages of sequence b's context, never more than the caller-declared bound.
@@ -431,6 +432,107 @@ __device__ __forceinline__ int share_of_block(int bid, int nw) {
   return (nw & 7) ? bid : (bid & 7) * (nw >> 3) + (bid >> 3);
 }
 
+// The units of a share: [x_begin, x_stop) of the batch's pieces (equal
+// pieces) or of its cost units (cost-balanced mode, where T is the units of
+// all segments and unit g belongs to workgroup floor((g + 1) nw - 1) / T).
+struct ShareRange {
+  long long x_begin, x_stop, T;
+};
+
+template <bool BAL>
+__device__ __forceinline__ ShareRange share_range(const int* s_pref, const int* s_kpref, int B, long long HR, int kpc,
+                                                  int nw, int wg) {
+  ShareRange r;
+  r.T = HR * s_pref[B];
+  auto page_start = [&](long long w) { return div_floor(w * r.T, nw); };
+  const long long N = BAL ? 0 : HR * s_kpref[B];  // pieces in the batch
+  r.x_begin = BAL ? page_start(wg) : div_floor((long long)wg * N, nw);
+  const long long x_end = BAL ? page_start(wg + 1) : div_floor((long long)(wg + 1) * N, nw);
+  // A range that ends among a segment's overhead units (no page of it) stops
+  // at that segment, so every piece of the loop holds pages.
+  r.x_stop = x_end;
+  if constexpr (BAL) {
+    if (x_end > r.x_begin) {
+      const long long xl = x_end - 1;
+      const int bl = uni(seq_of(s_pref, B, HR, xl));
+      const int npwl = uni(s_pref[bl + 1] - s_pref[bl]);
+      const long long locl = xl - HR * s_pref[bl];
+      const long long Gl = HR * s_pref[bl] + (locl / npwl) * npwl;
+      if (xl - Gl < kpc) r.x_stop = max(r.x_begin, Gl);
+    }
+  }
+  return r;
+}
+
+// The piece of a share that starts at unit x: pages [lp0, lp1) of segment
+// (b, hr), its partial slot, the arrivals its segment counts (narr), what
+// the merge needs to find the segment's slots (x0: the segment's first piece;
+// w_a, Gs: the workgroup holding its page 0 and its first unit), and the unit
+// after it.
+struct Piece {
+  int b, hr, lp0, lp1, slot, narr, x0, w_a;
+  long long Gs, x_next;
+};
+
+template <bool BAL>
+__device__ __forceinline__ Piece decode_piece(long long x, long long x_stop, const int* s_pref, const int* s_kpref,
+                                              int B, long long HR, int kpc, long long T, int nw, int wg) {
+  Piece q{};
+  if constexpr (BAL) {
+    auto page_start = [&](long long w) { return div_floor(w * T, nw); };
+    auto owner = [&](long long g) { return (int)div_floor((g + 1) * nw - 1, T); };
+    q.b = uni(seq_of(s_pref, B, HR, x));
+    const int npw = uni(s_pref[q.b + 1] - s_pref[q.b]);  // units of a segment: kpc + pages
+    const int np = npw - kpc;
+    const int local = (int)(x - HR * s_pref[q.b]);
+    q.hr = local / npw;
+    q.Gs = HR * s_pref[q.b] + (long long)q.hr * npw;  // the segment's first unit
+    const long long cend = min(q.Gs + npw, x_stop);
+    q.lp0 = max(0, (int)(x - q.Gs) - kpc);
+    q.lp1 = (int)(cend - q.Gs) - kpc;
+    q.w_a = owner(q.Gs + kpc);  // the workgroup holding page 0
+    q.narr = owner(q.Gs + kpc + np - 1) - q.w_a + 1;
+    q.slot = 2 * wg + (page_start(wg) >= q.Gs ? 0 : 1);
+    q.x_next = cend;
+  } else {
+    q.b = uni(seq_of(s_kpref, B, HR, x));
+    const int kb = uni(s_kpref[q.b + 1] - s_kpref[q.b]);  // pieces per segment of sequence b
+    const int rem = (int)(x - HR * s_kpref[q.b]);
+    q.hr = rem / kb;
+    const int piece = rem - q.hr * kb;
+    const int np = uni(s_pref[q.b + 1] - s_pref[q.b]);
+    q.lp0 = (int)div_floor((long long)piece * np, kb);
+    q.lp1 = (int)div_floor((long long)(piece + 1) * np, kb);
+    q.x0 = (int)(x - piece);  // the segment's first piece
+    q.narr = kb;
+    q.slot = (int)x;
+    q.x_next = x + 1;
+  }
+  return q;
+}
+
+// The plan of a round (attn_plan_kernel), in ints: a header, the batch's
+// prefix arrays (as build_plan leaves them in LDS), then one head per share:
+// its range, its first piece and the block ids of the first page of each
+// wave in the piece's first window.
+constexpr int kPlanHeader = 16;  // [0] B, [1] nw, [2] kpc, [3] valid, [4..5] T, [6..7] HR
+constexpr int kHeadInts = 32;
+enum : int {
+  H_XB = 0, H_XS = 2, H_XN = 4, H_GS = 6,  // x_begin, x_stop, x_next, Gs (two ints each)
+  H_B = 8, H_HR, H_LP0, H_LP1, H_SLOT, H_NARR, H_X0, H_WA, H_START, H_SID,
+  H_IDS = 24  // eight block ids
+};
+__host__ __device__ constexpr int plan_heads_at(int B) { return (kPlanHeader + 4 * (B + 1) + 31) & ~31; }
+__host__ __device__ constexpr size_t plan_ints(int B, int nw) { return (size_t)plan_heads_at(B) + (size_t)nw * kHeadInts; }
+
+__device__ __forceinline__ long long ld64(const int* a) {
+  return (long long)(((unsigned long long)(unsigned)a[1] << 32) | (unsigned)a[0]);
+}
+__device__ __forceinline__ void st64(int* a, long long v) {
+  a[0] = (int)(unsigned)(unsigned long long)v;
+  a[1] = (int)(unsigned)((unsigned long long)v >> 32);
+}
+
 // One page as a wave holds it: the K rows for S^T and the V^T tiles for O^T
 // (bf16, or fp8 e4m3 codes with the block's two scales).
 template <int D, int KT>
@@ -556,7 +658,10 @@ __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b
 // distinct banks.
 __device__ __forceinline__ int xswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-template <int NT, int D, int QT, bool BAL, int KT>
+// PL: the call reads the round's plan (attn_plan_kernel) instead of making
+// it: its first piece and the block ids of each wave's first page come in one
+// load, so the page walk starts one round trip after launch.
+template <int NT, int D, int QT, bool BAL, int KT, bool PL>
 __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p) {
   constexpr bool kFp8 = KT == SPV_FP8E4M3;
   constexpr int KS = D / 32;  // 32-dim k-steps of S^T
@@ -589,8 +694,6 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   int* s_start = s_sid + p.B + 1;
   const long long HR = (long long)p.Hkv * p.nrg;
   constexpr int KPC = BAL ? piece_cost(D, KT) : 0;
-  build_plan<BS, BAL>(p, s_pref, s_kpref, s_sid, s_start, HR, nw, KPC);
-  if (s_pref[p.B] == 0) return;
   // Cost-balanced mode (segments >= workgroups): every segment costs KPC
   // units (its piece overhead) followed by one unit per page; the segments
   // are laid end to end (sequence-major, then (kv head, row group)) and
@@ -600,26 +703,49 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   // starts at or after the segment's first unit: its first piece) or 2 wg + 1
   // (its last piece) for each workgroup w_a .. w_b that holds pages of it.
   // Otherwise: equal pieces, one slot each.
-  constexpr bool balanced = BAL;  // chosen by the host: HR * B >= nw
-  long long T = HR * s_pref[p.B];  // units of all segments
-  auto page_start = [&](long long w) { return div_floor(w * T, nw); };
-  auto owner = [&](long long g) { return (int)div_floor((g + 1) * nw - 1, T); };  // workgroup holding unit g
-  const long long N = balanced ? 0 : HR * s_kpref[p.B];  // pieces in the batch
-  const long long x_begin = balanced ? page_start(wg) : div_floor((long long)wg * N, nw);
-  const long long x_end = balanced ? page_start(wg + 1) : div_floor((long long)(wg + 1) * N, nw);
-  // A range that ends among a segment's overhead units (no page of it) stops
-  // at that segment, so every piece of the loop holds pages.
-  long long x_stop = x_end;
-  if constexpr (BAL) {
-    if (x_end > x_begin) {
-      const long long xl = x_end - 1;
-      const int bl = uni(seq_of(s_pref, p.B, HR, xl));
-      const int npwl = uni(s_pref[bl + 1] - s_pref[bl]);
-      const long long locl = xl - HR * s_pref[bl];
-      const long long Gl = HR * s_pref[bl] + (locl / npwl) * npwl;
-      if (xl - Gl < KPC) x_stop = max(x_begin, Gl);
-    }
+  long long x_begin, x_stop, T;
+  // The piece being walked and its sequence's start and id. A planned call
+  // takes the first from the plan's head of this share; the pieces after it
+  // are decoded from the prefix arrays, as an unplanned call decodes all.
+  Piece pc{};
+  int start = 0, sid = 0, first_id = 0;
+  if constexpr (PL) {
+    // Lane k of every wave loads word k of the head; the words are read out
+    // as wave-uniform values. The prefix arrays go to LDS for the pieces
+    // after the first (the first barrier publishes them).
+    const int* head = p.plan + plan_heads_at(p.B) + (size_t)wg * kHeadInts;
+    const int hv = head[lane & (kHeadInts - 1)];
+    auto word = [&](int k) { return __builtin_amdgcn_readlane(hv, k); };
+    auto word64 = [&](int k) {
+      return (long long)(((unsigned long long)(unsigned)word(k + 1) << 32) | (unsigned)word(k));
+    };
+    for (int t = threadIdx.x; t < 4 * (p.B + 1); t += kMfmaThreads) s_pref[t] = p.plan[kPlanHeader + t];
+    x_begin = word64(H_XB);
+    x_stop = word64(H_XS);
+    T = ld64(p.plan + 4);
+    if (x_begin >= x_stop) return;
+    pc.b = word(H_B);
+    pc.hr = word(H_HR);
+    pc.lp0 = word(H_LP0);
+    pc.lp1 = word(H_LP1);
+    pc.slot = word(H_SLOT);
+    pc.narr = word(H_NARR);
+    pc.x0 = word(H_X0);
+    pc.w_a = word(H_WA);
+    pc.Gs = word64(H_GS);
+    pc.x_next = word64(H_XN);
+    start = word(H_START);
+    sid = word(H_SID);
+    first_id = __builtin_amdgcn_readlane(hv, H_IDS + w);  // this wave's first page
+  } else {
+    build_plan<BS, BAL>(p, s_pref, s_kpref, s_sid, s_start, HR, nw, KPC);
+    if (s_pref[p.B] == 0) return;
+    const ShareRange r = share_range<BAL>(s_pref, s_kpref, p.B, HR, KPC, nw, wg);
+    x_begin = r.x_begin;
+    x_stop = r.x_stop;
+    T = r.T;
   }
+  auto page_start = [&](long long w) { return div_floor(w * T, nw); };
   const uint16_t* kbase = static_cast<const uint16_t*>(p.kpool);
   const uint16_t* vbase = static_cast<const uint16_t*>(p.vpool);
   const uint8_t* kbase8 = static_cast<const uint8_t*>(p.kpool);
@@ -633,44 +759,64 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     if constexpr (BAL) asm volatile("" : "+s"(T));
     // This piece: pages [lp0, lp1) of segment (b, hr); its partial slot, and
     // the number of pieces (arrivals) of its segment.
-    int b, hr, lp0, lp1, slot, narr, x0 = 0, w_a = 0;
-    long long Gs = 0;
-    if constexpr (BAL) {
-      b = uni(seq_of(s_pref, p.B, HR, x));
-      const int npw = uni(s_pref[b + 1] - s_pref[b]);  // units of a segment: KPC + pages
-      const int np = npw - KPC;
-      const int local = (int)(x - HR * s_pref[b]);
-      hr = local / npw;
-      Gs = HR * s_pref[b] + (long long)hr * npw;  // the segment's first unit
-      const long long cend = min(Gs + npw, x_stop);
-      lp0 = max(0, (int)(x - Gs) - KPC);
-      lp1 = (int)(cend - Gs) - KPC;
-      w_a = owner(Gs + KPC);  // the workgroup holding page 0
-      narr = owner(Gs + KPC + np - 1) - w_a + 1;
-      slot = 2 * wg + (page_start(wg) >= Gs ? 0 : 1);
-      x = cend;
-    } else {
-      b = uni(seq_of(s_kpref, p.B, HR, x));
-      const int kb = uni(s_kpref[b + 1] - s_kpref[b]);  // pieces per segment of sequence b
-      const int rem = (int)(x - HR * s_kpref[b]);
-      hr = rem / kb;
-      const int piece = rem - hr * kb;
-      const int np = uni(s_pref[b + 1] - s_pref[b]);
-      lp0 = (int)div_floor((long long)piece * np, kb);
-      lp1 = (int)div_floor((long long)(piece + 1) * np, kb);
-      x0 = (int)(x - piece);  // the segment's first piece
-      narr = kb;
-      slot = (int)x;
-      x += 1;
+    const bool first = PL && x == x_begin;  // planned: the head gave it
+    if (!first) {
+      pc = decode_piece<BAL>(x, x_stop, s_pref, s_kpref, p.B, HR, KPC, T, nw, wg);
+      start = uni(s_start[pc.b]);
+      sid = uni(s_sid[pc.b]);
     }
+    const int b = pc.b, hr = pc.hr, lp0 = pc.lp0, lp1 = pc.lp1, slot = pc.slot, narr = pc.narr;
+    const int x0 = pc.x0, w_a = pc.w_a;
+    const long long Gs = pc.Gs;
+    x = pc.x_next;
     const int h = hr / p.nrg, rg = hr - h * p.nrg;
     const int seg = b * (int)HR + hr;
-    const int start = uni(s_start[b]);
     const int L = start + p.C;
     const int qr0 = rg * RPG;
     const int nr = min(RPG, p.G - qr0);
-    const int sid = uni(s_sid[b]);
     const int32_t* table = p.tables + (size_t)sid * p.maxb;
+
+    int tab0 = lp0;  // first page whose block id is sTab[0]
+    // With four query tiles (no registers to spare) pages are read through raw
+    // buffers: the page's base is scalar and each lane keeps one 32-bit offset
+    // for K and one for V (the k-step and tile offsets are scalar operands), so
+    // no 64-bit lane address lives across the walk to be spilled and reloaded.
+    const uint32_t koff = (uint32_t)(i16 * D + 8 * g) * 2u, voff = (uint32_t)(i16 * BS + 4 * g) * 2u;
+    auto load_page_phys = [&](PageRegs<D, KT>& f, int phys) {
+      const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
+      if constexpr (kFp8) {
+        // codes: one byte per element; K lane: 8 dims, V lane: 4 keys
+        const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase8 + slot, BS * D), rv = span_rsrc(vbase8 + slot, BS * D);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint2, load_b64(rk, koff / 2, 32u * ks));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) f.v[mt] = load_b32(rv, voff / 2, 16u * BS * mt);
+        const float2 sc = *reinterpret_cast<const float2*>(p.scales + ((size_t)p.layer * p.cap + phys) * 2);
+        f.sk = sc.x;
+        f.sv = sc.y;
+      } else if constexpr (NT >= 4) {
+        const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase + slot, BS * D * 2);
+        const __amdgpu_buffer_rsrc_t rv = span_rsrc(vbase + slot, BS * D * 2);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint4, load_b128(rk, koff, 64u * ks));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) f.v[mt] = __builtin_bit_cast(uint2, load_b64(rv, voff, 32u * BS * mt));
+      } else {
+        const uint16_t* kp = kbase + slot;
+        const uint16_t* vp = vbase + slot;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) f.k[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) f.v[mt] = *reinterpret_cast<const uint2*>(vp + (16 * mt + i16) * BS + 4 * g);
+      }
+    };
+    auto load_page = [&](PageRegs<D, KT>& f, int page) { load_page_phys(f, uni(sTab[page - tab0])); };
+    // Wave w takes pages tab0 + w, tab0 + w + NWV, ...; kRing rotating
+    // register buffers keep kRing - 1 pages in flight while one is computed.
+    constexpr int kRing = ring_depth(NT, D, KT);
+    static_assert(kRing == 2, "one page is in flight when a window starts");
+    PageRegs<D, KT> buf[kRing];
+
 
     // With four query tiles the row index and the ratio are opaque here, so
     // that what derives from them (the rows 16 nt + i16, the divisor's
@@ -699,7 +845,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       const int ntab = min(kTabChunk, lp1 - lp0);
       int tabv = 0, lenv = 0x7fffffff;
       if (stid < ntab) tabv = table[lp0 + stid];
-      if (stid == 0 && p.lens) lenv = p.lens[sid];
+      if (!PL && stid == 0 && p.lens) lenv = p.lens[sid];
       uint4 qv[kQItems];
 #pragma unroll
       for (int k = 0; k < kQItems; ++k) {
@@ -711,6 +857,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
           qv[k] = *reinterpret_cast<const uint4*>(qbase + (((size_t)b * p.C + j) * p.Hq + hq) * D + 8 * c);
         }
       }
+      // Issued after the staging loads, so their wait does not include it.
+      if (first) load_page_phys(buf[0], first_id);
       __syncthreads();
       if (stid < ntab) sTab[stid] = safe_block(p, tabv, b);
       if (lenv < L) flag_bad_read(p, b);
@@ -721,7 +869,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         if (idx < RPG * (D / 8)) *reinterpret_cast<uint4*>(&sQ[rr * QSTR + 8 * c]) = qv[k];
       }
     } else {
-      const int lenv = threadIdx.x == 0 && p.lens ? p.lens[sid] : 0x7fffffff;
+      const int lenv = !PL && threadIdx.x == 0 && p.lens ? p.lens[sid] : 0x7fffffff;
+      if (first) load_page_phys(buf[0], first_id);
       __syncthreads();
       for (int t = threadIdx.x; t < min(kTabChunk, lp1 - lp0); t += blockDim.x)
         sTab[t] = safe_block(p, table[lp0 + t], b);
@@ -763,42 +912,6 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         for (int nt = 0; nt < NT; ++nt)
           qreg[ks][nt] = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
     }
-
-    int tab0 = lp0;  // first page whose block id is sTab[0]
-    // With four query tiles (no registers to spare) pages are read through raw
-    // buffers: the page's base is scalar and each lane keeps one 32-bit offset
-    // for K and one for V (the k-step and tile offsets are scalar operands), so
-    // no 64-bit lane address lives across the walk to be spilled and reloaded.
-    const uint32_t koff = (uint32_t)(i16 * D + 8 * g) * 2u, voff = (uint32_t)(i16 * BS + 4 * g) * 2u;
-    auto load_page = [&](PageRegs<D, KT>& f, int page) {
-      const int phys = uni(sTab[page - tab0]);
-      const size_t slot = slot_index(p, phys, h) * (size_t)(BS * D);
-      if constexpr (kFp8) {
-        // codes: one byte per element; K lane: 8 dims, V lane: 4 keys
-        const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase8 + slot, BS * D), rv = span_rsrc(vbase8 + slot, BS * D);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint2, load_b64(rk, koff / 2, 32u * ks));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) f.v[mt] = load_b32(rv, voff / 2, 16u * BS * mt);
-        const float2 sc = *reinterpret_cast<const float2*>(p.scales + ((size_t)p.layer * p.cap + phys) * 2);
-        f.sk = sc.x;
-        f.sv = sc.y;
-      } else if constexpr (NT >= 4) {
-        const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase + slot, BS * D * 2);
-        const __amdgpu_buffer_rsrc_t rv = span_rsrc(vbase + slot, BS * D * 2);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint4, load_b128(rk, koff, 64u * ks));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) f.v[mt] = __builtin_bit_cast(uint2, load_b64(rv, voff, 32u * BS * mt));
-      } else {
-        const uint16_t* kp = kbase + slot;
-        const uint16_t* vp = vbase + slot;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) f.k[ks] = *reinterpret_cast<const uint4*>(kp + i16 * D + 32 * ks + 8 * g);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) f.v[mt] = *reinterpret_cast<const uint2*>(vp + (16 * mt + i16) * BS + 4 * g);
-      }
-    };
 
     auto compute_page = [&](PageRegs<D, KT>& f, int page) {
       const int kpos0 = page * BS + 4 * g;  // key position of accumulator element 0
@@ -935,10 +1048,6 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       }
     };
 
-    // Wave w takes pages tab0 + w, tab0 + w + NWV, ...; kRing rotating
-    // register buffers keep kRing - 1 pages in flight while one is computed.
-    constexpr int kRing = ring_depth(NT, D, KT);
-    PageRegs<D, KT> buf[kRing];
     for (; tab0 < lp1; tab0 += kTabChunk) {
       const int wend = min(lp1, tab0 + kTabChunk);
       if (tab0 != lp0) {
@@ -952,8 +1061,11 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       // window's last page): the number of loads in flight is then the same on
       // every path, so each page waits only for its own loads (vmcnt(N)), not
       // for the pages prefetched after it (vmcnt(0)).
+      // (a planned call's first window: its first page is already in flight)
+      if (!(first && tab0 == lp0)) {
 #pragma unroll
-      for (int u = 0; u < kRing - 1; ++u) load_page(buf[u], min(pg0 + NWV * u, last));
+        for (int u = 0; u < kRing - 1; ++u) load_page(buf[u], min(pg0 + NWV * u, last));
+      }
       for (int it = 0; it < n; it += kRing) {
 #pragma unroll
         for (int u = 0; u < kRing; ++u) {
@@ -1107,6 +1219,72 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   }
 }
 
+// ------------------------------------------------------------------ plan of a round
+//
+// What every MFMA call of a round would otherwise recompute in its prologue
+// -- build_plan over the batch, each share's range and first piece -- plus the
+// (validated) block id of each wave's first page, for planned calls
+// (attn_mfma_kernel<..., true>) to read in one load. One wave per share of
+// the persistent grid; share 0 also writes the header and the prefix arrays,
+// and checks every sequence's written length.
+template <bool BAL>
+__global__ __launch_bounds__(64) void attn_plan_kernel(AttnParams p, int kpc) {
+  extern __shared__ int s_pref[];
+  int* s_kpref = s_pref + p.B + 1;
+  int* s_sid = s_kpref + p.B + 1;
+  int* s_start = s_sid + p.B + 1;
+  const int nw = gridDim.x, wg = blockIdx.x, lane = threadIdx.x;
+  const long long HR = (long long)p.Hkv * p.nrg;
+  build_plan<16, BAL>(p, s_pref, s_kpref, s_sid, s_start, HR, nw, kpc);
+  int* plan = p.plan;
+  if (wg == 0) {
+    for (int t = lane; t < 4 * (p.B + 1); t += 64) plan[kPlanHeader + t] = s_pref[t];
+    if (p.lens)
+      for (int b = lane; b < p.B; b += 64)
+        if (p.lens[s_sid[b]] < s_start[b] + p.C) flag_bad_read(p, b);
+  }
+  ShareRange r{0, 0, HR * s_pref[p.B]};
+  if (s_pref[p.B] > 0) r = share_range<BAL>(s_pref, s_kpref, p.B, HR, kpc, nw, wg);
+  Piece pc{};
+  int start = 0, sid = 0, id = 0;
+  if (r.x_begin < r.x_stop) {
+    pc = decode_piece<BAL>(r.x_begin, r.x_stop, s_pref, s_kpref, p.B, HR, kpc, r.T, nw, wg);
+    start = s_start[pc.b];
+    sid = s_sid[pc.b];
+    // Wave w's first load of the first window: page min(lp0 + w, window end - 1).
+    if (lane < kMfmaThreads / 64) {
+      const int page = min(pc.lp0 + lane, min(pc.lp1, pc.lp0 + kTabChunk) - 1);
+      id = safe_block(p, p.tables[(size_t)sid * p.maxb + page], pc.b);
+    }
+  }
+  int* head = plan + plan_heads_at(p.B) + (size_t)wg * kHeadInts;
+  if (lane == 0) {
+    st64(head + H_XB, r.x_begin);
+    st64(head + H_XS, r.x_stop);
+    st64(head + H_XN, pc.x_next);
+    st64(head + H_GS, pc.Gs);
+    head[H_B] = pc.b;
+    head[H_HR] = pc.hr;
+    head[H_LP0] = pc.lp0;
+    head[H_LP1] = pc.lp1;
+    head[H_SLOT] = pc.slot;
+    head[H_NARR] = pc.narr;
+    head[H_X0] = pc.x0;
+    head[H_WA] = pc.w_a;
+    head[H_START] = start;
+    head[H_SID] = sid;
+    if (wg == 0) {
+      plan[0] = p.B;
+      plan[1] = nw;
+      plan[2] = kpc;
+      plan[3] = 1;
+      st64(plan + 4, r.T);
+      st64(plan + 6, HR);
+    }
+  }
+  if (lane < kMfmaThreads / 64) head[H_IDS + lane] = id;
+}
+
 // ------------------------------------------------------------------ merge (VALU splits)
 template <int QT>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnParams p) {
@@ -1138,6 +1316,12 @@ struct Plan {
   bool mfma;
   int nt;  // MFMA query tiles per workgroup
   int pages_per_split, max_splits, nrg, rows_per_group;
+  // Calls of this shape read a round's plan when one is given. The head_dim
+  // 128 kernels with four query tiles have no registers to spare: the planned
+  // prologue made them spill in the page walk (the batch-128 Qwen2.5-3B shape
+  // ran 90.8 -> 97.5 us per layer), so they keep the in-kernel prologue.
+  bool plannable() const { return mfma && !(nt == 4 && rows_per_group == 64 && d128); }
+  bool d128;
 };
 
 Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv_dtype, int q_dtype) {
@@ -1152,6 +1336,7 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
   pl.mfma = (kv_dtype == SPV_BF16 || kv_dtype == SPV_FP8E4M3) && q_dtype == SPV_BF16 && bs == 16 &&
             (d == 128 || d == 64) && B <= kMfmaMaxB && fits32;
   const int max_pages = (max_ctx + bs - 1) / bs;
+  pl.d128 = d == 128;
   if (pl.mfma) {
     pl.nt = G >= 64 ? 4 : (G + 15) / 16;
     pl.rows_per_group = 16 * pl.nt;
@@ -1240,26 +1425,44 @@ int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s, b
   return SPV_OK;
 }
 
-template <int D, bool BAL, int KT>
+template <int D, bool BAL, int KT, bool PL>
 void launch_mfma_mode(const AttnParams& p, int nt, hipStream_t s, dim3 grid, size_t smem) {
   const dim3 blk(kMfmaThreads);
   switch (nt) {
-    case 1: launch_attn(attn_mfma_kernel<1, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
-    case 2: launch_attn(attn_mfma_kernel<2, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
-    case 3: launch_attn(attn_mfma_kernel<3, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
-    default: launch_attn(attn_mfma_kernel<4, D, SPV_BF16, BAL, KT>, grid, blk, smem, s, true, true, p); break;
+    case 1: launch_attn(attn_mfma_kernel<1, D, SPV_BF16, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
+    case 2: launch_attn(attn_mfma_kernel<2, D, SPV_BF16, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
+    case 3: launch_attn(attn_mfma_kernel<3, D, SPV_BF16, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
+    default:  // four query tiles: planned only at head_dim 64 (Plan::plannable)
+      launch_attn(attn_mfma_kernel<4, D, SPV_BF16, BAL, KT, PL && D != 128>, grid, blk, smem, s, true, true, p);
+      break;
   }
 }
 
 // Equal pieces when the workgroups outnumber the (sequence, kv head, row
-// group) segments, else the page-balanced split.
+// group) segments, else the page-balanced split. A planned call (p.plan set)
+// reads the round's plan.
+bool balanced_split(const AttnParams& p, int nw) { return (long long)p.Hkv * p.nrg * p.B >= nw; }
+
 template <int D, int KT>
 void launch_mfma(const AttnParams& p, int nt, hipStream_t s) {
   const size_t smem = (size_t)4 * (p.B + 1) * sizeof(int);  // page / piece prefixes, ids, starts
   const int nw = persistent_wgs();
-  const bool balanced = (long long)p.Hkv * p.nrg * p.B >= nw;
-  if (balanced) launch_mfma_mode<D, true, KT>(p, nt, s, dim3(nw), smem);
-  else launch_mfma_mode<D, false, KT>(p, nt, s, dim3(nw), smem);
+  const bool bal = balanced_split(p, nw);
+  if (p.plan) {  // (never with four query tiles at head_dim 128: Plan::plannable)
+    if (bal) launch_mfma_mode<D, true, KT, true>(p, nt, s, dim3(nw), smem);
+    else launch_mfma_mode<D, false, KT, true>(p, nt, s, dim3(nw), smem);
+  } else {
+    if (bal) launch_mfma_mode<D, true, KT, false>(p, nt, s, dim3(nw), smem);
+    else launch_mfma_mode<D, false, KT, false>(p, nt, s, dim3(nw), smem);
+  }
+}
+
+void launch_plan(const AttnParams& p, int d, int kv_dtype, hipStream_t s) {
+  const size_t smem = (size_t)4 * (p.B + 1) * sizeof(int);
+  const int nw = persistent_wgs();
+  const int kpc = piece_cost(d, kv_dtype);
+  if (balanced_split(p, nw)) hipLaunchKernelGGL(attn_plan_kernel<true>, dim3(nw), dim3(64), smem, s, p, kpc);
+  else hipLaunchKernelGGL(attn_plan_kernel<false>, dim3(nw), dim3(64), smem, s, p, 0);
 }
 
 }  // namespace
@@ -1288,7 +1491,7 @@ int spv::verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_p
                      const int32_t* seq_ids, const int32_t* start_pos, const int32_t* seq_lens, int32_t* ctr,
                      int32_t B, int32_t C, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int32_t layer, int32_t capacity, int32_t max_ctx, float scale,
-                     void* workspace, size_t workspace_bytes, bool exact_layout, void* stream) {
+                     const void* plan, void* workspace, size_t workspace_bytes, bool exact_layout, void* stream) {
   struct Disarm {
     ~Disarm() { g_arm = TimingArm{}; }
   } disarm;  // armed timing events serve this call only, whatever its outcome
@@ -1334,6 +1537,8 @@ int spv::verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_p
   p.rows_per_group = pl.rows_per_group;
   p.max_pages = (max_ctx + block_size - 1) / block_size;
   p.scale_log2 = scale * kLog2e;
+  // A round's plan serves MFMA calls only (the VALU path has no prologue to skip).
+  if (pl.plannable() && plan) p.plan = static_cast<int*>(const_cast<void*>(plan));
   if (need > 0) {
     const size_t rows = partial_rows(pl, B, C, num_q_heads, num_kv_heads, nw_layout);
     char* ws = static_cast<char*>(workspace);
@@ -1390,7 +1595,65 @@ int spv_verify_attn(void* out, const void* q, int q_dtype, const void* k_pool, c
                     void* workspace, size_t workspace_bytes, void* stream) {
   return spv::verify_attn_impl(out, q, q_dtype, k_pool, v_pool, kv_dtype, kv_scales, block_tables, max_blocks_per_seq,
                           seq_ids, start_pos, seq_lens, ctr, B, C, num_q_heads, num_kv_heads, head_dim, block_size,
-                          layer, capacity, max_ctx, scale, workspace, workspace_bytes, false, stream);
+                          layer, capacity, max_ctx, scale, nullptr, workspace, workspace_bytes, false, stream);
+}
+
+size_t spv_verify_attn_plan_bytes(int32_t B) {
+  if (B < 1 || B > kMfmaMaxB) return 0;
+  return plan_ints(B, kMfmaWGsMax) * sizeof(int32_t);
+}
+
+int spv_verify_attn_plan(const int32_t* block_tables, int32_t max_blocks_per_seq, const int32_t* seq_ids,
+                         const int32_t* start_pos, const int32_t* seq_lens, int32_t* ctr, int32_t B, int32_t C,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                         int32_t kv_dtype, int32_t capacity, int32_t max_ctx, void* plan, size_t plan_bytes,
+                         void* stream) {
+  if (!block_tables || !seq_ids || !start_pos || !plan) return SPV_ERR_ARG;
+  if (B < 0 || C < 1 || num_kv_heads < 1 || num_q_heads < num_kv_heads || num_q_heads % num_kv_heads ||
+      head_dim < 1 || block_size < 1 || capacity < 1 || max_ctx < C ||
+      max_blocks_per_seq < (max_ctx + block_size - 1) / block_size || dtype_size(kv_dtype) == 0)
+    return SPV_ERR_ARG;
+  if (B == 0) return SPV_OK;
+  // Planned calls take bf16 queries; a shape off the MFMA path needs no plan.
+  const Plan pl = make_plan(B, C, num_q_heads, num_kv_heads, head_dim, block_size, max_ctx, kv_dtype, SPV_BF16);
+  if (!pl.plannable()) return SPV_OK;
+  if (plan_bytes < plan_ints(B, persistent_wgs()) * sizeof(int32_t)) return SPV_ERR_WORKSPACE;
+  AttnParams p{};
+  p.tables = block_tables;
+  p.seq_ids = seq_ids;
+  p.start = start_pos;
+  p.lens = seq_lens;
+  p.ctr = ctr;
+  p.maxb = max_blocks_per_seq;
+  p.B = B;
+  p.C = C;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.ratio = num_q_heads / num_kv_heads;
+  p.G = C * p.ratio;
+  p.d = head_dim;
+  p.bs = block_size;
+  p.cap = capacity;
+  p.nrg = pl.nrg;
+  p.rows_per_group = pl.rows_per_group;
+  p.max_pages = (max_ctx + block_size - 1) / block_size;
+  p.plan = static_cast<int*>(plan);
+  launch_plan(p, head_dim, kv_dtype, (hipStream_t)stream);
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+int spv_verify_attn_planned(void* out, const void* q, int q_dtype, const void* k_pool, const void* v_pool,
+                            int kv_dtype, const float* kv_scales, const int32_t* block_tables,
+                            int32_t max_blocks_per_seq, const int32_t* seq_ids, const int32_t* start_pos,
+                            const int32_t* seq_lens, int32_t* ctr, int32_t B, int32_t C, int32_t num_q_heads,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t layer,
+                            int32_t capacity, int32_t max_ctx, float scale, const void* plan, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (!plan) return SPV_ERR_ARG;
+  return spv::verify_attn_impl(out, q, q_dtype, k_pool, v_pool, kv_dtype, kv_scales, block_tables, max_blocks_per_seq,
+                          seq_ids, start_pos, seq_lens, ctr, B, C, num_q_heads, num_kv_heads, head_dim, block_size,
+                          layer, capacity, max_ctx, scale, plan, workspace, workspace_bytes, false, stream);
 }
 
 }  // extern "C"

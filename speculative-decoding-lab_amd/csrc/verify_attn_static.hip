@@ -55,7 +55,7 @@ int spv_verify_attn_static(void* out, const void* q, int q_dtype, const void* k_
   // before anything is enqueued.
   return spv::verify_attn_impl(out, q, q_dtype, k_pool, v_pool, kv_dtype, kv_scales, block_tables,
                                max_blocks_per_seq, seq_ids, start_pos, seq_lens, ctr, B, C, num_q_heads,
-                               num_kv_heads, head_dim, block_size, layer, capacity, max_ctx, scale, ws,
+                               num_kv_heads, head_dim, block_size, layer, capacity, max_ctx, scale, nullptr, ws,
                                kStaticScratchBytes, true, stream);
 }
 

@@ -57,6 +57,9 @@ SIGNATURES = {
     "spv_kv_read_blocks": (I, [P, I, I, P, I, I, I, I, I, I, P, P]),
     "spv_verify_attn_workspace_bytes": (S, [I, I, I, I, I, I, I]),
     "spv_verify_attn": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P, S, P]),
+    "spv_verify_attn_plan_bytes": (S, [I]),
+    "spv_verify_attn_plan": (I, [P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, P, S, P]),
+    "spv_verify_attn_planned": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P, P, S, P]),
     "spv_prefill_attn": (I, [P, P, P, P, I, P, I, I, I, I, I, F, P]),
     "spv_time_next_attention": (I, [P, P]),
     "spv_verify_attn_static_max_bytes": (S, []),

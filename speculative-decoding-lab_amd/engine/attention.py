@@ -17,6 +17,11 @@ Drop-in for the reference's engine/attention.py on the verify path:
 ``paged_attention_extend`` reads the block tables and lengths from the device
 metadata of :class:`engine.kv.PagedKVCache`; the K/V of the query chunk must
 already be written (write-then-attend, engine/model.py:182-190).
+
+A round calls the attention once per layer with the same sequences and start
+positions. ``VerifyPlan`` computes what those calls share (the split of the
+batch over the workgroups and each workgroup's first pages) once; calls given
+the plan start their page walk one round trip after launch.
 """
 
 from __future__ import annotations
@@ -58,14 +63,57 @@ def gather_ctx(kv: PagedKVCache, layer: int, seq_id: int, length: int) -> torch.
     return out
 
 
+class VerifyPlan:
+    """The shared part of one round's attention calls, computed on the device.
+
+    Made once the round's blocks are allocated (after the first layer's
+    append) for the round's sequences, start positions (int32 device tensors
+    or lists), chunk length, query heads and ``max_ctx``; every layer's
+    ``verify_attention`` given it must use exactly those. It also checks, once,
+    that every sequence's written length covers its chunk (the per-call check
+    of unplanned calls). Valid while the round's start positions and block
+    tables stand.
+    """
+
+    def __init__(self, kv: PagedKVCache, seq_ids: Union[Sequence[int], torch.Tensor],
+                 start_positions: Union[Sequence[int], torch.Tensor], chunk: int, num_q_heads: int,
+                 max_ctx: int, buf: Optional[torch.Tensor] = None) -> None:
+        self.kv = kv
+        self.seq_ids = _hip.i32(seq_ids, kv.device)
+        self.start = _hip.i32(start_positions, kv.device)
+        self.B = int(self.seq_ids.numel())
+        self.chunk, self.num_q_heads, self.max_ctx = int(chunk), int(num_q_heads), int(max_ctx)
+        if self.max_ctx > kv.max_blocks_per_seq * kv.block_size:
+            kv._grow_width(-(-self.max_ctx // kv.block_size))
+        nbytes = int(_hip.lib().spv_verify_attn_plan_bytes(max(self.B, 1)))
+        if buf is not None and nbytes and (buf.numel() * buf.element_size() < nbytes or buf.device != kv.device):
+            raise ValueError("plan buffer too small or on another device")
+        # ``buf``: a buffer of an earlier plan to write this one into (no allocation)
+        self.buf = (buf if buf is not None else torch.empty(nbytes, dtype=torch.uint8, device=kv.device)) \
+            if nbytes else None
+        if self.B and self.buf is not None:
+            call("spv_verify_attn_plan", ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(self.seq_ids),
+                 ptr(self.start), ptr(kv.lens_dev), ptr(kv.allocator.ctr), self.B, self.chunk, self.num_q_heads,
+                 kv.num_kv_heads, kv.head_dim, kv.block_size, kv._dt, kv.allocator.capacity, self.max_ctx,
+                 ptr(self.buf), int(self.buf.numel() * self.buf.element_size()), _hip.stream_of(kv.device))
+            kv._stale = True
+
+    def check(self, kv: PagedKVCache, B: int, chunk: int, num_q_heads: int, max_ctx: int) -> None:
+        if kv is not self.kv or (B, chunk, num_q_heads, max_ctx) != (self.B, self.chunk, self.num_q_heads,
+                                                                      self.max_ctx):
+            raise ValueError("the attention call does not match its plan")
+
+
 def verify_attention(query_3d: torch.Tensor, kv: PagedKVCache, layer: int,
                      seq_ids: Union[Sequence[int], torch.Tensor],
                      start_positions: Union[Sequence[int], torch.Tensor], max_ctx: int,
-                     scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                     plan: Optional[VerifyPlan] = None) -> torch.Tensor:
     """Device-argument form of ``paged_attention_extend``.
 
     ``seq_ids``/``start_positions`` may be int32 device tensors (no host sync);
-    ``max_ctx`` must bound ``start + chunk`` for every row.
+    ``max_ctx`` must bound ``start + chunk`` for every row. ``plan``: the
+    round's ``VerifyPlan`` (same sequences, starts, chunk, heads, max_ctx).
     """
     B, chunk, hq, d = query_3d.shape
     if d != kv.head_dim or hq % kv.num_kv_heads:
@@ -77,19 +125,26 @@ def verify_attention(query_3d: torch.Tensor, kv: PagedKVCache, layer: int,
         out = torch.empty_like(q)
     if B == 0:
         return out
-    sid_t = _hip.i32(seq_ids, kv.device)
-    start_t = _hip.i32(start_positions, kv.device)
+    if plan is not None:
+        plan.check(kv, B, chunk, hq, int(max_ctx))
+        sid_t, start_t = plan.seq_ids, plan.start
+    else:
+        sid_t = _hip.i32(seq_ids, kv.device)
+        start_t = _hip.i32(start_positions, kv.device)
     if max_ctx > kv.max_blocks_per_seq * kv.block_size:
         kv._grow_width(-(-max_ctx // kv.block_size))
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
     ws_bytes = _hip.lib().spv_verify_attn_workspace_bytes(B, chunk, hq, kv.num_kv_heads, d,
                                                           kv.block_size, int(max_ctx))
     ws = _workspace.get(ws_bytes, kv.device) if ws_bytes else None
-    call("spv_verify_attn", ptr(out), ptr(q), _hip.dtype_code(q.dtype), ptr(kv.k_pool), ptr(kv.v_pool),
-         kv._dt, ptr(kv.scales), ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t),
-         ptr(kv.lens_dev), ptr(kv.allocator.ctr), B, chunk,
-         hq, kv.num_kv_heads, d, kv.block_size, int(layer), kv.allocator.capacity, int(max_ctx),
-         scale, ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
+    args = (ptr(out), ptr(q), _hip.dtype_code(q.dtype), ptr(kv.k_pool), ptr(kv.v_pool),
+            kv._dt, ptr(kv.scales), ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t),
+            ptr(kv.lens_dev), ptr(kv.allocator.ctr), B, chunk,
+            hq, kv.num_kv_heads, d, kv.block_size, int(layer), kv.allocator.capacity, int(max_ctx), scale)
+    if plan is not None and plan.buf is not None:
+        call("spv_verify_attn_planned", *args, ptr(plan.buf), ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
+    else:
+        call("spv_verify_attn", *args, ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
     # A read of unwritten keys is flagged on the device and raised (IndexError)
     # at the next metadata query, without a synchronisation here.
     kv._stale = True

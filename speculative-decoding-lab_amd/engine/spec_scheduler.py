@@ -37,7 +37,7 @@ import torch
 
 from . import _hip
 from ._hip import call, ptr
-from .attention import verify_attention
+from .attention import VerifyPlan, verify_attention
 from .kv import PagedKVCache
 
 _workspace = _hip.Workspace()
@@ -241,8 +241,10 @@ class VerifyStep:
     positions (``kv.seq_lengths`` at round start), per-layer ``(q, k, v)`` of the
     ``gamma+1`` verify tokens, the target/draft logits of the round, the draft
     proposals, and the randomness. The round writes the K/V of every layer,
-    runs verify attention per layer, samples, and rewinds the pool on the device
-    with the sampled lengths. Nothing synchronises with the host.
+    runs verify attention per layer (the layers share one ``VerifyPlan``, made
+    after the first layer's append allocated the round's blocks), samples, and
+    rewinds the pool on the device with the sampled lengths. Nothing
+    synchronises with the host.
     """
 
     def __init__(self, kv: PagedKVCache, gamma: int, temperature: float, eos_id: Optional[int] = None):
@@ -273,14 +275,17 @@ class VerifyStep:
                 e.record()
                 events.append(e)
 
+        plan = None
         for layer in range(len(q_layers)):
             mark()
             # the first layer's call allocates the chunk's blocks for every layer
             self.kv.write_block_device(layer, sid_t, st_t, k_layers[layer].to(self.kv.dtype).contiguous(),
                                        v_layers[layer].to(self.kv.dtype).contiguous(), alloc=layer == 0)
+            if plan is None:  # the round's attention plan, once its blocks exist
+                plan = VerifyPlan(self.kv, sid_t, st_t, chunk, int(q_layers[layer].shape[2]), max_ctx)
             mark()
             results.append(verify_attention(q_layers[layer], self.kv, layer, sid_t, st_t, max_ctx,
-                                            out=None if outs is None else outs[layer]))
+                                            out=None if outs is None else outs[layer], plan=plan))
         mark()
         return results
 
@@ -391,10 +396,14 @@ class DraftLoop:
         for s in range(self.gamma):
             pos = ctx + s
             outs_s = []
+            plan = None
             for layer in range(len(q_steps[s])):
                 kv.write_block_device(layer, seq_ids, pos, k_steps[s][layer], v_steps[s][layer], alloc=layer == 0)
+                if plan is None:  # the step's attention plan, once its blocks exist
+                    plan = VerifyPlan(kv, seq_ids, pos, 1, int(q_steps[s][layer].shape[2]), max_ctx + s + 1)
                 o = None if attn_out is None else attn_out[s][layer]
-                outs_s.append(verify_attention(q_steps[s][layer], kv, layer, seq_ids, pos, max_ctx + s + 1, out=o))
+                outs_s.append(verify_attention(q_steps[s][layer], kv, layer, seq_ids, pos, max_ctx + s + 1, out=o,
+                                               plan=plan))
             outs.append(outs_s)
             draft_sample(logits_steps[s], self.temperature, None if noise_steps is None else noise_steps[s],
                          out=proposals[:, s])
