@@ -271,7 +271,7 @@ __host__ __device__ constexpr int combine_tiles(int nt, int mt) {
   return (nt == 1 ? 8 : nt <= 3 ? 4 : mt <= 4 ? 4 : 2) < mt ? (nt == 1 ? 8 : nt <= 3 ? 4 : mt <= 4 ? 4 : 2) : mt;
 }
 constexpr int kTabChunk = 512;    // block ids staged in LDS per window
-constexpr int kMergeChunk = 4;    // partial slots the merging workgroup loads at once
+constexpr int kMergeChunk = 8;    // partial slots the merging workgroup loads at once
 // log2 units a score may exceed its column's reference before O is rescaled.
 constexpr float kSlack = 8.f;
 
