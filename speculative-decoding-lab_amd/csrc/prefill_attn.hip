@@ -16,13 +16,16 @@
 // barrier per tile. Per 16-key part of a tile and query tile:
 //   S^T = K Q^T    v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims (LDS),
 //                  B = Q^T fragments held in registers for the whole walk;
-//   O^T += V^T P^T v_mfma_f32_16x16x32_bf16, A = {V^T, V^T} (LDS), B =
-//                  {P_hi, P_lo}: P split into two bf16 halves, so P V carries
-//                  ~16 significant bits of P, not 8.
+//   O^T += V^T P^T two v_mfma_f32_16x16x32_bf16 per pair of 16-key parts,
+//                  A = V^T (LDS, one 16-byte read: keys of both parts), B =
+//                  P_hi, then P_lo: P split into two bf16 halves, so P V
+//                  carries ~16 significant bits of P, not 8.
 // The accumulator layout of S^T is the operand layout of P^T (lane l: keys
 // 4 (l / 16) .. + 3 of query column l % 16), so the softmax moves no data.
 // Online softmax with a per-column reference maximum that scores may exceed by
-// kSlack (log2 units) before O is rescaled; masks only on diagonal tiles.
+// kSlack (log2 units) before O is rescaled; the growth test compares raw
+// scores with a per-column threshold and P = 2^(s scale log2(e) - m) is one
+// fma and one exp2 per score (scale > 0); masks only on diagonal tiles.
 // Workgroups take position blocks from the last (longest key range) to the
 // first, so the long blocks start first.
 //
@@ -68,7 +71,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
   constexpr int KS = D / 32;          // 32-dim k-steps of S^T
   constexpr int MT = D / 16;          // 16-dim tiles of O^T
   constexpr int KP = D + 8;           // bf16 pitch of a K row in LDS (16 bytes of padding)
-  constexpr int VP = kBK + 4;         // bf16 pitch of a V^T row in LDS (8 bytes of padding)
+  constexpr int VP = kBK + 8;         // bf16 pitch of a V^T row in LDS (16 bytes of padding)
   constexpr int kKElems = kBK * KP, kVElems = D * VP;
   __shared__ __align__(16) uint16_t sK[2][kKElems];
   __shared__ __align__(16) uint16_t sV[2][kVElems];
@@ -124,10 +127,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
                                     qb + (((size_t)b * Lc + cpos[nt]) * Hq + chead[nt]) * D + 32 * ks + 8 * g)
                               : make_uint4(0u, 0u, 0u, 0u);
 
-  // Staging: K tile as 16-byte chunks (key, 8 dims); V tile as (key pair, 8
-  // dims) items written transposed, one 32-bit word (two keys) per dim.
+  // Staging: K tile as 16-byte chunks (key, 8 dims), row-major. V tile as
+  // (key pair, 8 dims) items written transposed, one 32-bit word (two keys)
+  // per dim; the 32 pairs of one 8-dim column go to 32 consecutive lanes, so a
+  // wave's word stores cover the 64 banks. In a V^T row, key
+  // k = 32 q + 16 h + 4 g + j sits at 32 q + 8 g + 4 h + j: the 16-byte read of
+  // lane group g returns keys 4 g .. + 3 of the 16-key parts 2 q and 2 q + 1,
+  // the k-slots of the P^T operand below.
   constexpr int kKChunks = kBK * D / 8, kKPer = (kKChunks + kThreads - 1) / kThreads;
-  constexpr int kVItems = kBK / 2 * D / 8, kVPer = (kVItems + kThreads - 1) / kThreads;
+  constexpr int kPairs = kBK / 2;
+  constexpr int kVItems = kPairs * D / 8, kVPer = (kVItems + kThreads - 1) / kThreads;
   uint4 kreg[kKPer], vreg[kVPer][2];
   auto load_tile = [&](int t) {
     const int t0 = t * kBK;
@@ -142,7 +151,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
 #pragma unroll
     for (int i = 0; i < kVPer; ++i) {
       const int c = threadIdx.x + i * kThreads;
-      const int pair = c / (D / 8), col = c % (D / 8);
+      const int pair = c % kPairs, col = c / kPairs;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         vreg[i][e] = make_uint4(0u, 0u, 0u, 0u);  // keys beyond the range stay zero (never NaN)
@@ -165,16 +174,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     for (int i = 0; i < kVPer; ++i) {
       const int c = threadIdx.x + i * kThreads;
       if (c < kVItems) {
-        const int pair = c / (D / 8), col = c % (D / 8);
+        const int pair = c % kPairs, col = c / kPairs;
+        const int k = 2 * pair;
+        const int pos = 32 * (k >> 5) + 8 * ((k >> 2) & 3) + 4 * ((k >> 4) & 1) + (k & 3);
         const uint32_t a[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
         const uint32_t bb[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          // dims 8 col + 2 e (low halves) and + 1 (high halves): keys 2 pair, 2 pair + 1
+          // dims 8 col + 2 e (low halves) and + 1 (high halves): keys k, k + 1
           const uint32_t lo = (a[e] & 0xffffu) | (bb[e] << 16);
           const uint32_t hi = (a[e] >> 16) | (bb[e] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e) * VP + 2 * pair]) = lo;
-          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e + 1) * VP + 2 * pair]) = hi;
+          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e) * VP + pos]) = lo;
+          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e + 1) * VP + pos]) = hi;
         }
       }
     }
@@ -185,13 +196,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m[NT], l[NT];
+  // m: reference maximum in log2 units; thr: the raw score above which a
+  // column's m must grow (scores become log2 units as s * sl2, sl2 > 0).
+  float m[NT], l[NT], thr[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     m[nt] = -INFINITY;
     l[nt] = 0.f;
+    thr[nt] = -INFINITY;
   }
-  const float sl2 = p.scale_log2;
+  const float sl2 = p.scale_log2, inv_sl2 = 1.f / p.scale_log2;
 
   load_tile(0);
   store_tile(0);
@@ -200,10 +214,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     const int buf = t & 1;
     if (t + 1 < ntiles) load_tile(t + 1);  // in flight while this tile is computed
     const int t0 = t * kBK;
-    const bool need_mask = t0 + kBK - 1 > p0;  // some key beyond the block's first position
     const uint16_t* K = sK[buf];
     const uint16_t* Vt = sV[buf];
-    // S^T for the four 16-key parts of the tile
+    // raw S^T for the four 16-key parts of the tile
     f32x4_t sc[4][NT];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -219,63 +232,82 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
                                                                0, 0);
       }
     }
-    // scores in log2 units, masks, and the growth test against the reference m
+    if (t0 + kBK - 1 > p0) {  // the tile crosses the block's diagonal: causal mask
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+            if (t0 + 16 * kt + 4 * g + jj > cpos[nt]) sc[kt][nt][jj] = -INFINITY;
+    }
+    // growth test against the reference maximum, on the column maxima
+    float mx[NT];
     bool grow = false;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int nt = 0; nt < NT; ++nt) {
+      float a = fmaxf(fmaxf(sc[0][nt][0], sc[0][nt][1]), fmaxf(sc[0][nt][2], sc[0][nt][3]));
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          float x = sc[kt][nt][jj] * sl2;
-          if (need_mask && t0 + 16 * kt + 4 * g + jj > cpos[nt]) x = -INFINITY;
-          sc[kt][nt][jj] = x;
-          grow |= x > m[nt] + kSlack;
-        }
+      for (int kt = 1; kt < 4; ++kt)
+        a = fmaxf(a, fmaxf(fmaxf(sc[kt][nt][0], sc[kt][nt][1]), fmaxf(sc[kt][nt][2], sc[kt][nt][3])));
+      mx[nt] = a;
+      grow |= a > thr[nt];
+    }
     if (__any(grow)) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-          mx = fmaxf(mx, fmaxf(fmaxf(sc[kt][nt][0], sc[kt][nt][1]), fmaxf(sc[kt][nt][2], sc[kt][nt][3])));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m[nt], mx);
+        float a = fmaxf(mx[nt], __shfl_xor(mx[nt], 16, 64));
+        a = fmaxf(a, __shfl_xor(a, 32, 64));
+        const float m_new = fmaxf(m[nt], a * sl2);
         const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[nt] - m_new);
         l[nt] *= alpha;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) o[mt][nt] *= alpha;
         m[nt] = m_new;
+        thr[nt] = (m_new + kSlack) * inv_sl2;
       }
     }
-    // P = 2^(x - m) as hi + lo bf16 halves; row sums take P itself
+    // P = 2^(s sl2 - m) as hi + lo bf16 halves, two 16-key parts per operand;
+    // row sums take P itself.
+    float mu[NT];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      bf16x8_t pf[NT];
+    for (int nt = 0; nt < NT; ++nt) mu[nt] = m[nt] == -INFINITY ? 0.f : m[nt];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
-        float e[4];
+    for (int q2 = 0; q2 < 2; ++q2) {
+      uint32_t ph[NT][4], pl[NT][4];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(sc[kt][nt][jj] - mu);
-        l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
-        const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
-        const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
-        const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
-        const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
-        pf[nt] = __builtin_bit_cast(
-            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
-                                 pack2_bf16(r01[0], r01[1]), pack2_bf16(r23[0], r23[1])));
-      }
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int kt = 2 * q2 + h;
+          float e[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[kt][nt][jj], sl2, -mu[nt]));
+          l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
+          const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
+          const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
+          const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
+          const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
+          ph[nt][2 * h] = __builtin_bit_cast(uint32_t, h01);
+          ph[nt][2 * h + 1] = __builtin_bit_cast(uint32_t, h23);
+          pl[nt][2 * h] = pack2_bf16(r01[0], r01[1]);
+          pl[nt][2 * h + 1] = pack2_bf16(r23[0], r23[1]);
+        }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        // V^T rows (dim 16 mt + i16), keys 16 kt + 4 g .. + 3, in both halves of the k-slots
-        const uint2 vv = *reinterpret_cast<const uint2*>(&Vt[(16 * mt + i16) * VP + 16 * kt + 4 * g]);
-        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(vv.x, vv.y, vv.x, vv.y));
+        // V^T row (dim 16 mt + i16): keys 4 g .. + 3 of parts 2 q2 and 2 q2 + 1
+        const bf16x8_t va =
+            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&Vt[(16 * mt + i16) * VP + 32 * q2 + 8 * g]));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[nt], o[mt][nt], 0, 0, 0);
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              va, __builtin_bit_cast(bf16x8_t, make_uint4(ph[nt][0], ph[nt][1], ph[nt][2], ph[nt][3])), o[mt][nt],
+              0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              va, __builtin_bit_cast(bf16x8_t, make_uint4(pl[nt][0], pl[nt][1], pl[nt][2], pl[nt][3])), o[mt][nt],
+              0, 0, 0);
       }
     }
     if (t + 1 < ntiles) store_tile(buf ^ 1);  // that buffer's readers finished before the last barrier
@@ -441,7 +473,10 @@ int spv_prefill_attn(void* out, const void* q, const void* k, const void* v, int
   hipStream_t s = (hipStream_t)stream;
   // The MFMA path holds 256 rows (positions x heads of a kv head) per
   // workgroup: at least one position, i.e. up to 256 q heads per kv head.
-  if (dtype == SPV_BF16 && (head_dim == 128 || head_dim == 64) && p.ratio <= 256) {
+  // It applies the scale inside the exponent (growth tests on raw scores), so
+  // it takes a positive finite scale; any other scale takes the VALU path.
+  if (dtype == SPV_BF16 && (head_dim == 128 || head_dim == 64) && p.ratio <= 256 && scale > 0.f &&
+      p.scale_log2 < INFINITY) {
     if (head_dim == 128) launch_prefill_mfma<2, 128>(p, s);
     else launch_prefill_mfma<2, 64>(p, s);
     SPV_CHECK_LAUNCH();
