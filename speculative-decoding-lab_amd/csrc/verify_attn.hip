@@ -38,6 +38,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kAttnThreads = 256;
@@ -251,9 +253,10 @@ constexpr int kMfmaMaxB = 2048;   // the page and piece prefixes of the batch li
 // Register page buffers per wave: one page in flight while one is computed.
 // One workgroup of eight waves per CU (two per SIMD, <= 256 registers each, so
 // every operand stays in VGPRs) keeps eight pages in flight per CU. Deeper
-// rings measured slower: bf16 decode 16.0 -> 17.3 us with three, fp8 pages at
-// the long-context shape (batch 16, 32,768 keys, head_dim 64) 48.8 -> 50.4 us
-// with four, where the conversions and softmax, not the bytes, set the rate.
+// rings measured no faster: bf16 decode 16.0 -> 17.3 us with three; fp8 pages
+// at the long-context shape (batch 16, 32,768 keys, head_dim 64) 48.7 us with
+// two, 50.6 with three, 49.8 with four (with the loads' waits at the ring's
+// depth): a page's MFMA, softmax and P V MFMA in sequence set the rate there.
 __host__ __device__ constexpr int ring_depth(int, int, int) { return 2; }
 // The fixed cost of a piece (query staging, wave combine, partial and merge)
 // in pages of the walk, for the page-balanced split: 32 pages of 8 KB (bf16,
@@ -301,6 +304,9 @@ __device__ __forceinline__ float2 load2_coherent(__amdgpu_buffer_rsrc_t r, size_
 // Values that are the same in every lane of a wave, moved to scalar registers
 // so that page addresses become scalar base + lane offset.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uni_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
 
 // Largest b with hr_count * pref[b] <= x.
 __device__ __forceinline__ int seq_of(const int* pref, int B, long long hr_count, long long x) {
@@ -546,7 +552,7 @@ template <int D>
 struct PageRegs<D, SPV_FP8E4M3> {
   uint2 k[D / 32];     // key i16, dims 32 ks + 8 g .. + 7 (codes)
   uint32_t v[D / 16];  // dim 16 mt + i16, keys 4 g .. 4 g + 3 (codes)
-  float sk, sv;        // the block's K and V scales
+  float sk, sv;        // the block's K and V scales, where the page carries them
 };
 
 // e4m3 codes -> bf16, exactly (every e4m3 value is a bf16 value): the gfx950
@@ -563,6 +569,13 @@ template <int D>
 __device__ __forceinline__ uint4 k_frag(const PageRegs<D, SPV_FP8E4M3>& f, int ks) {
   return make_uint4(fp8x2_to_bf16x2<false>(f.k[ks].x), fp8x2_to_bf16x2<true>(f.k[ks].x),
                     fp8x2_to_bf16x2<false>(f.k[ks].y), fp8x2_to_bf16x2<true>(f.k[ks].y));
+}
+// e4m3 codes -> fp16 times 2^k, k = floor(log2 |s|): the gfx950 conversion
+// applies only the exponent of its scale operand. Exact for k in [-15, 7]
+// (448 * 2^7 < 65504; every product is a multiple of 2^-24).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_f16x2(uint32_t w, float s) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, s, HI));
 }
 template <int D>
 __device__ __forceinline__ uint2 v_frag(const PageRegs<D, SPV_BF16>& f, int mt) { return f.v[mt]; }
@@ -664,6 +677,9 @@ __device__ __forceinline__ int xswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 template <int NT, int D, int QT, bool BAL, int KT, bool PL>
 __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p) {
   constexpr bool kFp8 = KT == SPV_FP8E4M3;
+  // Block ids (and fp8 scales) of a window per lane, or per page from LDS
+  // (see the page walk).
+  constexpr bool kLaneIds = D == 64 || NT <= 2 || (NT == 3 && PL);
   constexpr int KS = D / 32;  // 32-dim k-steps of S^T
   constexpr int MT = D / 16;  // 16-dim tiles of O^T
   constexpr int BS = 16;
@@ -791,9 +807,11 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint2, load_b64(rk, koff / 2, 32u * ks));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) f.v[mt] = load_b32(rv, voff / 2, 16u * BS * mt);
-        const float2 sc = *reinterpret_cast<const float2*>(p.scales + ((size_t)p.layer * p.cap + phys) * 2);
-        f.sk = sc.x;
-        f.sv = sc.y;
+        if constexpr (!kLaneIds) {
+          const float2 sc = *reinterpret_cast<const float2*>(p.scales + ((size_t)p.layer * p.cap + phys) * 2);
+          f.sk = sc.x;
+          f.sv = sc.y;
+        }
       } else if constexpr (NT >= 4) {
         const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase + slot, BS * D * 2);
         const __amdgpu_buffer_rsrc_t rv = span_rsrc(vbase + slot, BS * D * 2);
@@ -810,11 +828,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         for (int mt = 0; mt < MT; ++mt) f.v[mt] = *reinterpret_cast<const uint2*>(vp + (16 * mt + i16) * BS + 4 * g);
       }
     };
-    auto load_page = [&](PageRegs<D, KT>& f, int page) { load_page_phys(f, uni(sTab[page - tab0])); };
     // Wave w takes pages tab0 + w, tab0 + w + NWV, ...; kRing rotating
     // register buffers keep kRing - 1 pages in flight while one is computed.
     constexpr int kRing = ring_depth(NT, D, KT);
-    static_assert(kRing == 2, "one page is in flight when a window starts");
     PageRegs<D, KT> buf[kRing];
 
 
@@ -913,17 +929,49 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
           qreg[ks][nt] = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
     }
 
-    auto compute_page = [&](PageRegs<D, KT>& f, int page) {
+    // sk, sv: an fp8 page's K and V scales (wave-uniform)
+    auto compute_page = [&](PageRegs<D, KT>& f, int page, float sk, float sv) {
       const int kpos0 = page * BS + 4 * g;  // key position of accumulator element 0
-      // V^T as bf16: the page registers themselves, or an fp8 page's conversion.
+      // fp8 pages take P V in fp16, one v_mfma_f32_16x16x16_f16 per tile pair
+      // and no hi/lo split: the V scale is sv = vf 2^a with a = floor(log2 sv)
+      // clamped to [-15, 7], V^T is fp16 codes x 2^a (exact: the conversion
+      // applies the exponent of its scale operand, 448 2^7 < 65504 and every
+      // product is a multiple of 2^-24), P is fp16 P vf. vf is in [1, 2) for
+      // sv in [2^-15, 2^8), so P vf < 2^kSlack 2 = 512. Outside that range the
+      // power of two 2^c of vf (c >= -24) is taken out of P and applied to O
+      // around the page's products (O x 2^-c before, x 2^c after: exact), so
+      // P vf stays in fp16's normal range; an all-zero block (sv = 0) has
+      // P vf = 0. bf16 pages, and fp8 pages in the
+      // head_dim-128 kernels with four query tiles (no register to spare),
+      // take P V in bf16 hi + lo.
+      constexpr bool h16 = kFp8 && !(NT == 4 && D == 128);
+      float vf = 1.f, vsc = 1.f;
+      int vc = 0;
+      if constexpr (h16) {
+        const int a = min(max((int)((__builtin_bit_cast(uint32_t, sv) >> 23) & 255u) - 127, -15), 7);
+        vsc = __builtin_bit_cast(float, (uint32_t)(a + 127) << 23);
+        vf = sv * __builtin_bit_cast(float, (uint32_t)(127 - a) << 23);
+        if (vf != 0.f && (vf >= 2.f || vf < 1.f)) {  // sv >= 2^8 or sv < 2^-15
+          vc = max((int)((__builtin_bit_cast(uint32_t, vf) >> 23) & 255u) - 127, -24);
+          vf *= __builtin_bit_cast(float, (uint32_t)(127 - vc) << 23);
+        }
+      }
+      // V^T as 16-bit values: the page registers themselves, or an fp8 page's
+      // conversion (fp16 or bf16, as above).
       uint2 vb8[kFp8 ? MT : 1];
       auto vfrag = [&](int mt) -> uint2& {
         if constexpr (kFp8) return vb8[mt];
         else return f.v[mt];
       };
       if constexpr (kFp8) {
+        if constexpr (h16) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) vb8[mt] = v_frag<D>(f, mt);
+          for (int mt = 0; mt < MT; ++mt)
+            vb8[mt] = make_uint2(fp8x2_to_f16x2<false>(f.v[mt], vsc), fp8x2_to_f16x2<true>(f.v[mt], vsc));
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) vb8[mt] = v_frag<D>(f, mt);
+        }
       }
       if (page * BS + BS > L) {
         // Keys at or beyond L are stale pool contents: zero their V.
@@ -941,8 +989,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       // meets its V (the row sums take P itself).
       float spage = sl2, vscale = 1.f;
       if constexpr (kFp8) {
-        spage = sl2 * f.sk;
-        vscale = f.sv;
+        spage = sl2 * sk;
+        vscale = h16 ? vf : sv;
       }
       // The query fragments (B operand: row 16 nt + i16, dims 32 ks + 8 g .. + 7)
       // are re-read from LDS for every page at head_dim 128 instead of being
@@ -1013,11 +1061,10 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
           m[nt] = m_new;
         }
       }
-      bf16x8_t pf[NT];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
+      // P = 2^(s - m) (times the page's V factor) per query tile; the row sums
+      // take 2^(s - m) itself.
+      auto p_tile = [&](int nt, float (&e)[4]) {
         const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
-        float e[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           if constexpr (kLean) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[nt][jj], spage, -mu));
@@ -1028,23 +1075,60 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) e[jj] *= vscale;
         }
-        // P = hi + lo, both bf16: slots 0..3 carry hi, 4..7 lo of the same keys,
-        // so one 16x16x32 MFMA against {V, V} accumulates P V to ~16 bits.
-        const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
-        const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
-        const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
-        const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
-        pf[nt] = __builtin_bit_cast(
-            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
-                                 pack2_bf16(r01[0], r01[1]), pack2_bf16(r23[0], r23[1])));
-      }
+      };
+      if constexpr (h16) {
+        const float o_down = __builtin_bit_cast(float, (uint32_t)(127 - vc) << 23);
+        if (vc) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        // {V^T, V^T}: the same keys in both halves of the k-slots.
-        const uint2 vv = vfrag(mt);
-        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(vv.x, vv.y, vv.x, vv.y));
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[nt], o[mt][nt], 0, 0, 0);
+            for (int nt = 0; nt < NT; ++nt) o[mt][nt] *= o_down;
+        }
+        // P as fp16 (16x16x16: lane l holds keys 4 (l / 16) .. + 3 of column
+        // l % 16, the accumulator layout of S^T; V^T the same keys of dim l % 16).
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float e[4];
+          p_tile(nt, e);
+          const f16x4_t pv = __builtin_bit_cast(
+              f16x4_t, make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{e[0], e[1]}, f16x2_t)),
+                                  __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{e[2], e[3]}, f16x2_t))));
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, vfrag(mt)), pv, o[mt][nt], 0, 0, 0);
+        }
+        if (vc) {
+          const float o_up = __builtin_bit_cast(float, (uint32_t)(127 + vc) << 23);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) o[mt][nt] *= o_up;
+        }
+      } else {
+        bf16x8_t pf[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float e[4];
+          p_tile(nt, e);
+          // P = hi + lo, both bf16: slots 0..3 carry hi, 4..7 lo of the same keys,
+          // so one 16x16x32 MFMA against {V, V} accumulates P V to ~16 bits.
+          const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
+          const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
+          const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
+          const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
+          pf[nt] = __builtin_bit_cast(
+              bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
+                                   pack2_bf16(r01[0], r01[1]), pack2_bf16(r23[0], r23[1])));
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          // {V^T, V^T}: the same keys in both halves of the k-slots.
+          const uint2 vv = vfrag(mt);
+          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(vv.x, vv.y, vv.x, vv.y));
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[nt], o[mt][nt], 0, 0, 0);
+        }
       }
     };
 
@@ -1057,6 +1141,29 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       }
       const int pg0 = tab0 + w, last = wend - 1;
       const int n = pg0 < wend ? (last - pg0) / NWV + 1 : 0;  // this wave's pages in the window
+      // The wave's block ids of the window, one per lane: lane s holds page
+      // min(pg0 + NWV s, last) (a window of kTabChunk pages gives each of the
+      // NWV waves at most 64), so a page's id is a readlane. (An LDS read per
+      // page needs an address register, which the allocator takes from a
+      // page buffer still being loaded: the wait for it drained the ring.)
+      // An fp8 page's two scales come the same way (lane s: page s's K and V
+      // scales), so a page's loads are its six buffer loads only. The
+      // head_dim-128 kernels with four query tiles, or three without a plan,
+      // read the id from LDS per page (and an fp8 page's scales with its
+      // codes): the extra registers make them spill.
+      static_assert(kTabChunk <= 64 * NWV, "a wave's pages of a window fit its lanes");
+      int wid = 0;
+      float2 wsc = make_float2(0.f, 0.f);
+      if constexpr (kLaneIds) wid = sTab[min(pg0 + NWV * lane, last) - tab0];
+      if constexpr (kFp8 && kLaneIds)
+        wsc = *reinterpret_cast<const float2*>(p.scales + ((size_t)p.layer * p.cap + wid) * 2);
+      auto lane_f = [&](float v, int s) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), s));
+      };
+      auto load_slot = [&](PageRegs<D, KT>& f, int s) {
+        if constexpr (kLaneIds) load_page_phys(f, __builtin_amdgcn_readlane(wid, min(s, 63)));
+        else load_page_phys(f, uni(sTab[min(pg0 + NWV * s, last) - tab0]));
+      };
       // Every load is issued unconditionally (past the end it re-reads the
       // window's last page): the number of loads in flight is then the same on
       // every path, so each page waits only for its own loads (vmcnt(N)), not
@@ -1064,15 +1171,20 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       // (a planned call's first window: its first page is already in flight)
       if (!(first && tab0 == lp0)) {
 #pragma unroll
-        for (int u = 0; u < kRing - 1; ++u) load_page(buf[u], min(pg0 + NWV * u, last));
+        for (int u = 0; u < kRing - 1; ++u) load_slot(buf[u], u);
+      } else {
+        // buf[0] holds the first page already; the rest of the ring follows
+#pragma unroll
+        for (int u = 1; u < kRing - 1; ++u) load_slot(buf[u], u);
       }
       for (int it = 0; it < n; it += kRing) {
 #pragma unroll
         for (int u = 0; u < kRing; ++u) {
           const int s = it + u;
           if (s >= n) break;
-          load_page(buf[(u + kRing - 1) % kRing], min(pg0 + NWV * (s + kRing - 1), last));
-          compute_page(buf[u], pg0 + NWV * s);
+          load_slot(buf[(u + kRing - 1) % kRing], s + kRing - 1);
+          if constexpr (kLaneIds || !kFp8) compute_page(buf[u], pg0 + NWV * s, lane_f(wsc.x, s), lane_f(wsc.y, s));
+          else compute_page(buf[u], pg0 + NWV * s, uni_f(buf[u].sk), uni_f(buf[u].sv));
         }
       }
     }

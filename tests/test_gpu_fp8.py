@@ -214,3 +214,53 @@ def test_fp8_mfma_attention_matches_oracle(cuda, Hq, H, d, C, lens):
     out = verify_attention(q.to(cuda), gpu, 0, sids, lens, max(lens) + C).float().cpu()
     want = ref_attn.paged_attention_extend(q.float(), cpu.dequantized(), 0, sids, lens, Hq)
     _bf16_check(out, want)
+
+
+def _fp8_pool_scaled(cuda, lens, H, d, C, v_mag, seed):
+    """An fp8 pool whose V rows of sequence s are N(0, 1) times v_mag(s, pos):
+    the block scales (amax / 448) then cover zero, tiny and huge values."""
+    cap = sum(-(-(L + C) // 16) for L in lens) + 4
+    gpu = PagedKVCache(1, H, d, cap, 16, cuda, FP8, max_seqs=len(lens))
+    cpu = Fp8PagedKVCache(1, H, d, cap, 16)
+    g = torch.Generator().manual_seed(seed)
+    for s, L in enumerate(lens):
+        gpu.add_sequence(s)
+        cpu.add_sequence(s)
+        k = torch.randn(1, L + C, H, d, generator=g)
+        mag = torch.tensor([v_mag(s, p) for p in range(L + C)], dtype=torch.float32).view(1, L + C, 1, 1)
+        v = torch.randn(1, L + C, H, d, generator=g) * mag
+        k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+        gpu.write_block(0, [s], [0], k.to(cuda), v.to(cuda))
+        cpu.write_block(0, [s], [0], k, v)
+    return gpu, cpu, g
+
+
+@pytest.mark.parametrize("d,Hq,C", [(64, 14, 9), (128, 12, 6), (64, 14, 1), (128, 16, 7)])
+def test_fp8_attention_over_extreme_v_scales(cuda, d, Hq, C):
+    """V block scales of every class the fp16 P V path distinguishes: tiny
+    (below 2^-15: V amax ~1e-4 and ~1e-7), zero (all-zero V blocks), ordinary,
+    huge (2^8 and above: V amax ~1e6 and ~3e9, where O is rescaled around the
+    page), and all of them mixed block by block within one sequence. Compared
+    with the oracle on the dequantised K/V at the bf16 bar."""
+    mags = [1e-4, 0.0, 1.0, 1e6, 3e9, 1e-7]
+
+    def v_mag(s, p):
+        if s < len(mags):
+            return mags[s]
+        return mags[(p // 16 + s) % len(mags)]  # mixed: the class changes every block
+
+    lens = [700, 333, 1500, 64, 900, 2100, 1234, 3000]
+    gpu, cpu, g = _fp8_pool_scaled(cuda, lens, 2, d, C, v_mag, seed=d + C)
+    scales_v = gpu.scales[0, :, 1].cpu()
+    assert float(scales_v.max()) >= 2.0 ** 8 and float(scales_v[scales_v > 0].min()) < 2.0 ** -15
+    assert bool((scales_v == 0).any())
+    q = torch.randn(len(lens), C, Hq, d, generator=g).to(torch.bfloat16)
+    sids = list(range(len(lens)))
+    out = verify_attention(q.to(cuda), gpu, 0, sids, [L for L in lens], max(lens) + C).float().cpu()
+    want = ref_attn.paged_attention_extend(q.float(), cpu.dequantized(), 0, sids, lens, Hq)
+    assert torch.isfinite(out).all()
+    for b in range(len(lens)):
+        if float(want[b].abs().max()) == 0.0:  # all-zero V: the output is exactly zero
+            assert float(out[b].abs().max()) == 0.0, b
+        else:
+            _bf16_check(out[b:b + 1], want[b:b + 1])
