@@ -446,6 +446,7 @@ FD_CTX = (512, 8192)          # prompt lengths, log-uniform
 FD_BUDGET = (32, 160)         # new tokens per request, uniform
 FD_RATE = 4.0                 # Poisson arrivals per step once the first batch is in
 FD_SIGMA = 1.05               # draft = target + N(0, sigma^2): acceptance ~0.6 per draft
+FD_BREAKDOWN_ROUNDS = 3       # rounds with events around every layer's append and attention
 
 
 def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
@@ -457,14 +458,18 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
     tokens in each of 36 layers, runs 36 verify attentions, the fused sampling
     and the rewind (``engine.continuous``). Rounds are timed on the host
     (device drained before each, one synchronisation at its end) and on the
-    device with events around every layer's append and attention.
+    device with events around the round only; FD_BREAKDOWN_ROUNDS further
+    rounds record events around every layer's append and attention for the
+    per-layer figures (those events add their own gaps between the kernels:
+    about 330 us per round of 36 layers, so they are kept out of the round
+    times).
     """
     import statistics
 
     import torch
 
     from engine.continuous import SpecContinuousDriver, SyntheticVerifyModel, poisson_requests
-    from engine.kv import PagedKVCache
+    from engine.kv import PagedKVCache, WritePlan
     from engine.scheduler import blocks_for_hbm, bytes_per_block
 
     chunk = FD_GAMMA + 1
@@ -477,7 +482,7 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
     cap = blocks_for_hbm(FD_LAYERS, FD_BS, FD_HKV, FD_D, torch.bfloat16, dev, reserve_bytes=0,
                          fraction=pool_frac)
     maxb = -(-(FD_CTX[1] + FD_BUDGET[1] + chunk) // FD_BS) + 1
-    n_req = FD_BATCH + int(FD_RATE * (rounds + warmup)) + 16
+    n_req = FD_BATCH + int(FD_RATE * (rounds + warmup + FD_BREAKDOWN_ROUNDS)) + 16
     kv = PagedKVCache(FD_LAYERS, FD_HKV, FD_D, cap, FD_BS, dev, torch.bfloat16, max_seqs=n_req,
                       max_blocks_per_seq=maxb)
     g = torch.Generator().manual_seed(seed + 1)
@@ -494,17 +499,29 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
                           "attn_bytes": attention_bytes(info.starts, chunk, FD_HQ, FD_HKV, FD_D, FD_BS),
                           "ctx": sum(info.starts) / n, "k": info.result.n_commit.tolist()})
 
-    res = drv.run(first + stream, max_steps=rounds + warmup, on_round=on_round, sync_timing=True,
-                  gpu_timing=True)
+    res = drv.run(first + stream, max_steps=rounds + warmup + FD_BREAKDOWN_ROUNDS, on_round=on_round,
+                  sync_timing=True, gpu_timing=lambda step: "round" if step < warmup + rounds else "layers")
     torch.cuda.synchronize()
-    timed = per_round[warmup:]
+    timed = per_round[warmup:warmup + rounds]
+    brk = per_round[warmup + rounds:]
     med = statistics.median
     host_us = med(r["host_s"] for r in timed) * 1e6
     gpu_us = med(r["gpu"]["round"] for r in timed) * 1e3
-    attend_ms = sum(r["gpu"]["attend"] for r in timed)
-    attn_gbs = sum(r["attn_bytes"] for r in timed) * FD_LAYERS / (attend_ms * 1e-3) / 1e9
+    attend_ms = sum(r["gpu"]["attend"] for r in brk)
+    attn_gbs = sum(r["attn_bytes"] for r in brk) * FD_LAYERS / (attend_ms * 1e-3) / 1e9
     ks = [k for r in timed for k in r["k"]]
     batch = sum(r["batch"] for r in timed) / len(timed)
+    # A later layer's append alone: the write plan recorded by a first layer's
+    # append of the running sequences' next chunk, then the 35 later layers'
+    # planned copies replayed as a graph (no event between them).
+    sid_t = torch.tensor([q.sid for q in drv.running], dtype=torch.int32, device=dev)
+    st_t = torch.tensor([q.length for q in drv.running], dtype=torch.int32, device=dev)
+    kn = torch.randn(len(drv.running), chunk, FD_HKV, FD_D, device=dev).to(torch.bfloat16)
+    wplan = WritePlan()
+    kv.write_block_device(0, sid_t, st_t, kn, kn, alloc=True, plan=wplan)
+    gw = graph_of(lambda: [kv.write_block_device(layer, sid_t, st_t, kn, kn, alloc=False, plan=wplan)
+                           for layer in range(1, FD_LAYERS)], 1, torch)
+    planned_us = time_graph(gw, 5, torch) * 1e3 / (FD_LAYERS - 1)
     out = {
         "workload": "Qwen2.5-3B-shaped continuous batching: {} layers, {}q/{}kv heads, head_dim {}, "
                     "block {}, bf16 KV, gamma {}, batch cap {}, prompts log-U[{},{}], budgets U[{},{}], "
@@ -520,9 +537,11 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
         "us_per_seq": round(host_us / batch, 3),
         "gpu_us_per_round": round(gpu_us, 1),
         "gpu_us_per_seq": round(gpu_us / batch, 3),
-        "attend_us_per_layer": round(med(r["gpu"]["attend"] for r in timed) * 1e3 / FD_LAYERS, 2),
-        "append_us_per_layer": round(med(r["gpu"]["append"] for r in timed) * 1e3 / FD_LAYERS, 2),
-        "sample_rewind_us": round(med(r["gpu"]["sample"] for r in timed) * 1e3, 1),
+        "breakdown_rounds": len(brk),
+        "attend_us_per_layer": round(med(r["gpu"]["attend"] for r in brk) * 1e3 / FD_LAYERS, 2),
+        "append_us_per_layer": round(med(r["gpu"]["append"] for r in brk) * 1e3 / FD_LAYERS, 2),
+        "sample_rewind_us": round(med(r["gpu"]["sample"] for r in brk) * 1e3, 1),
+        "append_planned_us": round(planned_us, 2),
         "attn_gbs": round(attn_gbs, 1),
         "mean_commit_per_seq_round": round(sum(ks) / len(ks), 3),
         "mean_acceptance": round(sum(ks) / len(ks) / chunk, 4),

@@ -105,6 +105,39 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype,
                   int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
                   int32_t may_alloc, int32_t write_limit_b, void* stream);
 
+/* spv_kv_append that also records the round's write plan: write_plan (B x C
+ * int32, device) receives for chunk token j of entry b the pool row
+ * phys * block_size + (start_b + j) % block_size it was written to, or -1 where
+ * nothing was written (the write limit, the entry's blocks, an out-of-pool id).
+ * The plan then serves the same chunk's appends into the round's later layers
+ * (spv_kv_write_planned): the loop of engine/model.py:184-187 runs once per
+ * layer over the same positions, and only its first layer allocates
+ * (kv.py:119-147). No reference counterpart for the plan itself.
+ * Requires capacity * block_size < 2^31. */
+int spv_kv_append_plan(void* k_pool, void* v_pool, int kv_dtype,
+                       const void* k_new, const void* v_new,
+                       int32_t* block_tables, int32_t max_blocks_per_seq,
+                       int32_t* num_blocks, int32_t* seq_lens,
+                       int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                       const int32_t* seq_ids, const int32_t* start_pos,
+                       int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                       int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t may_alloc, int32_t write_limit_b, int32_t* write_plan,
+                       void* stream);
+
+/* PagedKVCache.write (engine/kv.py:125-147) of a chunk into a later layer of
+ * its round by the write plan of the round's first layer (spv_kv_append_plan):
+ * k_new/v_new (B, C, Hkv, d) in kv_dtype (not fp8) go to the planned rows of
+ * `layer`; no table, block count, length or counter is read or written, so the
+ * result equals spv_kv_append with may_alloc = 0 and write_limit_b = -1 on the
+ * state the plan was made from. C <= 64, head_dim * element size a multiple
+ * of 16 bytes and C * head_dim * element size <= 16 KB. */
+int spv_kv_write_planned(void* k_pool, void* v_pool, int kv_dtype,
+                         const void* k_new, const void* v_new, const int32_t* write_plan,
+                         int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                         int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                         void* stream);
+
 /* spv_kv_append for an fp8 (OCP e4m3, SPV_FP8E4M3) pool with one fp32 scale
  * per (layer, block, K | V): kv_scales is [num_layers][capacity][2] (K, V), a
  * stored code q meaning q * scale. The reference pool has no fp8 storage

@@ -259,7 +259,8 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
     const uint8_t* __restrict__ vnew, int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
     int32_t* __restrict__ seq_lens, const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
     int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start,
-    int32_t B, int32_t C, int32_t layer, int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t limit_b) {
+    int32_t B, int32_t C, int32_t layer, int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t limit_b,
+    int32_t* __restrict__ wplan) {
   using T = typename Elem<ES>::T;
   __shared__ int s_scan[kFusedThreads / 64];
   __shared__ int s_free[kFusedStage];
@@ -350,6 +351,16 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
   // only the tokens whose block exists.
   const int lim = limit_b >= 0 ? limit_b : (fail < B ? fail : 0x7fffffff);
   const int n = (b > lim || s0 < 0) ? 0 : min(C, nb_new * bs - s0);
+  if (wplan && h == 0) {  // the round's write plan: slot row of each chunk token, or -1
+    for (int o = threadIdx.x; o < C; o += kFusedThreads) {
+      int dest = -1;
+      if (o < n) {
+        const int p = s0 + o, phys = s_phys[p / bs - blk0];
+        if ((unsigned)phys < (unsigned)cap) dest = phys * bs + p % bs;
+      }
+      wplan[(size_t)b * C + o] = dest;
+    }
+  }
   if (n > 0) {
     if (h == 0 && threadIdx.x == 0 && seq_lens[sid] < s0 + n) seq_lens[sid] = s0 + n;
     // One pass (the host launches this kernel only when the chunk's K pieces
@@ -388,6 +399,90 @@ __global__ __launch_bounds__(kFusedThreads) void kv_append_fused_kernel(
       ctr[CTR_TOP] = top - consumed;
       ctr[CTR_EXHAUSTED] = fail < B ? fail + 1 : 0;
       if (ovf < B) ctr[CTR_OVERFLOW] = ovf + 1;
+    }
+  }
+}
+
+// The round's write plan after an allocation by kv_alloc_kernel: for chunk
+// token o of entry b, the pool row phys * bs + (p % bs) that kv_write_kernel
+// writes it to (p = start + o), or -1 where it writes nothing (past an
+// exhausted pool's cut, past the entry's blocks, or an out-of-pool id). The
+// rule is kv_write_kernel's. One thread per (entry, token).
+__global__ void kv_write_plan_kernel(const int32_t* __restrict__ tables, int32_t maxb,
+                                     const int32_t* __restrict__ nblocks, const int32_t* __restrict__ seq_ids,
+                                     const int32_t* __restrict__ start, const int32_t* __restrict__ ctr,
+                                     int32_t limit_b, int32_t B, int32_t C, int32_t bs, int32_t cap,
+                                     int32_t* __restrict__ wplan) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * C) return;
+  const int b = i / C, o = i - b * C;
+  const int sid = seq_ids[b], s0 = start[b];
+  const int lim = limit_b >= 0 ? limit_b : (ctr[CTR_EXHAUSTED] ? ctr[CTR_EXHAUSTED] - 1 : 0x7fffffff);
+  const int n = (b > lim || s0 < 0) ? 0 : min(C, nblocks[sid] * bs - s0);
+  int dest = -1;
+  if (o < n) {
+    const int p = s0 + o;
+    const int phys = tables[(size_t)sid * maxb + min(p / bs, maxb - 1)];
+    if ((unsigned)phys < (unsigned)cap) dest = phys * bs + p % bs;
+  }
+  wplan[i] = dest;
+}
+
+// A later layer's append of the round's chunk by its write plan (no table,
+// block count or length is read: the first layer's append allocated and
+// recorded every token's row). One workgroup per (entry, kv head): the plan
+// entries, the K pieces and the V pieces are loaded in one round trip (V rows
+// go to LDS), then K rows are stored as 16-byte pieces and V^T elements with
+// the chunk's tokens fastest across lanes, so a wave's stores to one dim's row
+// of the transposed page are contiguous.
+constexpr int kPlannedThreads = 256;
+constexpr int kPlannedItems = 4;                 // 16-byte pieces per thread for K, and for V
+constexpr int kPlannedMaxC = 64;                 // chunk tokens
+template <int ES>
+__global__ __launch_bounds__(kPlannedThreads) void kv_write_planned_kernel(
+    uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool, const uint8_t* __restrict__ knew,
+    const uint8_t* __restrict__ vnew, const int32_t* __restrict__ wplan, int32_t C, int32_t layer, int32_t cap,
+    int32_t bs, int32_t hkv, int32_t d) {
+  using T = typename Elem<ES>::T;
+  extern __shared__ __align__(16) uint8_t s_v[];  // the chunk's V rows of this head, C x d elements
+  __shared__ int s_dest[kPlannedMaxC];
+  const int b = blockIdx.x / hkv, h = blockIdx.x - b * hkv;
+  const size_t row_elems = (size_t)hkv * d;
+  const int vec = (d * ES) >> 4;  // 16-byte pieces of one row
+  const int np = C * vec;         // pieces of the chunk's K (and of its V)
+  uint4 kreg[kPlannedItems], vreg[kPlannedItems];
+#pragma unroll
+  for (int k = 0; k < kPlannedItems; ++k) {
+    const int ip = min((int)threadIdx.x + k * kPlannedThreads, np - 1);
+    const size_t src = (((size_t)b * C + ip / vec) * row_elems + (size_t)h * d) * ES;
+    kreg[k] = reinterpret_cast<const uint4*>(knew + src)[ip % vec];
+    vreg[k] = reinterpret_cast<const uint4*>(vnew + src)[ip % vec];
+  }
+  if ((int)threadIdx.x < C) s_dest[threadIdx.x] = wplan[(size_t)b * C + threadIdx.x];
+#pragma unroll
+  for (int k = 0; k < kPlannedItems; ++k) {
+    const int ip = (int)threadIdx.x + k * kPlannedThreads;
+    if (ip < np) reinterpret_cast<uint4*>(s_v)[ip] = vreg[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPlannedItems; ++k) {
+    const int ip = (int)threadIdx.x + k * kPlannedThreads;
+    if (ip < np) {
+      const int dest = s_dest[ip / vec];
+      if (dest >= 0) {
+        const size_t slot = ((size_t)layer * cap + dest / bs) * hkv + h;
+        reinterpret_cast<uint4*>(kpool + (slot * bs + dest % bs) * (size_t)(d * ES))[ip % vec] = kreg[k];
+      }
+    }
+  }
+  const T* sv = reinterpret_cast<const T*>(s_v);
+  for (int iv = threadIdx.x; iv < C * d; iv += kPlannedThreads) {
+    const int e = iv / C, o = iv - e * C;  // tokens fastest
+    const int dest = s_dest[o];
+    if (dest >= 0) {
+      T* vdst = reinterpret_cast<T*>(vpool) + (((size_t)layer * cap + dest / bs) * hkv + h) * (size_t)d * bs;
+      vdst[(size_t)e * bs + dest % bs] = sv[o * d + e];
     }
   }
 }
@@ -1213,12 +1308,17 @@ int spv_pool_free_one(int32_t* free_stack, int32_t* free_flag, int32_t* ctr, int
   return SPV_OK;
 }
 
-int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, const void* v_new,
-                  int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
-                  int32_t* free_stack, int32_t* free_flag, int32_t* ctr, const int32_t* seq_ids,
-                  const int32_t* start_pos, int32_t B, int32_t C, int32_t layer, int32_t capacity,
-                  int32_t block_size, int32_t num_kv_heads, int32_t head_dim, int32_t may_alloc,
-                  int32_t write_limit_b, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// spv_kv_append, and with write_plan (B x C int32) the round's write plan.
+int kv_append_impl(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, const void* v_new,
+                   int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
+                   int32_t* free_stack, int32_t* free_flag, int32_t* ctr, const int32_t* seq_ids,
+                   const int32_t* start_pos, int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                   int32_t block_size, int32_t num_kv_heads, int32_t head_dim, int32_t may_alloc,
+                   int32_t write_limit_b, int32_t* write_plan, void* stream) {
   const int es = dtype_size(kv_dtype);
   const bool alloc_only = !k_new && !v_new;
   if (!k_pool || !v_pool || (!alloc_only && (!k_new || !v_new)) || !block_tables || !num_blocks || !seq_lens ||
@@ -1243,7 +1343,8 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
 #define SPV_FUSED(ES)                                                                                           \
   hipLaunchKernelGGL(kv_append_fused_kernel<ES>, dim3(B * num_kv_heads), dim3(kFusedThreads), 0, s, kp, vp, kn,  \
                      vn, block_tables, max_blocks_per_seq, num_blocks, seq_lens, free_stack, free_flag, ctr,      \
-                     seq_ids, start_pos, B, C, layer, capacity, block_size, num_kv_heads, head_dim, write_limit_b)
+                     seq_ids, start_pos, B, C, layer, capacity, block_size, num_kv_heads, head_dim, write_limit_b,  \
+                     write_plan)
     if (es == 4) SPV_FUSED(4);
     else SPV_FUSED(2);
 #undef SPV_FUSED
@@ -1255,6 +1356,12 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
     hipLaunchKernelGGL(kv_alloc_kernel, dim3(1), dim3(kPoolThreads), 0, s, block_tables, max_blocks_per_seq,
                        num_blocks, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, block_size, nullptr, 0,
                        capacity);
+    SPV_CHECK_LAUNCH();
+  }
+  if (write_plan) {
+    hipLaunchKernelGGL(kv_write_plan_kernel, dim3((B * C + 255) / 256), dim3(256), 0, s, block_tables,
+                       max_blocks_per_seq, num_blocks, seq_ids, start_pos, ctr, write_limit_b, B, C, block_size,
+                       capacity, write_plan);
     SPV_CHECK_LAUNCH();
   }
   if (alloc_only) return SPV_OK;
@@ -1276,6 +1383,61 @@ int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, c
     else SPV_WRITE(kv_write_small_kernel<2>);
   }
 #undef SPV_WRITE
+  SPV_CHECK_LAUNCH();
+  return SPV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int spv_kv_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, const void* v_new,
+                  int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
+                  int32_t* free_stack, int32_t* free_flag, int32_t* ctr, const int32_t* seq_ids,
+                  const int32_t* start_pos, int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                  int32_t block_size, int32_t num_kv_heads, int32_t head_dim, int32_t may_alloc,
+                  int32_t write_limit_b, void* stream) {
+  return kv_append_impl(k_pool, v_pool, kv_dtype, k_new, v_new, block_tables, max_blocks_per_seq, num_blocks,
+                        seq_lens, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, layer, capacity, block_size,
+                        num_kv_heads, head_dim, may_alloc, write_limit_b, nullptr, stream);
+}
+
+int spv_kv_append_plan(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, const void* v_new,
+                       int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
+                       int32_t* free_stack, int32_t* free_flag, int32_t* ctr, const int32_t* seq_ids,
+                       const int32_t* start_pos, int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                       int32_t block_size, int32_t num_kv_heads, int32_t head_dim, int32_t may_alloc,
+                       int32_t write_limit_b, int32_t* write_plan, void* stream) {
+  if (!write_plan || (long long)capacity * block_size > 0x7fffffffLL) return SPV_ERR_ARG;  // int32 plan rows
+  return kv_append_impl(k_pool, v_pool, kv_dtype, k_new, v_new, block_tables, max_blocks_per_seq, num_blocks,
+                        seq_lens, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, layer, capacity, block_size,
+                        num_kv_heads, head_dim, may_alloc, write_limit_b, write_plan, stream);
+}
+
+int spv_kv_write_planned(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, const void* v_new,
+                         const int32_t* write_plan, int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                         int32_t block_size, int32_t num_kv_heads, int32_t head_dim, void* stream) {
+  const int es = dtype_size(kv_dtype);
+  if (!k_pool || !v_pool || !k_new || !v_new || !write_plan || es == 0 || kv_dtype == SPV_FP8E4M3)
+    return SPV_ERR_ARG;
+  if (B < 0 || B > 65535 || C < 1 || C > kPlannedMaxC || layer < 0 || capacity < 1 || block_size < 1 ||
+      num_kv_heads < 1 || head_dim < 1 || (head_dim * es) % 16 ||
+      C * (head_dim * es / 16) > kPlannedItems * kPlannedThreads)
+    return SPV_ERR_ARG;
+  if ((long long)capacity * block_size > 0x7fffffffLL) return SPV_ERR_ARG;  // plan entries are int32 rows
+  if (B == 0) return SPV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t smem = (size_t)C * head_dim * es;
+  auto* kp = static_cast<uint8_t*>(k_pool);
+  auto* vp = static_cast<uint8_t*>(v_pool);
+  auto* kn = static_cast<const uint8_t*>(k_new);
+  auto* vn = static_cast<const uint8_t*>(v_new);
+  if (es == 4)
+    hipLaunchKernelGGL(kv_write_planned_kernel<4>, dim3(B * num_kv_heads), dim3(kPlannedThreads), smem, s, kp, vp,
+                       kn, vn, write_plan, C, layer, capacity, block_size, num_kv_heads, head_dim);
+  else
+    hipLaunchKernelGGL(kv_write_planned_kernel<2>, dim3(B * num_kv_heads), dim3(kPlannedThreads), smem, s, kp, vp,
+                       kn, vn, write_plan, C, layer, capacity, block_size, num_kv_heads, head_dim);
   SPV_CHECK_LAUNCH();
   return SPV_OK;
 }

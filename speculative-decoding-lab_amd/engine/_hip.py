@@ -49,6 +49,8 @@ SIGNATURES = {
     "spv_pool_alloc_one": (I, [P, P, P, I, P, P]),
     "spv_pool_free_one": (I, [P, P, P, I, I, P, P]),
     "spv_kv_append": (I, [P, P, I, P, P, P, I, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
+    "spv_kv_append_plan": (I, [P, P, I, P, P, P, I, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, P, P]),
+    "spv_kv_write_planned": (I, [P, P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "spv_kv_append_fp8": (I, [P, P, P, I, P, P, P, I, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "spv_kv_rewind": (I, [P, I, P, P, P, P, P, P, P, P, I, I, I, I, P]),
     "spv_kv_draft_align": (I, [P, I, P, P, P, P, P, P, I, P, P, P, P, P, I, P, P, P, I, I, I, P]),

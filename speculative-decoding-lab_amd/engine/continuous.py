@@ -281,7 +281,7 @@ class SpecContinuousDriver:
 
     # ---------------------------------------------------------------- round
     def _round(self, step: int, result: DriverResult, on_round: Optional[Callable[[RoundInfo], None]],
-               sync_timing: bool, gpu_timing: bool) -> None:
+               sync_timing: bool, gpu_timing) -> None:
         running = self.running
         sids = [s.sid for s in running]
         starts = [s.length for s in running]
@@ -292,7 +292,12 @@ class SpecContinuousDriver:
         if sync_timing:
             torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
-        evs = [] if gpu_timing else None
+        per_layer = gpu_timing is True or gpu_timing == "layers"
+        evs = [] if per_layer else None
+        round_evs = None
+        if gpu_timing == "round":  # the round's span only: no event between its kernels
+            round_evs = [torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+            round_evs[0].record()
         sid_t = _hip.i32(sids, dev)
         st_t = _hip.i32(starts, dev)
         d_outs = cu = None
@@ -316,9 +321,11 @@ class SpecContinuousDriver:
             cu = align_draft(self.draft_kv, sid_t, st_t, res, chunk)
             last = res.out_tokens.gather(1, (res.n_commit.long() - 1).clamp(min=0).unsqueeze(1)).squeeze(1)
             self._pending[sid_l] = torch.where(res.n_commit > 0, last, pending)
-        if gpu_timing:
+        if per_layer:
             evs.append(torch.cuda.Event(enable_timing=True))
             evs[-1].record()
+        if round_evs is not None:
+            round_evs[1].record()
         # the round's one host synchronisation
         counts = [res.n_commit, res.finished] + ([cu.count] if cu is not None else [])
         host = torch.stack(counts).tolist()
@@ -328,7 +335,11 @@ class SpecContinuousDriver:
             cu_outs, cu_rows = self._catch_up(cu, host[2], sids, inp, result)
         dt = time.perf_counter() - t0
         gms = None
-        if gpu_timing:
+        if round_evs is not None:
+            torch.cuda.synchronize(dev)
+            gms = {"round": round_evs[0].elapsed_time(round_evs[1])}
+            result.gpu_ms.append(gms)
+        elif per_layer:
             torch.cuda.synchronize(dev)
             nl = len(inp["q"])
             gms = {"append": sum(evs[2 * i].elapsed_time(evs[2 * i + 1]) for i in range(nl)),
@@ -405,16 +416,18 @@ class SpecContinuousDriver:
 
     def run(self, requests: Sequence[Request], max_steps: Optional[int] = None,
             on_round: Optional[Callable[[RoundInfo], None]] = None, sync_timing: bool = False,
-            gpu_timing: bool = False) -> DriverResult:
+            gpu_timing=False) -> DriverResult:
         """Steps until every request has finished (or ``max_steps``), in the
         reference's order (spec_scheduler.py:181-208): admit the requests due at
         step 0; then per step run a round over the running sequences, advance
         the step, admit the requests due by then, and record the metrics.
 
         ``sync_timing`` drains the device before each round so that
-        ``round_seconds`` holds the round alone; ``gpu_timing`` records events
-        around every layer's append and attention and around the sampling
-        (``gpu_ms`` per round, in ms)."""
+        ``round_seconds`` holds the round alone; ``gpu_timing`` True (or
+        "layers") records events around every layer's append and attention and
+        around the sampling (``gpu_ms`` per round, in ms; the events add their
+        own gaps between the kernels), "round" only around the round. A
+        callable gives the mode per step."""
         result = DriverResult(self.gamma)
         self._nrec = 0
         self._peak.zero_()
@@ -426,7 +439,8 @@ class SpecContinuousDriver:
         waiting = self._flush_arrivals(due, result) if due else []
         while self.running or pending or waiting:
             if self.running:
-                self._round(step, result, on_round, sync_timing, gpu_timing)
+                self._round(step, result, on_round, sync_timing,
+                            gpu_timing(step) if callable(gpu_timing) else gpu_timing)
             step += 1
             due = waiting + [r for r in pending if r.arrive_step <= step]
             pending = [r for r in pending if r.arrive_step > step]

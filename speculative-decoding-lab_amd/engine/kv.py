@@ -330,7 +330,8 @@ class PagedKVCache:
             raise _exhausted(self.allocator.capacity)
 
     def write_block_device(self, layer: int, seq_ids: torch.Tensor, start_positions: torch.Tensor,
-                           k_new: torch.Tensor, v_new: torch.Tensor, alloc: bool = True) -> None:
+                           k_new: torch.Tensor, v_new: torch.Tensor, alloc: bool = True,
+                           plan: Optional["WritePlan"] = None) -> None:
         """``write_block`` with int32 device ``seq_ids``/``start_positions`` and no host sync.
 
         The allocation decides on the device which sequence (if any) exhausts
@@ -340,14 +341,47 @@ class PagedKVCache:
         ``max_blocks_per_seq`` blocks. ``alloc=False`` skips the allocation for
         a chunk whose blocks an earlier call allocated (the same ids and starts
         in an earlier layer) and applies that call's exhaustion verdict.
+
+        ``plan`` (a ``WritePlan``): with ``alloc`` the call records the rows of
+        the chunk's tokens into it; without, a recorded plan of the same chunk
+        replaces the table lookups (the round's later layers: one round trip,
+        ``spv_kv_write_planned``). fp8 pools, and chunks the planned copy does
+        not take, ignore it.
         """
         B, chunk = int(k_new.shape[0]), int(k_new.shape[1])
         if B == 0:
             return
         k_new, v_new = self._new_kv(k_new, v_new)
+        if plan is not None and not self.fp8 and self._plannable(chunk):
+            if alloc:
+                plan._reserve(B, chunk, self.device)
+                a = self.allocator
+                call("spv_kv_append_plan", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
+                     ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
+                     ptr(a.free_stack), ptr(a.free_flag), ptr(a.ctr), ptr(seq_ids), ptr(start_positions), B, chunk,
+                     int(layer), a.capacity, self.block_size, self.num_kv_heads, self.head_dim, 1, -1,
+                     ptr(plan.rows), self._stream())
+                plan.ready = True
+                self._stale = True
+                self.allocator._stale = True
+                return
+            if plan.ready:
+                if (B, chunk) != (plan.B, plan.C):
+                    raise ValueError("the chunk ({}, {}) does not match its write plan ({}, {})".format(
+                        B, chunk, plan.B, plan.C))
+                call("spv_kv_write_planned", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
+                     ptr(plan.rows), B, chunk, int(layer), self.allocator.capacity, self.block_size,
+                     self.num_kv_heads, self.head_dim, self._stream())
+                return
         self._launch_append(layer, seq_ids, start_positions, k_new, v_new, B, chunk, 1 if alloc else 0, -1)
         self._stale = True
         self.allocator._stale = True
+
+    def _plannable(self, chunk: int) -> bool:
+        """Whether spv_kv_write_planned takes this pool's chunks of ``chunk`` tokens."""
+        es = self.k_pool.element_size()
+        return (chunk <= 64 and (self.head_dim * es) % 16 == 0 and chunk * self.head_dim * es <= 16384
+                and self.allocator.capacity * self.block_size < 2 ** 31)
 
     def _new_kv(self, k_new: torch.Tensor, v_new: torch.Tensor):
         """New keys / values as the append takes them: the pool dtype, or for an
@@ -594,3 +628,21 @@ class PagedKVCache:
         self._lens = [int(x) for x in lengths]
         self.allocator.load_free_list(free_list)
         self._stale = False
+
+
+class WritePlan:
+    """The pool rows one round's chunk was written to by its first layer's
+    append (``write_block_device(..., alloc=True, plan=...)``), for the same
+    chunk's appends into the round's later layers. A buffer of B x C int32 on
+    the device, reused across rounds; ``ready`` once recorded."""
+
+    def __init__(self):
+        self.rows: Optional[torch.Tensor] = None
+        self.B = self.C = 0
+        self.ready = False
+
+    def _reserve(self, B: int, C: int, device) -> None:
+        if self.rows is None or self.rows.numel() < B * C or self.rows.device != device:
+            self.rows = torch.empty(max(B * C, 64), dtype=torch.int32, device=device)
+        self.B, self.C = B, C
+        self.ready = False

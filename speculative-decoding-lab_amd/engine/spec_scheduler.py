@@ -38,7 +38,7 @@ import torch
 from . import _hip
 from ._hip import call, ptr
 from .attention import VerifyPlan, verify_attention
-from .kv import PagedKVCache
+from .kv import PagedKVCache, WritePlan
 
 _workspace = _hip.Workspace()
 _draft_workspace = _hip.Workspace()
@@ -252,6 +252,7 @@ class VerifyStep:
         self.gamma = int(gamma)
         self.temperature = float(temperature)
         self.eos_id = eos_id
+        self._write_plan = WritePlan()  # the round's rows, recorded by its first layer's append
 
     def attend_layers(self, seq_ids: Sequence[int], start_positions: Sequence[int],
                       q_layers: Sequence[torch.Tensor], k_layers: Sequence[torch.Tensor],
@@ -279,8 +280,10 @@ class VerifyStep:
         for layer in range(len(q_layers)):
             mark()
             # the first layer's call allocates the chunk's blocks for every layer
+            # (and records where its tokens went: the later layers copy by that plan)
             self.kv.write_block_device(layer, sid_t, st_t, k_layers[layer].to(self.kv.dtype).contiguous(),
-                                       v_layers[layer].to(self.kv.dtype).contiguous(), alloc=layer == 0)
+                                       v_layers[layer].to(self.kv.dtype).contiguous(), alloc=layer == 0,
+                                       plan=self._write_plan)
             if plan is None:  # the round's attention plan, once its blocks exist
                 plan = VerifyPlan(self.kv, sid_t, st_t, chunk, int(q_layers[layer].shape[2]), max_ctx)
             mark()
@@ -374,6 +377,7 @@ class DraftLoop:
         self.kv = kv
         self.gamma = int(gamma)
         self.temperature = float(temperature)
+        self._write_plan = WritePlan()  # a step's rows, recorded by its first layer's append
 
     def run(self, seq_ids: torch.Tensor, ctx: torch.Tensor, max_ctx: int,
             q_steps: Sequence[Sequence[torch.Tensor]], k_steps: Sequence[Sequence[torch.Tensor]],
@@ -398,7 +402,8 @@ class DraftLoop:
             outs_s = []
             plan = None
             for layer in range(len(q_steps[s])):
-                kv.write_block_device(layer, seq_ids, pos, k_steps[s][layer], v_steps[s][layer], alloc=layer == 0)
+                kv.write_block_device(layer, seq_ids, pos, k_steps[s][layer], v_steps[s][layer], alloc=layer == 0,
+                                      plan=self._write_plan)
                 if plan is None:  # the step's attention plan, once its blocks exist
                     plan = VerifyPlan(kv, seq_ids, pos, 1, int(q_steps[s][layer].shape[2]), max_ctx + s + 1)
                 o = None if attn_out is None else attn_out[s][layer]
