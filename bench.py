@@ -630,7 +630,7 @@ def draft_decode(dev, seed=0):
     import torch
 
     from engine.attention import VerifyPlan, verify_attention
-    from engine.kv import PagedKVCache
+    from engine.kv import PagedKVCache, WritePlan
 
     hq, hkv, d, reps = 14, 2, 64, 8
     lens, g = workload_lens(seed)
@@ -662,6 +662,12 @@ def draft_decode(dev, seed=0):
     plans = [VerifyPlan(kv, sids[r], st, 1, hq, max_ctx) for r in range(reps)]
     attend = lambda i: verify_attention(q, kv, 0, sids[i % reps], st, max_ctx, out=out, plan=plans[i % reps])
     append = lambda i: kv.write_block_device(0, sids[i % reps], st, kn, vn, alloc=False)
+    # each replica's write plan (its blocks exist: the allocating append only records it)
+    wplans = [WritePlan() for _ in range(reps)]
+    for r in range(reps):
+        kv.write_block_device(0, sids[r], st, kn, vn, alloc=True, plan=wplans[r])
+    append_planned = lambda i: kv.write_block_device(0, sids[i % reps], st, kn, vn, alloc=False,
+                                                     plan=wplans[i % reps])
     n = 3 * reps
     for i in range(reps):
         attend(i)
@@ -670,6 +676,8 @@ def draft_decode(dev, seed=0):
     attn_us = time_graph(ga, 5, torch) * 1000.0 / n
     gw = graph_of(lambda: [append(i) for i in range(n)], 1, torch)
     app_us = time_graph(gw, 5, torch) * 1000.0 / n
+    gwp = graph_of(lambda: [append_planned(i) for i in range(n)], 1, torch)
+    app_planned_us = time_graph(gwp, 5, torch) * 1000.0 / n
     nbytes = attention_bytes(lens, 1, hq, hkv, d, BS)
     # Batched draft sampling of one step (B rows of V draft logits, T = 1) and
     # one whole draft step at the draft model's depth as a captured graph:
@@ -688,7 +696,9 @@ def draft_decode(dev, seed=0):
     def draft_step(i):
         for layer in range(depth):
             r = (i * depth + layer) % reps
-            kv.write_block_device(0, sids[r], st, kn, vn, alloc=False)
+            # the first layer's append allocates (and records the step's write
+            # plan); the later layers copy by the plan, as DraftLoop does
+            kv.write_block_device(0, sids[r], st, kn, vn, alloc=layer == 0, plan=wplans[r])
             if layer == 0:  # the step's plan, made once its blocks exist
                 plans[r] = VerifyPlan(kv, sids[r], st, 1, hq, max_ctx, buf=plans[r].buf)
             verify_attention(q, kv, 0, sids[r], st, max_ctx, out=out, plan=plans[r])
@@ -702,6 +712,7 @@ def draft_decode(dev, seed=0):
                        "of append + decode attention, then the sampling, as one captured graph",
            "attn_us": round(attn_us, 2), "attn_gbs": round(nbytes / (attn_us * 1e-6) / 1e9, 1),
            "attn_bytes_per_call": nbytes, "append_us": round(app_us, 2),
+           "append_planned_us": round(app_planned_us, 2),
            "sample_us": round(samp_us, 2),
            "sample_gbs": round(2 * B * VOCAB * 4 / (samp_us * 1e-6) / 1e9, 1),
            "step_24_layers_us": round(step_us, 1)}

@@ -430,11 +430,12 @@ __global__ void kv_write_plan_kernel(const int32_t* __restrict__ tables, int32_t
 
 // A later layer's append of the round's chunk by its write plan (no table,
 // block count or length is read: the first layer's append allocated and
-// recorded every token's row). One workgroup per (entry, kv head): the plan
-// entries, the K pieces and the V pieces are loaded in one round trip (V rows
-// go to LDS), then K rows are stored as 16-byte pieces and V^T elements with
-// the chunk's tokens fastest across lanes, so a wave's stores to one dim's row
-// of the transposed page are contiguous.
+// recorded every token's row). One workgroup per (entry, kv head), of as many
+// waves as the chunk's 16-byte pieces need (at most four): the plan entries,
+// the K pieces and the V pieces are loaded in one round trip (V rows go to
+// LDS), then K rows are stored as 16-byte pieces and V^T elements with the
+// chunk's tokens fastest across lanes, so a wave's stores to one dim's row of
+// the transposed page are contiguous.
 constexpr int kPlannedThreads = 256;
 constexpr int kPlannedItems = 4;                 // 16-byte pieces per thread for K, and for V
 constexpr int kPlannedMaxC = 64;                 // chunk tokens
@@ -450,24 +451,49 @@ __global__ __launch_bounds__(kPlannedThreads) void kv_write_planned_kernel(
   const size_t row_elems = (size_t)hkv * d;
   const int vec = (d * ES) >> 4;  // 16-byte pieces of one row
   const int np = C * vec;         // pieces of the chunk's K (and of its V)
+  const int nth = blockDim.x;
   uint4 kreg[kPlannedItems], vreg[kPlannedItems];
+  int dreg[kPlannedItems];
 #pragma unroll
   for (int k = 0; k < kPlannedItems; ++k) {
-    const int ip = min((int)threadIdx.x + k * kPlannedThreads, np - 1);
-    const size_t src = (((size_t)b * C + ip / vec) * row_elems + (size_t)h * d) * ES;
-    kreg[k] = reinterpret_cast<const uint4*>(knew + src)[ip % vec];
-    vreg[k] = reinterpret_cast<const uint4*>(vnew + src)[ip % vec];
+    const int ip = (int)threadIdx.x + k * nth;
+    if (ip < np) {
+      const size_t src = (((size_t)b * C + ip / vec) * row_elems + (size_t)h * d) * ES;
+      kreg[k] = reinterpret_cast<const uint4*>(knew + src)[ip % vec];
+      vreg[k] = reinterpret_cast<const uint4*>(vnew + src)[ip % vec];
+      dreg[k] = wplan[(size_t)b * C + ip / vec];
+    }
   }
-  if ((int)threadIdx.x < C) s_dest[threadIdx.x] = wplan[(size_t)b * C + threadIdx.x];
+  if (C <= 2) {
+    // One or two tokens: every thread stores its pieces straight from its
+    // registers (no transposition through LDS, no barrier).
+    constexpr int kPer = 16 / ES;  // elements of a piece
+#pragma unroll
+    for (int k = 0; k < kPlannedItems; ++k) {
+      const int ip = (int)threadIdx.x + k * nth;
+      if (ip < np && dreg[k] >= 0) {
+        const int dest = dreg[k], c = ip % vec;
+        const size_t slot = ((size_t)layer * cap + dest / bs) * hkv + h;
+        reinterpret_cast<uint4*>(kpool + (slot * bs + dest % bs) * (size_t)(d * ES))[c] = kreg[k];
+        T* vdst = reinterpret_cast<T*>(vpool) + slot * (size_t)d * bs + dest % bs;
+        T ve[kPer];
+        __builtin_memcpy(ve, &vreg[k], 16);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) vdst[(size_t)(c * kPer + j) * bs] = ve[j];
+      }
+    }
+    return;
+  }
+  for (int o = threadIdx.x; o < C; o += nth) s_dest[o] = wplan[(size_t)b * C + o];
 #pragma unroll
   for (int k = 0; k < kPlannedItems; ++k) {
-    const int ip = (int)threadIdx.x + k * kPlannedThreads;
+    const int ip = (int)threadIdx.x + k * nth;
     if (ip < np) reinterpret_cast<uint4*>(s_v)[ip] = vreg[k];
   }
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < kPlannedItems; ++k) {
-    const int ip = (int)threadIdx.x + k * kPlannedThreads;
+    const int ip = (int)threadIdx.x + k * nth;
     if (ip < np) {
       const int dest = s_dest[ip / vec];
       if (dest >= 0) {
@@ -477,7 +503,7 @@ __global__ __launch_bounds__(kPlannedThreads) void kv_write_planned_kernel(
     }
   }
   const T* sv = reinterpret_cast<const T*>(s_v);
-  for (int iv = threadIdx.x; iv < C * d; iv += kPlannedThreads) {
+  for (int iv = threadIdx.x; iv < C * d; iv += nth) {
     const int e = iv / C, o = iv - e * C;  // tokens fastest
     const int dest = s_dest[o];
     if (dest >= 0) {
@@ -1428,15 +1454,19 @@ int spv_kv_write_planned(void* k_pool, void* v_pool, int kv_dtype, const void* k
   if (B == 0) return SPV_OK;
   hipStream_t s = (hipStream_t)stream;
   const size_t smem = (size_t)C * head_dim * es;
+  const int np = C * (head_dim * es / 16);  // 16-byte pieces of the chunk's K (and V), <= 4 per thread
+  // threads: <= kPlannedItems K/V pieces each, and <= 4 V^T elements each in the staged store
+  const int need = max((np + kPlannedItems - 1) / kPlannedItems, C <= 2 ? 0 : (C * head_dim + 3) / 4);
+  const int nth = min(kPlannedThreads, max(64, (need + 63) / 64 * 64));
   auto* kp = static_cast<uint8_t*>(k_pool);
   auto* vp = static_cast<uint8_t*>(v_pool);
   auto* kn = static_cast<const uint8_t*>(k_new);
   auto* vn = static_cast<const uint8_t*>(v_new);
   if (es == 4)
-    hipLaunchKernelGGL(kv_write_planned_kernel<4>, dim3(B * num_kv_heads), dim3(kPlannedThreads), smem, s, kp, vp,
+    hipLaunchKernelGGL(kv_write_planned_kernel<4>, dim3(B * num_kv_heads), dim3(nth), smem, s, kp, vp,
                        kn, vn, write_plan, C, layer, capacity, block_size, num_kv_heads, head_dim);
   else
-    hipLaunchKernelGGL(kv_write_planned_kernel<2>, dim3(B * num_kv_heads), dim3(kPlannedThreads), smem, s, kp, vp,
+    hipLaunchKernelGGL(kv_write_planned_kernel<2>, dim3(B * num_kv_heads), dim3(nth), smem, s, kp, vp,
                        kn, vn, write_plan, C, layer, capacity, block_size, num_kv_heads, head_dim);
   SPV_CHECK_LAUNCH();
   return SPV_OK;
