@@ -42,6 +42,10 @@ constexpr int kVecPerThread = kChunk / 4 / kThreads;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr double kEps = 1e-12;     // specdec/sampler.py:16
 constexpr float kTieRel = 1e-6f;   // top-2 gap below which the race is redone exactly
+// Relative error of p (and q) in logits mode against torch's softmax (fast
+// exp2, another summation order): r = p - q then carries up to
+// kProbRel (p + q) of absolute error, which a near cancellation does not shrink.
+constexpr float kProbRel = 4e-6f;
 
 enum RaceMode : int { RACE_NONE = 0, RACE_RESIDUAL = 1, RACE_BONUS = 2 };
 
@@ -505,7 +509,8 @@ __device__ __forceinline__ float exact_prob(float z, float m, float s, float tf,
 
 // The draw and the commit of sequence b, in the workgroup that completed its
 // race: combine the per-chunk top-2 (coherent loads), re-race exactly when the
-// best two keys are within kTieRel or the residual is empty, then cut.
+// best two keys are within kTieRel plus their own error bound (logits mode:
+// kProbRel (p + q) / E each) or the residual is empty, then cut.
 __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitArgs& cm, const SampleWs& ws, int b,
                                              const RaceInfo& info) {
   const int C = a.gamma + 1, nch = num_chunks(a.V);
@@ -540,7 +545,22 @@ __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitAr
     }
     if (threadIdx.x == 0) {
       int exact = 0;
-      const bool tie = !isnan(t2.v1) && !(t2.v1 - t2.v2 > kTieRel * t2.v1);
+      // The two best keys' own error in logits mode: kProbRel (p + q) / E each
+      // (p and q reloaded at the two indices).
+      float werr = 0.f;
+      if (!a.is_probs && !isnan(t2.v1) && t2.i1 < a.V && t2.i2 < a.V) {
+        const int k = info.k;
+        const float* pr = a.target + ((size_t)b * C + k) * a.V;
+        const float* qr = info.mode == RACE_RESIDUAL ? a.draft + ((size_t)b * a.gamma + k) * a.V : nullptr;
+        const float* e = cm.noise + (size_t)b * a.V;
+        auto w = [&](int i) {
+          float pq = exact_prob(pr[i], info.mp, info.sp, a.tf, false);
+          if (qr) pq += exact_prob(qr[i], info.mq, info.sq, a.tf, false);
+          return pq / e[i];
+        };
+        werr = kProbRel * (w(t2.i1) + w(t2.i2));
+      }
+      const bool tie = !isnan(t2.v1) && !(t2.v1 - t2.v2 > kTieRel * t2.v1 + werr);
       if (info.mode == RACE_RESIDUAL) {
         const float t = (float)rs;  // fp32 sum, accumulated in fp64 and rounded once
         s_t = t;

@@ -206,6 +206,46 @@ def test_near_tie_race_takes_the_exact_path(cuda, reject_at, relation):
     assert res.accepted_lists() == want
 
 
+def _cancelling_residual_case(seed, V, gap, gamma=3):
+    """Logits mode, row 0 rejected (u = 1): the draft row is the target row with
+    the logits of two tokens a < b lowered by 0.01, so only a and b keep a
+    residual r = p - q, about 1% of p (p and q nearly cancel). Their Exp(1)
+    entries make them the two best keys, key_b = key_a (1 + gap) on the
+    oracle's arithmetic."""
+    g = torch.Generator().manual_seed(seed)
+    target = torch.randn(1, gamma + 1, V, generator=g) * 2.0
+    draft = target[:, :gamma].clone()
+    a, b = sorted(torch.randperm(V, generator=g)[:2].tolist())
+    draft[0, 0, a] -= 0.01
+    draft[0, 0, b] -= 0.01
+    x = torch.randint(0, V, (1, gamma), generator=g).to(torch.int32)
+    u = torch.ones(1, gamma)
+    noise = torch.empty(1, V).exponential_(1, generator=g)
+    p = S.logits_to_probs(target, 1.0)[0, 0]
+    q = S.logits_to_probs(draft, 1.0)[0, 0]
+    d = torch.clamp(p - q, min=0)  # the residual before its normalisation
+    assert float(d[a]) > 0 and float(d[b]) > 0 and int((d > 0).sum()) == 2
+    assert float(d[a] / p[a]) < 0.02  # the residual is a near cancellation
+    r = S.residual_distribution(p, q)
+    noise[0, a] = float(r[a]) * 1e-3  # key_a ~ 1000, far above the rest (r = 0 elsewhere)
+    noise[0, b] = float(r[b]) * 1e-3 / (1.0 + gap)
+    return target, draft, x, u, noise, (b if gap > 0 else a)
+
+
+@pytest.mark.parametrize("gap", [2e-4, -2e-4])
+def test_cancelling_residual_near_tie_in_logits_mode(cuda, gap):
+    """Two residual keys 2e-4 apart where r = p - q cancels to ~1% of p: the
+    fast race's keys carry up to ~2e-4 of relative error there (p and q each
+    ~1e-6 off torch's), beyond the fixed 1e-6 tie window, so the kernel's tie
+    test adds the keys' own bound (4e-6 (p + q) / E each) and re-races exactly;
+    the token must be the oracle's."""
+    target, draft, x, u, noise, tok = _cancelling_residual_case(7 if gap > 0 else 8, 151936, gap)
+    want = S.verify_from_logits(target, draft, x, u, noise, 1.0)
+    assert want[0][-1] == tok
+    res = es.verify_sample(target.to(cuda), draft.to(cuda), x.to(cuda), u.to(cuda), noise.to(cuda), 1.0)
+    assert res.accepted_lists() == want
+
+
 def test_fused_sampler_probs_mode_matches_batch_accept(cuda):
     g, target, draft, u, noise = _workload(7, B=8, gamma=3, V=5000)
     p, q = S.logits_to_probs(target, 1.0), S.logits_to_probs(draft, 1.0)
