@@ -1023,12 +1023,12 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
             for (int jj = 0; jj < 4; ++jj)
               if (kpos0 + jj > start + jrow[nt]) sc[nt][jj] = -INFINITY;
         }
+        // (one compare per tile, on the largest of the lane's four scores)
         const float rsp = __builtin_amdgcn_rcpf(spage);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const float t = (m[nt] + kSlack) * rsp;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) grow |= sc[nt][jj] > t;
+          grow |= fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])) > t;
         }
       } else {
 #pragma unroll
@@ -1062,18 +1062,36 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         }
       }
       // P = 2^(s - m) (times the page's V factor) per query tile; the row sums
-      // take 2^(s - m) itself.
+      // take 2^(s - m) itself. With the lean softmax over fp16 fp8 pages the V
+      // factor vf rides in the exponent, 2^(s - m + log2 vf), and the row sum
+      // takes the tile's sum times 1 / vf (an all-zero block, vf = 0, instead
+      // has its V operand zeroed and P unscaled).
+      constexpr bool kFold = kLean && h16;
+      float lvf = 0.f, rvf = 1.f;
+      if constexpr (kFold) {
+        if (vscale != 0.f) {
+          lvf = __builtin_amdgcn_logf(vscale);
+          rvf = __builtin_amdgcn_rcpf(vscale);
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) vfrag(mt) = make_uint2(0u, 0u);
+        }
+      }
       auto p_tile = [&](int nt, float (&e)[4]) {
         const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          if constexpr (kLean) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[nt][jj], spage, -mu));
+          if constexpr (kLean) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[nt][jj], spage, lvf - mu));
           else e[jj] = __builtin_amdgcn_exp2f(x[nt][jj] - mu);
         }
-        l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
-        if constexpr (kFp8) {
+        if constexpr (kFold) {
+          l[nt] = fmaf((e[0] + e[1]) + (e[2] + e[3]), rvf, l[nt]);
+        } else {
+          l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
+          if constexpr (kFp8) {
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) e[jj] *= vscale;
+            for (int jj = 0; jj < 4; ++jj) e[jj] *= vscale;
+          }
         }
       };
       if constexpr (h16) {
