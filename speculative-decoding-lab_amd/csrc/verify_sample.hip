@@ -61,7 +61,9 @@ struct RacePart {
   float v1, v2;  // best and second-best r / E of the chunk
   int i1, i2;
   double rsum, psum;
-};  // 32 bytes: two coherent 16-byte stores
+  float e1, e2;  // their error weights (p + q) / E (logits mode)
+  int pad[2];
+};  // 48 bytes: three coherent 16-byte stores
 
 struct SampleWs {
   int* cnt_stats;  // [B] row-stats workgroups of each sequence that have finished
@@ -144,13 +146,16 @@ __device__ __forceinline__ void block_argmax(float& v, int& i) {
   __syncthreads();
 }
 
-// Top-2 (value, index) under `better`.
+// Top-2 (value, index) under `better`; the verify race also carries each
+// key's error weight (e1, e2), which moves with its key.
 struct Top2 {
   float v1, v2;
   int i1, i2;
+  float e1, e2;
   __device__ __forceinline__ void init() {
     v1 = v2 = -INFINITY;
     i1 = i2 = 0x7fffffff;
+    e1 = e2 = 0.f;
   }
   __device__ __forceinline__ void push(float v, int i) {
     if (better(v, i, v1, i1)) {
@@ -185,6 +190,36 @@ struct Top2 {
       const float w1 = __shfl_xor(v1, o, 64), w2 = __shfl_xor(v2, o, 64);
       const int j1 = __shfl_xor(i1, o, 64), j2 = __shfl_xor(i2, o, 64);
       merge(w1, j1, w2, j2);
+    }
+  }
+  // merge and wave_reduce with the error weights
+  __device__ __forceinline__ void merge_e(float w1, int j1, float f1, float w2, int j2, float f2) {
+    if (better(w1, j1, v1, i1)) {
+      if (better(v1, i1, w2, j2)) {
+        v2 = v1;
+        i2 = i1;
+        e2 = e1;
+      } else {
+        v2 = w2;
+        i2 = j2;
+        e2 = f2;
+      }
+      v1 = w1;
+      i1 = j1;
+      e1 = f1;
+    } else if (better(w1, j1, v2, i2)) {
+      v2 = w1;
+      i2 = j1;
+      e2 = f1;
+    }
+  }
+  __device__ __forceinline__ void wave_reduce_e() {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float w1 = __shfl_xor(v1, o, 64), w2 = __shfl_xor(v2, o, 64);
+      const int j1 = __shfl_xor(i1, o, 64), j2 = __shfl_xor(i2, o, 64);
+      const float f1 = __shfl_xor(e1, o, 64), f2 = __shfl_xor(e2, o, 64);
+      merge_e(w1, j1, f1, w2, j2, f2);
     }
   }
 };
@@ -532,12 +567,14 @@ __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitAr
     double rs = 0.0, ps = 0.0;
     for (int c = threadIdx.x; c < nch; c += 64) {
       const size_t o = ((size_t)b * nch + c) * sizeof(RacePart);
-      const u32x4_t lo = load_coherent_b128(rr, o), hi = load_coherent_b128(rr, o + 16);
-      t2.merge(__uint_as_float(lo.x), (int)lo.z, __uint_as_float(lo.y), (int)lo.w);
+      const u32x4_t lo = load_coherent_b128(rr, o), hi = load_coherent_b128(rr, o + 16),
+                    ew = load_coherent_b128(rr, o + 32);
+      t2.merge_e(__uint_as_float(lo.x), (int)lo.z, __uint_as_float(ew.x), __uint_as_float(lo.y), (int)lo.w,
+                 __uint_as_float(ew.y));
       rs += __hiloint2double((int)hi.y, (int)hi.x);
       ps += __hiloint2double((int)hi.w, (int)hi.z);
     }
-    t2.wave_reduce();
+    t2.wave_reduce_e();
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       rs += __shfl_xor(rs, o, 64);
@@ -545,21 +582,9 @@ __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitAr
     }
     if (threadIdx.x == 0) {
       int exact = 0;
-      // The two best keys' own error in logits mode: kProbRel (p + q) / E each
-      // (p and q reloaded at the two indices).
-      float werr = 0.f;
-      if (!a.is_probs && !isnan(t2.v1) && t2.i1 < a.V && t2.i2 < a.V) {
-        const int k = info.k;
-        const float* pr = a.target + ((size_t)b * C + k) * a.V;
-        const float* qr = info.mode == RACE_RESIDUAL ? a.draft + ((size_t)b * a.gamma + k) * a.V : nullptr;
-        const float* e = cm.noise + (size_t)b * a.V;
-        auto w = [&](int i) {
-          float pq = exact_prob(pr[i], info.mp, info.sp, a.tf, false);
-          if (qr) pq += exact_prob(qr[i], info.mq, info.sq, a.tf, false);
-          return pq / e[i];
-        };
-        werr = kProbRel * (w(t2.i1) + w(t2.i2));
-      }
+      // The two best keys' own error in logits mode: kProbRel (p + q) / E
+      // each, their weights carried with them through the chunks' partials.
+      const float werr = a.is_probs ? 0.f : kProbRel * (t2.e1 + t2.e2);
       const bool tie = !isnan(t2.v1) && !(t2.v1 - t2.v2 > kTieRel * t2.v1 + werr);
       if (info.mode == RACE_RESIDUAL) {
         const float t = (float)rs;  // fp32 sum, accumulated in fp64 and rounded once
@@ -641,9 +666,10 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
   int nan_i = 0x7fffffff;
   auto visit = [&](int i, bool ok, float zp, float zq, float ei) {
     float p = prob(zp, mp, isp);
-    float r = p;
+    float r = p, qv = 0.f;
     if (RESID) {
-      const float d = p - prob(zq, mq, isq);
+      qv = prob(zq, mq, isq);
+      const float d = p - qv;
       r = d < 0.f ? 0.f : d;  // torch.clamp(p - q, min=0): NaN stays NaN
     }
     r = ok ? r : 0.f;
@@ -651,12 +677,17 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
       rs += r;
       ps += ok ? p : 0.f;
     }
-    const float key = ok ? r * __builtin_amdgcn_rcpf(ei) : -1.f;
+    const float re = __builtin_amdgcn_rcpf(ei);
+    const float key = ok ? r * re : -1.f;
+    // error weight (p + q) / E of the key (logits mode)
+    const float ew = PROBS ? 0.f : (p + qv) * re;
     const bool c1 = key > t2.v1, c2 = key > t2.v2;
     t2.v2 = c1 ? t2.v1 : (c2 ? key : t2.v2);
     t2.i2 = c1 ? t2.i1 : (c2 ? i : t2.i2);
+    t2.e2 = c1 ? t2.e1 : (c2 ? ew : t2.e2);
     t2.v1 = c1 ? key : t2.v1;
     t2.i1 = c1 ? i : t2.i1;
+    t2.e1 = c1 ? ew : t2.e1;
     nan_i = (key != key && nan_i == 0x7fffffff) ? i : nan_i;
   };
   if ((V & 3) == 0) {
@@ -687,8 +718,10 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
   if (nan_i != 0x7fffffff) {  // a NaN key leads the thread's list
     t2.v2 = t2.v1;
     t2.i2 = t2.i1;
+    t2.e2 = t2.e1;
     t2.v1 = __uint_as_float(0x7fc00000u);
     t2.i1 = nan_i;
+    t2.e1 = 0.f;
   }
 }
 
@@ -704,8 +737,8 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
   float rs = 0.f, ps = 0.f;
   if (info.mode == RACE_RESIDUAL) race_chunk<true, UNIT, PROBS>(a, info, b, c, t2, rs, ps, e);
   else if (info.mode == RACE_BONUS) race_chunk<false, UNIT, PROBS>(a, info, b, c, t2, rs, ps, e);
-  t2.wave_reduce();
-  __shared__ float s_v1[kWaves], s_v2[kWaves];
+  t2.wave_reduce_e();
+  __shared__ float s_v1[kWaves], s_v2[kWaves], s_e1[kWaves], s_e2[kWaves];
   __shared__ int s_i1[kWaves], s_i2[kWaves];
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
@@ -713,17 +746,20 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
     s_v2[w] = t2.v2;
     s_i1[w] = t2.i1;
     s_i2[w] = t2.i2;
+    s_e1[w] = t2.e1;
+    s_e2[w] = t2.e2;
   }
   const double rsum = block_sum_f64((double)rs);
   const double psum = block_sum_f64((double)ps);
   if (threadIdx.x == 0) {
-    for (int k = 1; k < kWaves; ++k) t2.merge(s_v1[k], s_i1[k], s_v2[k], s_i2[k]);
+    for (int k = 1; k < kWaves; ++k) t2.merge_e(s_v1[k], s_i1[k], s_e1[k], s_v2[k], s_i2[k], s_e2[k]);
     const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(ws.race);
     const size_t o = ((size_t)b * nch + c) * sizeof(RacePart);
     store_coherent_b128(rp, o, u32x4_t{__float_as_uint(t2.v1), __float_as_uint(t2.v2), (unsigned)t2.i1,
                                        (unsigned)t2.i2});
     store_coherent_b128(rp, o + 16, u32x4_t{(unsigned)__double2loint(rsum), (unsigned)__double2hiint(rsum),
                                             (unsigned)__double2loint(psum), (unsigned)__double2hiint(psum)});
+    store_coherent_b128(rp, o + 32, u32x4_t{__float_as_uint(t2.e1), __float_as_uint(t2.e2), 0u, 0u});
   }
   __shared__ int s_last;
   if (arrive_last(ws.cnt_race + b, nch, &s_last)) finalize_seq(a, cm, ws, b, info);
