@@ -34,9 +34,11 @@ using namespace spv;
 
 namespace {
 
-// Elements of a row per race workgroup: 16,384 (10 chunks at V = 151,936) ran
-// about 1 us faster per sampling call than 8,192 or 32,768, and 4,096 3 us slower.
-constexpr int kChunk = 16384;
+// Elements of a row per race workgroup: 19,456 (8 chunks at V = 151,936, so a
+// batch of 32 is one workgroup per CU) ran about 1 us faster per sampling call
+// than 16,384 (10 chunks) and 12,288; 16,384 had been about 1 us faster than
+// 8,192 or 32,768, and 4,096 3 us slower. A multiple of 4 x 256.
+constexpr int kChunk = 19456;
 constexpr int kThreads = 256;
 constexpr int kVecPerThread = kChunk / 4 / kThreads;
 constexpr float kLog2e = 1.4426950408889634f;
