@@ -6,14 +6,20 @@ Workload (Qwen2.5-1.5B-shaped single-layer verify, gamma = 5): batch 32, 12 q /
 tables are a random permutation of a 65,536-block pool; the rest of the pool is
 the free list. One step =
 
-  1. append the 6 verify tokens of every sequence (device allocation + copy),
+  1. the commit of the replica's previous round (rewind of the pool to start +
+     n_commit with the lengths that round sampled) and the append of this
+     round's 6 verify tokens of every sequence (device allocation + copy), in
+     one launch (``rewind_append_device``: the two calls' exact result),
   2. the round's attention plan (``VerifyPlan``: the split of the batch over
      the workgroups and their first block ids, made once per round and shared
      by the round's layers),
   3. verify attention of the 6 rows x 12 heads over the paged context,
   4. fused rejection sampling of the round over a 151,936-entry vocabulary
      (target logits N(0, 2^2), draft = target + N(0, 1), T = 1, caller noise),
-  5. rewind of the pool to start + n_commit with the sampled lengths.
+     whose committed lengths the replica's next step rewinds to.
+
+``parts_us.append_rewind`` times that one launch; ``append_rewind_separate``
+the same work as the two calls (``write_block_device``, ``rewind_device``).
 
 All inputs are resident in HBM before timing. The batch exists in 8 replicas on
 disjoint random pages of the pool, each with its own draw of the context
@@ -205,6 +211,9 @@ def make_step(w):
     # one result per replica: a rewind applies the lengths sampled against its
     # own replica's start positions
     results = [_new_result(B, GAMMA, kv.device) for _ in range(REPLICAS)]
+    for res in results:  # nothing to commit before a replica's first round
+        res.new_len.fill_(-1)
+        res.finished.zero_()
     plans = [VerifyPlan(kv, w["sids"][r], w["start"][r], C, HQ, w["max_ctx"][r]) for r in range(REPLICAS)]
 
     def append(r):
@@ -225,17 +234,21 @@ def make_step(w):
     def rewind(r):
         kv.rewind_device(w["sids"][r], results[r].new_len, results[r].finished)
 
+    def rewind_append(r):  # the replica's last commit, then this round's append: one launch
+        kv.rewind_append_device(w["sids"][r], results[r].new_len, results[r].finished, w["start"][r],
+                                w["k_new"], w["v_new"])
+
     def step(i, events=None):
         r, t = i % REPLICAS, i % LOGIT_SETS
-        append(r)
+        rewind_append(r)
         plan(r)
         if events is not None:
             events.arm()
         attend(r)
         sample(t, r)
-        rewind(r)
 
-    return step, {"append": append, "plan": plan, "attend": attend, "sample": sample, "rewind": rewind}, \
+    return step, {"append": append, "plan": plan, "attend": attend, "sample": sample, "rewind": rewind,
+                  "rewind_append": rewind_append}, \
         results[0]
 
 
@@ -823,9 +836,13 @@ def main() -> int:
     del g_plan
     g_smp = graph_of(lambda: [parts["sample"](i % LOGIT_SETS, i % REPLICAS) for i in range(reps)], 1, torch)
     part_us["sample"] = time_graph(g_smp, 5, torch) * 1000.0 / reps
+    g_ra = graph_of(lambda: [parts["rewind_append"](i % REPLICAS) for i in range(reps)], 1, torch)
+    part_us["append_rewind"] = time_graph(g_ra, 5, torch) * 1000.0 / reps
+    del g_ra
     g_ar = graph_of(lambda: [(parts["append"](i % REPLICAS), parts["rewind"](i % REPLICAS)) for i in range(reps)],
                     1, torch)
-    part_us["append_rewind"] = time_graph(g_ar, 5, torch) * 1000.0 / reps
+    part_us["append_rewind_separate"] = time_graph(g_ar, 5, torch) * 1000.0 / reps
+    del g_ar
     # the same sampling with top-k / top-p filtering of both sides' logits
     from engine.spec_scheduler import _new_result, verify_sample
 
@@ -907,14 +924,14 @@ def main() -> int:
         print("bench: prefill", file=sys.stderr, flush=True)
         line["prefill"] = prefill(dev, args.seed)
     if args.full_depth_rounds > 0:
-        del g_step, g_att, g_smp, g_ar, step, parts, res, w
+        del g_step, g_att, g_smp, step, parts, res, w
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         print("bench: full-depth continuous batching", file=sys.stderr, flush=True)
         line["full_depth"] = full_depth(dev, args.full_depth_rounds, 4, args.seed)
     if not args.no_long_context:
         if args.full_depth_rounds <= 0:
-            del g_step, g_att, g_smp, g_ar, step, parts, res, w
+            del g_step, g_att, g_smp, step, parts, res, w
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
         print("bench: long-context fp8 / bf16 attention", file=sys.stderr, flush=True)

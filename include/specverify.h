@@ -181,6 +181,32 @@ int spv_kv_rewind(int32_t* block_tables, int32_t max_blocks_per_seq,
                   const int32_t* finished, int32_t n, int32_t capacity,
                   int32_t block_size, int32_t shrink_only, void* stream);
 
+/* One round's commit and the next round's append of the same batch in one
+ * launch: exactly spv_kv_rewind(seq_ids, new_len, finished, B, shrink_only =
+ * 0) followed by spv_kv_append_plan(k_new, v_new at start_pos, may_alloc = 1,
+ * write_limit_b = -1, write_plan) -- PagedKVCache.truncate / clear of the
+ * commit loop (engine/spec_scheduler.py:296-322, engine/kv.py:150-171) then
+ * the next round's per-token writes (engine/model.py:184-187, engine/kv.py:
+ * 119-147), with nothing between them (no admission). Block tables, lengths,
+ * the free stack (bottom to top), flags, counters, stored K/V and the write
+ * plan (B x C int32, or NULL) equal the two calls' results in every case,
+ * including exhaustion, table-width overflow, finished sequences and blocks
+ * already free. One launch for 16-byte-multiple K rows, B <= 256, chunks of
+ * at most 1024 K/V elements per head touching at most 8 blocks; otherwise the
+ * two calls are enqueued. new_len / finished may be NULL (no truncation /
+ * none finished). Not for fp8 pools (SPV_ERR_ARG). No reference counterpart
+ * for the fusion itself. */
+int spv_kv_rewind_append(void* k_pool, void* v_pool, int kv_dtype,
+                         const void* k_new, const void* v_new,
+                         int32_t* block_tables, int32_t max_blocks_per_seq,
+                         int32_t* num_blocks, int32_t* seq_lens,
+                         int32_t* free_stack, int32_t* free_flag, int32_t* ctr,
+                         const int32_t* seq_ids, const int32_t* new_len,
+                         const int32_t* finished, const int32_t* start_pos,
+                         int32_t B, int32_t C, int32_t layer, int32_t capacity,
+                         int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t* write_plan, void* stream);
+
 /* Draft-cache alignment after a verify round (engine/spec_scheduler.py:296-322:
  * the draft truncate / catch-up / clear of the commit loop, on the draft pool).
  * Entry i: sequence seq_ids[i] started the round at start_pos[i] = L and

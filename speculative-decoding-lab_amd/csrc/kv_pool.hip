@@ -64,11 +64,13 @@ __global__ void free_one_kernel(int32_t* __restrict__ free_stack, int32_t* __res
 // and the stack's top entries (as many as this call can pop, staged in LDS).
 constexpr int kAllocStage = 4096;
 
-__global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
-    int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
-    const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
-    const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, int32_t B, int32_t C,
-    int32_t bs, float* __restrict__ scales, int32_t num_layers, int32_t cap) {
+// One workgroup of at most kPoolThreads threads (kv_alloc_kernel: kPoolThreads;
+// also the fallback of kv_rewind_append_kernel).
+__device__ __forceinline__ void alloc_wg(int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+                         const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+                         int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_ids,
+                         const int32_t* __restrict__ start, int32_t B, int32_t C, int32_t bs,
+                         float* __restrict__ scales, int32_t num_layers, int32_t cap) {
   __shared__ int s_scan[kPoolThreads / 64];
   __shared__ int s_fail, s_ovf;
   __shared__ int s_free[kAllocStage];  // s_free[i] = free_stack[top - 1 - i]
@@ -135,6 +137,14 @@ __global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
     ctr[CTR_EXHAUSTED] = s_fail < B ? s_fail + 1 : 0;
     if (s_ovf < B) ctr[CTR_OVERFLOW] = s_ovf + 1;
   }
+}
+
+__global__ __launch_bounds__(kPoolThreads) void kv_alloc_kernel(
+    int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+    const int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
+    const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ start, int32_t B, int32_t C,
+    int32_t bs, float* __restrict__ scales, int32_t num_layers, int32_t cap) {
+  alloc_wg(tables, maxb, nblocks, free_stack, free_flag, ctr, seq_ids, start, B, C, bs, scales, num_layers, cap);
 }
 
 // The K/V copy of an append: one workgroup per (batch entry b, kv head h,
@@ -725,11 +735,14 @@ __device__ void rewind_replay(const int32_t* __restrict__ tables, int maxb, int3
   ctr[CTR_SLOWPATH] += 1;
 }
 
-__global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
-    const int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
-    int32_t* __restrict__ seq_lens, int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
-    int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ new_len,
-    const int32_t* __restrict__ finished, int32_t n, int32_t bs, int32_t shrink_only, int32_t cap) {
+// One workgroup of at most kPoolThreads threads (kv_rewind_kernel: kPoolThreads;
+// also the fallback of kv_rewind_append_kernel).
+__device__ __forceinline__ void rewind_wg(const int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+                          int32_t* __restrict__ seq_lens, int32_t* __restrict__ free_stack,
+                          int32_t* __restrict__ free_flag, int32_t* __restrict__ ctr,
+                          const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ new_len,
+                          const int32_t* __restrict__ finished, int32_t n, int32_t bs, int32_t shrink_only,
+                          int32_t cap) {
   __shared__ int s_scan[kPoolThreads / 64];
   __shared__ int s_top, s_dup;
   __shared__ int s_off[kPoolThreads], s_sid[kPoolThreads], s_nb[kPoolThreads], s_ft[kPoolThreads];
@@ -793,7 +806,7 @@ __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
                       bs, shrink_only, cap, top);
       return;
     }
-    if (total <= kRewindItems) {
+    if (total <= kRewindRounds * (int)blockDim.x) {  // (kRewindItems with kPoolThreads threads)
       if (i < n) {
         s_off[i] = off;
         s_sid[i] = e.sid;
@@ -931,6 +944,296 @@ __global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
   if (threadIdx.x == 0)
     rewind_replay(tables, maxb, nblocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len, finished, n, bs,
                   shrink_only, cap, top);
+}
+
+__global__ __launch_bounds__(kPoolThreads) void kv_rewind_kernel(
+    const int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+    int32_t* __restrict__ seq_lens, int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+    int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ new_len,
+    const int32_t* __restrict__ finished, int32_t n, int32_t bs, int32_t shrink_only, int32_t cap) {
+  rewind_wg(tables, maxb, nblocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len, finished, n, bs,
+            shrink_only, cap);
+}
+
+// ------------------------------------------------------------------ rewind + append
+//
+// One round's commit and the next round's append of the same batch in one
+// launch: exactly spv_kv_rewind (new_len / finished, shrink_only = 0) followed
+// by spv_kv_append (the chunk at start_pos, allocating, write limit from the
+// exhaustion verdict). Between rounds nothing else touches the pool when no
+// sequence is admitted, so the reference's commit loop (spec_scheduler.py:
+// 296-322: truncate, clear) and the next round's writes (model.py:184-187,
+// kv.py:119-147) meet here. One 256-thread workgroup per (batch entry b, kv head h), as
+// kv_append_fused_kernel; every workgroup recomputes the whole batch's rewind
+// (each truncated tail pushed tail-first, in batch order, kv.py:150-162) and
+// then its allocation from the stack those pushes leave, so it knows the
+// blocks of its own chunk without waiting for another workgroup.
+//
+// The common case -- no entry finished, every truncation frees at most
+// kSpecTail blocks, none of them already free or freed twice -- takes four
+// dependent round trips: ids / starts / new lengths / stack height, then block
+// counts, table tails and stack entries, then the freed blocks' flags (the
+// already-free test), then the arrival count. Every workgroup reads the
+// table tails and flags that the commit changes, so all of those writes
+// (pushes, new table entries, flags, block counts, stack height) are made by
+// the workgroup that arrives last, one entry per thread; the others write only
+// their chunk's keys and values (and their entry's length and plan row).
+// Anything else (a finished sequence, a long truncation, a block already free
+// or listed twice, an id outside the pool) changes nothing until all have
+// arrived; the last workgroup then runs the exact single-workgroup rewind and
+// allocation (rewind_wg, alloc_wg) and copies every entry's chunk itself.
+constexpr int kRaThreads = 256;  // one batch entry per thread (B <= 256)
+constexpr int kRaItems = 4;      // chunk K pieces / V elements per thread
+constexpr int kRaStage = 1024;   // stack entries staged in LDS
+constexpr int kRaHash = 2048;    // LDS hash slots: > kSpecTail * kRaThreads freed ids
+
+template <int ES>
+__global__ __launch_bounds__(kRaThreads) void kv_rewind_append_kernel(
+    uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool, const uint8_t* __restrict__ knew,
+    const uint8_t* __restrict__ vnew, int32_t* __restrict__ tables, int32_t maxb, int32_t* __restrict__ nblocks,
+    int32_t* __restrict__ seq_lens, int32_t* __restrict__ free_stack, int32_t* __restrict__ free_flag,
+    int32_t* __restrict__ ctr, const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ new_len,
+    const int32_t* __restrict__ finished, const int32_t* __restrict__ start, int32_t B, int32_t C, int32_t layer,
+    int32_t cap, int32_t bs, int32_t hkv, int32_t d, int32_t* __restrict__ wplan) {
+  using T = typename Elem<ES>::T;
+  __shared__ int s_scan[kRaThreads / 64];
+  __shared__ int s_free[kRaStage];              // s_free[i] = free_stack[top - 1 - i]
+  __shared__ int s_push[kSpecTail * kRaThreads];  // stack index top + i after the pushes
+  __shared__ int s_hash[kRaHash];
+  __shared__ int s_fail, s_ovf, s_aoff, s_got, s_nb1, s_len1, s_flag;
+  __shared__ int s_phys[kFusedMaxBlocks];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x / hkv, h = blockIdx.x - b * hkv;
+  const size_t row_elems = (size_t)hkv * d;
+  const int vec = (d * ES) >> 4;  // 16-byte pieces of one K row
+  const int nk = C * vec, nv = C * d;
+  // Round trip 1: the chunk's rows (independent of the state), the batch's
+  // ids, starts, new lengths and flags, the stack height.
+  auto load_k = [&](int k) {
+    const int ik = min(tid + k * kRaThreads, nk - 1);
+    return reinterpret_cast<const uint4*>(knew + (((size_t)b * C + ik / vec) * row_elems + (size_t)h * d) * ES)[ik % vec];
+  };
+  auto load_v = [&](int k) {
+    const int iv = min(tid + k * kRaThreads, nv - 1);
+    return reinterpret_cast<const T*>(vnew)[((size_t)b * C + iv / d) * row_elems + (size_t)h * d + iv % d];
+  };
+  static_assert(kRaItems == 4, "four named items");
+  const uint4 k0 = load_k(0), k1 = load_k(1), k2 = load_k(2), k3 = load_k(3);
+  const T v0 = load_v(0), v1 = load_v(1), v2 = load_v(2), v3 = load_v(3);
+  const int top = ctr[CTR_TOP];
+  const int sid = seq_ids[b], s0 = start[b];
+  const bool act = tid < B;
+  const int e = min(tid, B - 1);
+  const int sid_e = seq_ids[e], st_e = start[e];
+  const int nl_e = new_len ? new_len[e] : -1;
+  const int fin_e = finished ? finished[e] : 0;
+  for (int i = tid; i < kRaHash; i += kRaThreads) s_hash[i] = -1;
+  if (tid == 0) s_fail = s_ovf = B;
+  // Round trip 2: block counts, the table entries from each new length's
+  // first dropped block on, this entry's chunk blocks and length, and the
+  // stack's top entries (as many as the allocation can pop).
+  const int nb_e = nblocks[sid_e];
+  const int kb_e = nl_e <= 0 ? 0 : (nl_e + bs - 1) / bs;
+  const int32_t* trow = tables + (size_t)sid_e * maxb;
+  int tail[kSpecTail];
+#pragma unroll
+  for (int j = 0; j < kSpecTail; ++j) tail[j] = trow[min(kb_e + j, maxb - 1)];
+  const int blk0 = max(s0, 0) / bs;
+  const int nyb = (max(s0, 0) + C - 1) / bs - blk0 + 1;  // blocks the chunk touches
+  int tab = 0;
+  if (tid < nyb) tab = tables[(size_t)sid * maxb + min(blk0 + tid, maxb - 1)];
+  // (only workgroup (b, 0) reads or writes sequence b's length)
+  const int len_own = h == 0 && tid == b ? seq_lens[sid] : 0;
+  const int maxneed = min(B * ((C + bs - 1) / bs + 1), kRaStage);
+  const int nstage = min(top, maxneed);
+  for (int i = tid; i < nstage; i += kRaThreads) s_free[i] = free_stack[top - 1 - i];
+  // The rewind of entry e: truncate to nl_e (kv.py:150-162; nl_e < 0: none).
+  const bool trunc = act && nl_e >= 0;
+  const int ft = trunc ? max(0, nb_e - kb_e) : 0;  // blocks freed: table[kb_e .. nb_e - 1]
+  const int nb1 = nb_e - ft;
+  bool ok = !act || (fin_e == 0 && ft <= kSpecTail);
+#pragma unroll
+  for (int j = 0; j < kSpecTail; ++j)
+    if (j < ft && (unsigned)tail[j] >= (unsigned)cap) ok = false;
+  bool fast = __syncthreads_and(ok);
+  if (fast) {
+    // Round trip 3: a block already free is ignored by the reference's free
+    // (kv.py:73-74); such a batch, or one freeing a block twice, takes the
+    // exact path. The LDS hash finds repeats while the flags travel.
+    int fl[kSpecTail];
+#pragma unroll
+    for (int j = 0; j < kSpecTail; ++j) fl[j] = j < ft ? free_flag[tail[j]] : 0;
+    bool dup = false;
+#pragma unroll
+    for (int j = 0; j < kSpecTail; ++j) {
+      if (j >= ft) continue;
+      unsigned slot = ((unsigned)tail[j] * 2654435761u) & (kRaHash - 1);
+      for (;;) {  // at most kSpecTail * B < kRaHash ids: a free slot exists
+        const int prev = atomicCAS(&s_hash[slot], -1, tail[j]);
+        if (prev == -1) break;
+        if (prev == tail[j]) {
+          dup = true;
+          break;
+        }
+        slot = (slot + 1) & (kRaHash - 1);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kSpecTail; ++j) dup |= fl[j] != 0;
+    fast = !__syncthreads_or(dup);
+  }
+  int poff = 0, aoff = 0, got = 0, top2 = top, consumed = 0;
+  if (fast) {
+    // Pushes: entry e's k-th freed block (table[nb_e - 1 - k]) goes to stack
+    // index top + poff + k.
+    int ptot;
+    poff = block_exclusive_scan(ft, s_scan, &ptot);
+#pragma unroll
+    for (int j = 0; j < kSpecTail; ++j)
+      if (j < ft) s_push[poff + j] = tail[ft - 1 - j];
+    top2 = top + ptot;
+    // The allocation from the rewound state (kv_alloc_kernel's rule).
+    const int want = act ? max(0, (st_e + C - 1) / bs + 1 - nb1) : 0;
+    const int need = min(want, max(0, maxb - nb1));
+    if (need < want) atomicMin(&s_ovf, e);
+    int atot;
+    aoff = block_exclusive_scan(need, s_scan, &atot);
+    got = min(need, max(0, top2 - aoff));
+    if (act && got < need) atomicMin(&s_fail, e);
+    consumed = min(atot, max(top2, 0));
+    if (tid == b) {
+      s_aoff = aoff;
+      s_got = got;
+      s_nb1 = nb1;
+      s_len1 = trunc ? max(0, nl_e) : len_own;  // the rewind's length (kv.py:162)
+    }
+    __syncthreads();
+  }
+  // pos-th entry from the top of the stack after the pushes
+  auto stack_at = [&](int pos) {
+    const int q = top2 - 1 - pos;
+    if (q >= top) return s_push[q - top];
+    const int i = top - 1 - q;
+    return i < nstage ? s_free[i] : free_stack[q];
+  };
+  int n = 0;
+  if (fast) {
+    const int nb1b = s_nb1, gotb = s_got, aoffb = s_aoff;
+    if (tid < nyb) {
+      const int blk = blk0 + tid;
+      s_phys[tid] = blk < nb1b ? tab : (blk < nb1b + gotb ? stack_at(aoffb + blk - nb1b) : -1);
+    }
+    const int fail = s_fail;
+    const int lim = fail < B ? fail : 0x7fffffff;
+    n = (b > lim || s0 < 0) ? 0 : min(C, (nb1b + gotb) * bs - s0);
+  }
+  __syncthreads();
+  // Every workgroup has consumed its loads of the shared state: count it in.
+  int arrived = 0;
+  if (tid == 0) arrived = __hip_atomic_fetch_add(&ctr[CTR_ARRIVE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (fast) {
+    // the rewind's length, then the append's (kv.py:147)
+    if (h == 0 && tid == 0) seq_lens[sid] = n > 0 ? max(s_len1, s0 + n) : s_len1;
+    if (wplan && h == 0) {  // the round's write plan: slot row of each chunk token, or -1
+      for (int o = tid; o < C; o += kRaThreads) {
+        int dest = -1;
+        if (o < n) {
+          const int p = s0 + o, phys = s_phys[p / bs - blk0];
+          if ((unsigned)phys < (unsigned)cap) dest = phys * bs + p % bs;
+        }
+        wplan[(size_t)b * C + o] = dest;
+      }
+    }
+    auto store = [&](int k, const uint4& kv, T vv) {
+      const int ik = tid + k * kRaThreads;
+      if (ik < nk && ik / vec < n) {
+        const int p = s0 + ik / vec, phys = s_phys[p / bs - blk0];
+        if ((unsigned)phys < (unsigned)cap) {
+          uint8_t* kdst = kpool + ((((size_t)layer * cap + phys) * hkv + h) * bs + p % bs) * (size_t)(d * ES);
+          reinterpret_cast<uint4*>(kdst)[ik % vec] = kv;
+        }
+      }
+      const int iv = tid + k * kRaThreads;
+      if (iv < nv && iv / d < n) {
+        const int p = s0 + iv / d, phys = s_phys[p / bs - blk0];
+        if ((unsigned)phys < (unsigned)cap) {
+          T* vdst = reinterpret_cast<T*>(vpool) + (((size_t)layer * cap + phys) * hkv + h) * (size_t)d * bs;
+          vdst[(size_t)(iv % d) * bs + p % bs] = vv;
+        }
+      }
+    };
+    if (n > 0) {
+      store(0, k0, v0);
+      store(1, k1, v1);
+      store(2, k2, v2);
+      store(3, k3, v3);
+    }
+  }
+  if (tid == 0) s_flag = arrived + 1 == (int)gridDim.x;
+  __syncthreads();
+  if (!s_flag) return;
+  if (fast) {
+    // The last workgroup writes the commit's and the allocation's state, entry
+    // e per thread (its registers hold entry e's rewind and allocation).
+    const int final_top = top2 - consumed;
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < kSpecTail; ++j) {
+        if (j < ft) {
+          const int q = top + poff + j, id = s_push[poff + j];
+          free_stack[q] = id;
+          if (q < final_top) free_flag[id] = 1;  // (a pushed block popped again stays allocated)
+        }
+      }
+      for (int t = 0; t < got; ++t) {
+        const int id = stack_at(aoff + t);
+        tables[(size_t)sid_e * maxb + nb1 + t] = id;
+        free_flag[id] = 0;
+      }
+      nblocks[sid_e] = nb1 + got;
+    }
+    if (tid == 0) {
+      const int fail = s_fail, ovf = s_ovf;
+      ctr[CTR_ARRIVE] = 0;
+      ctr[CTR_TOP] = final_top;
+      ctr[CTR_PUSHED] = top2 - top;
+      ctr[CTR_EXHAUSTED] = fail < B ? fail + 1 : 0;
+      if (ovf < B) ctr[CTR_OVERFLOW] = ovf + 1;
+    }
+    return;
+  }
+  // The exact path: nothing has been written; rewind, allocate and copy here.
+  if (tid == 0) ctr[CTR_ARRIVE] = 0;
+  rewind_wg(tables, maxb, nblocks, seq_lens, free_stack, free_flag, ctr, seq_ids, new_len, finished, B, bs, 0, cap);
+  __syncthreads();
+  alloc_wg(tables, maxb, nblocks, free_stack, free_flag, ctr, seq_ids, start, B, C, bs, nullptr, 0, cap);
+  __syncthreads();
+  const int ex = ctr[CTR_EXHAUSTED];
+  const int lim = ex ? ex - 1 : 0x7fffffff;
+  for (int t = tid; t < B * C; t += kRaThreads) {
+    const int bb = t / C, o = t - bb * C;
+    const int sb = seq_ids[bb], st = start[bb];
+    const int nn = (bb > lim || st < 0) ? 0 : min(C, nblocks[sb] * bs - st);
+    int dest = -1;
+    if (o < nn) {
+      const int p = st + o, phys = tables[(size_t)sb * maxb + p / bs];
+      if ((unsigned)phys < (unsigned)cap) dest = phys * bs + p % bs;
+    }
+    if (wplan) wplan[t] = dest;
+    if (o == 0 && nn > 0 && seq_lens[sb] < st + nn) seq_lens[sb] = st + nn;
+    if (dest < 0) continue;
+    const int phys = dest / bs, r = dest - phys * bs;
+    for (int hh = 0; hh < hkv; ++hh) {
+      const size_t src = ((size_t)bb * C + o) * row_elems + (size_t)hh * d;
+      const size_t slot = ((size_t)layer * cap + phys) * hkv + hh;
+      T* kd = reinterpret_cast<T*>(kpool) + (slot * bs + r) * (size_t)d;
+      T* vd = reinterpret_cast<T*>(vpool) + slot * (size_t)d * bs + r;
+      for (int x = 0; x < d; ++x) {
+        kd[x] = reinterpret_cast<const T*>(knew)[src + x];
+        vd[(size_t)x * bs] = reinterpret_cast<const T*>(vnew)[src + x];
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ draft alignment
@@ -1526,6 +1829,50 @@ int spv_kv_rewind(int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* nu
                      finished, n, block_size, shrink_only, capacity);
   SPV_CHECK_LAUNCH();
   return SPV_OK;
+}
+
+int spv_kv_rewind_append(void* k_pool, void* v_pool, int kv_dtype, const void* k_new, const void* v_new,
+                         int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,
+                         int32_t* free_stack, int32_t* free_flag, int32_t* ctr, const int32_t* seq_ids,
+                         const int32_t* new_len, const int32_t* finished, const int32_t* start_pos, int32_t B,
+                         int32_t C, int32_t layer, int32_t capacity, int32_t block_size, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t* write_plan, void* stream) {
+  const int es = dtype_size(kv_dtype);
+  if (!k_pool || !v_pool || !k_new || !v_new || !block_tables || !num_blocks || !seq_lens || !free_stack ||
+      !free_flag || !ctr || !seq_ids || !start_pos || es == 0 || kv_dtype == SPV_FP8E4M3)
+    return SPV_ERR_ARG;
+  if (B < 0 || C < 1 || layer < 0 || capacity < 1 || block_size < 1 || num_kv_heads < 1 || head_dim < 1 ||
+      max_blocks_per_seq < 1)
+    return SPV_ERR_ARG;
+  if (write_plan && (long long)capacity * block_size > 0x7fffffffLL) return SPV_ERR_ARG;  // int32 plan rows
+  if ((C + block_size - 1) / block_size + 1 > 65535) return SPV_ERR_ARG;
+  if (B == 0) return SPV_OK;
+  const bool vec16 = (head_dim * es) % 16 == 0;
+  if (vec16 && B <= kRaThreads && (C + block_size - 1) / block_size + 1 <= kFusedMaxBlocks &&
+      C * head_dim <= kRaItems * kRaThreads && C * (head_dim * es / 16) <= kRaItems * kRaThreads) {
+    hipStream_t s = (hipStream_t)stream;
+    auto* kp = static_cast<uint8_t*>(k_pool);
+    auto* vp = static_cast<uint8_t*>(v_pool);
+    auto* kn = static_cast<const uint8_t*>(k_new);
+    auto* vn = static_cast<const uint8_t*>(v_new);
+#define SPV_RA(ES)                                                                                               \
+  hipLaunchKernelGGL(kv_rewind_append_kernel<ES>, dim3(B * num_kv_heads), dim3(kRaThreads), 0, s, kp, vp, kn, vn, \
+                     block_tables, max_blocks_per_seq, num_blocks, seq_lens, free_stack, free_flag, ctr, seq_ids,  \
+                     new_len, finished, start_pos, B, C, layer, capacity, block_size, num_kv_heads, head_dim,      \
+                     write_plan)
+    if (es == 4) SPV_RA(4);
+    else SPV_RA(2);
+#undef SPV_RA
+    SPV_CHECK_LAUNCH();
+    return SPV_OK;
+  }
+  // Shapes the one launch does not take: the two calls.
+  const int rc = spv_kv_rewind(block_tables, max_blocks_per_seq, num_blocks, seq_lens, free_stack, free_flag, ctr,
+                               seq_ids, new_len, finished, B, capacity, block_size, 0, stream);
+  if (rc != SPV_OK) return rc;
+  return kv_append_impl(k_pool, v_pool, kv_dtype, k_new, v_new, block_tables, max_blocks_per_seq, num_blocks,
+                        seq_lens, free_stack, free_flag, ctr, seq_ids, start_pos, B, C, layer, capacity, block_size,
+                        num_kv_heads, head_dim, 1, -1, write_plan, stream);
 }
 
 int spv_kv_draft_align(int32_t* block_tables, int32_t max_blocks_per_seq, int32_t* num_blocks, int32_t* seq_lens,

@@ -53,6 +53,7 @@ SIGNATURES = {
     "spv_kv_write_planned": (I, [P, P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "spv_kv_append_fp8": (I, [P, P, P, I, P, P, P, I, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "spv_kv_rewind": (I, [P, I, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "spv_kv_rewind_append": (I, [P, P, I, P, P, P, I, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, P]),
     "spv_kv_draft_align": (I, [P, I, P, P, P, P, P, P, I, P, P, P, P, P, I, P, P, P, I, I, I, P]),
     "spv_pool_metrics": (I, [P, P, I, I, P, P, I, P, P, P]),
     "spv_kv_gather": (I, [P, P, I, P, P, I, I, I, I, I, I, I, I, P, P]),

@@ -480,6 +480,43 @@ class PagedKVCache:
         self._stale = True
         self.allocator._stale = True
 
+    def rewind_append_device(self, seq_ids: torch.Tensor, new_lens: Optional[torch.Tensor],
+                             finished: Optional[torch.Tensor], start_positions: torch.Tensor,
+                             k_new: torch.Tensor, v_new: torch.Tensor, layer: int = 0,
+                             plan: Optional["WritePlan"] = None) -> None:
+        """``rewind_device(seq_ids, new_lens, finished)`` followed by the allocating
+        ``write_block_device(layer, seq_ids, start_positions, k_new, v_new, plan=plan)``
+        of the same batch, in one launch (``spv_kv_rewind_append``).
+
+        The commit of one round (engine/spec_scheduler.py:296-322) meets the next
+        round's first-layer append (engine/model.py:184-187) when no request is
+        admitted in between. Tables, lengths, free list, stored keys and values
+        and the write plan equal the two calls' results in every case. No host
+        sync; distinct, added sequence ids; not for fp8 pools.
+        """
+        if self.fp8:
+            raise ValueError("rewind_append_device does not take fp8 pools; use rewind_device + write_block_device")
+        if not 0 <= int(layer) < self.num_layers:
+            raise IndexError("layer {} out of range".format(layer))
+        B, chunk = int(k_new.shape[0]), int(k_new.shape[1])
+        if B == 0:
+            return
+        k_new, v_new = self._new_kv(k_new, v_new)
+        rows = None
+        if plan is not None and self._plannable(chunk):
+            plan._reserve(B, chunk, self.device)
+            rows = plan.rows
+        a = self.allocator
+        call("spv_kv_rewind_append", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
+             ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
+             ptr(a.free_stack), ptr(a.free_flag), ptr(a.ctr), ptr(seq_ids), ptr(new_lens), ptr(finished),
+             ptr(start_positions), B, chunk, int(layer), a.capacity, self.block_size, self.num_kv_heads,
+             self.head_dim, ptr(rows), self._stream())
+        if rows is not None:
+            plan.ready = True
+        self._stale = True
+        self.allocator._stale = True
+
     def align_device(self, seq_ids: torch.Tensor, start_pos: torch.Tensor, n_commit: torch.Tensor,
                      finished: torch.Tensor, chunk_tokens: torch.Tensor, catch_n: torch.Tensor,
                      catch_pos: torch.Tensor, catch_tok: torch.Tensor, max_len: Optional[int] = None) -> None:

@@ -54,6 +54,8 @@ def test_argument_validation_needs_no_gpu(lib):
     ARG = _hip.SPV_ERR_ARG
     assert lib.spv_pool_init(None, None, None, 8, None) == ARG
     assert lib.spv_kv_rewind(None, 1, None, None, None, None, None, None, None, None, 1, 8, 16, 0, None) == ARG
+    assert lib.spv_kv_rewind_append(None, None, 1, None, None, None, 4, None, None, None, None, None, None, None,
+                                    None, None, 1, 1, 0, 8, 16, 2, 8, None, None) == ARG
     assert lib.spv_kv_append(None, None, 1, None, None, None, 4, None, None, None, None, None, None,
                              None, 1, 1, 0, 8, 16, 2, 8, 1, 1, None) == ARG
     assert lib.spv_verify_sample(None, None, 0, 1.0, None, None, None, None, None, -1, 1, 5, 8,
