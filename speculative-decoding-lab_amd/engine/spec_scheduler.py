@@ -245,6 +245,14 @@ class VerifyStep:
     after the first layer's append allocated the round's blocks), samples, and
     rewinds the pool on the device with the sampled lengths. Nothing
     synchronises with the host.
+
+    ``sample_and_commit(..., apply=False)`` holds the round's commit instead:
+    the next ``attend_layers`` over the same sequence ids (same order) applies
+    it together with its first layer's append in one launch
+    (``rewind_append_device``: the two calls' exact result). Any other batch, or
+    ``flush()``, applies it on its own first. Until then the pool still holds
+    the round's uncommitted tail, so a caller that reads or changes the pool
+    between rounds (admission, metrics) calls ``flush()`` first.
     """
 
     def __init__(self, kv: PagedKVCache, gamma: int, temperature: float, eos_id: Optional[int] = None):
@@ -253,6 +261,14 @@ class VerifyStep:
         self.temperature = float(temperature)
         self.eos_id = eos_id
         self._write_plan = WritePlan()  # the round's rows, recorded by its first layer's append
+        self._pending = None  # (sequence ids, their VerifyResult): a commit not yet applied
+
+    def flush(self) -> None:
+        """Apply a held commit (``sample_and_commit(..., apply=False)``)."""
+        if self._pending is not None:
+            sids, res = self._pending
+            self._pending = None
+            self.kv.rewind_device(_hip.i32(sids, self.kv.device), res.new_len, res.finished)
 
     def attend_layers(self, seq_ids: Sequence[int], start_positions: Sequence[int],
                       q_layers: Sequence[torch.Tensor], k_layers: Sequence[torch.Tensor],
@@ -276,14 +292,26 @@ class VerifyStep:
                 e.record()
                 events.append(e)
 
+        pending = None
+        if self._pending is not None:
+            if list(self._pending[0]) == [int(s) for s in seq_ids] and not self.kv.fp8:
+                pending = self._pending[1]
+                self._pending = None
+            else:
+                self.flush()
         plan = None
         for layer in range(len(q_layers)):
             mark()
-            # the first layer's call allocates the chunk's blocks for every layer
-            # (and records where its tokens went: the later layers copy by that plan)
-            self.kv.write_block_device(layer, sid_t, st_t, k_layers[layer].to(self.kv.dtype).contiguous(),
-                                       v_layers[layer].to(self.kv.dtype).contiguous(), alloc=layer == 0,
-                                       plan=self._write_plan)
+            kl = k_layers[layer].to(self.kv.dtype).contiguous()
+            vl = v_layers[layer].to(self.kv.dtype).contiguous()
+            if layer == 0 and pending is not None:
+                # the previous round's commit, then this round's allocating append: one launch
+                self.kv.rewind_append_device(sid_t, pending.new_len, pending.finished, st_t, kl, vl,
+                                             layer=0, plan=self._write_plan)
+            else:
+                # the first layer's call allocates the chunk's blocks for every layer
+                # (and records where its tokens went: the later layers copy by that plan)
+                self.kv.write_block_device(layer, sid_t, st_t, kl, vl, alloc=layer == 0, plan=self._write_plan)
             if plan is None:  # the round's attention plan, once its blocks exist
                 plan = VerifyPlan(self.kv, sid_t, st_t, chunk, int(q_layers[layer].shape[2]), max_ctx)
             mark()
@@ -295,14 +323,20 @@ class VerifyStep:
     def sample_and_commit(self, seq_ids: Sequence[int], start_positions: Sequence[int],
                           target_logits: torch.Tensor, draft_logits: torch.Tensor,
                           proposals: torch.Tensor, u: torch.Tensor, noise: Optional[torch.Tensor],
-                          remaining: Optional[Sequence[int]] = None) -> VerifyResult:
+                          remaining: Optional[Sequence[int]] = None, apply: bool = True) -> VerifyResult:
+        """Fused accept / resample / bonus and the commit cut; then the pool's
+        rewind, or (``apply=False``) the commit held for the next round."""
+        self.flush()
         dev = self.kv.device
         sid_t = _hip.i32(seq_ids, dev)
         st_t = _hip.i32(start_positions, dev)
         rem_t = None if remaining is None else _hip.i32(remaining, dev)
         res = verify_sample(target_logits, draft_logits, proposals, u, noise, self.temperature,
                             start_pos=st_t, remaining=rem_t, eos_id=self.eos_id, validate=False)
-        self.kv.rewind_device(sid_t, res.new_len, res.finished)
+        if apply:
+            self.kv.rewind_device(sid_t, res.new_len, res.finished)
+        else:
+            self._pending = ([int(s) for s in seq_ids], res)
         return res
 
 

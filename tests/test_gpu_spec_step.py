@@ -5,6 +5,9 @@ VerifyStep`` and, in lockstep, through the oracle (per-token writes, masked SDPA
 per sequence, batch_accept on the same noise, the reference's commit rule).
 After every round the pool state (tables, lengths, free list) must be identical
 and the attention outputs within the fp32 tolerance of the reference's tests.
+With the commit held (``apply=False``) each round's commit goes with the next
+round's first append (one launch, or on its own once the batch changes): the
+pool must then equal the oracle's after every append, and after the last flush.
 """
 
 from __future__ import annotations
@@ -22,7 +25,8 @@ from oracle.spec_step import SeqState, commit_round
 pytestmark = pytest.mark.gpu
 
 
-def test_verify_rounds_match_oracle(cuda):
+@pytest.mark.parametrize("defer", [False, True])
+def test_verify_rounds_match_oracle(cuda, defer):
     torch.manual_seed(0)
     B, gamma, Hq, Hkv, d, bs, V, cap = 5, 3, 4, 2, 16, 4, 32, 96
     C = gamma + 1
@@ -52,6 +56,10 @@ def test_verify_rounds_match_oracle(cuda):
         v = torch.randn(n, C, Hkv, d, generator=g)
         out = step.attend_layers(sids, starts, [q.to(cuda)], [k.to(cuda)], [v.to(cuda)])[0]
         cpu.write_block(0, sids, starts, k, v)
+        if defer:  # the previous commit and this append are applied now
+            assert gpu.block_tables == cpu.block_tables
+            assert gpu.seq_lengths == cpu.seq_lengths
+            assert gpu.allocator.free_list() == cpu.allocator.free_list
         want = ref_attn.paged_attention_extend(q, cpu, 0, sids, starts, Hq)
         assert torch.allclose(out.cpu(), want, atol=1e-5, rtol=1e-5)
         target = torch.randn(n, C, V, generator=g) * 2
@@ -61,11 +69,17 @@ def test_verify_rounds_match_oracle(cuda):
         noise = torch.empty(n, V).exponential_(1, generator=g)
         remaining = [s.max_new_tokens - len(s.generated) for s in running]
         res = step.sample_and_commit(sids, starts, target.to(cuda), draft.to(cuda), x.to(cuda),
-                                     u.to(cuda), noise.to(cuda), remaining)
+                                     u.to(cuda), noise.to(cuda), remaining, apply=not defer)
         acc = S.verify_from_logits(target, draft, x, u, noise, 1.0)
         assert res.accepted_lists() == acc
         ks = commit_round(running, {s: a for s, a in zip(sids, acc)}, cpu)
         assert res.n_commit.tolist() == ks
+        if defer:
+            continue
         assert gpu.block_tables == cpu.block_tables
         assert gpu.seq_lengths == cpu.seq_lengths
         assert gpu.allocator.free_list() == cpu.allocator.free_list
+    step.flush()
+    assert gpu.block_tables == cpu.block_tables
+    assert gpu.seq_lengths == cpu.seq_lengths
+    assert gpu.allocator.free_list() == cpu.allocator.free_list
