@@ -271,3 +271,35 @@ def test_fp8_pool_is_refused(cuda):
     k = torch.zeros(1, 2, 2, 64, device=cuda)
     with pytest.raises(ValueError):
         kv.rewind_append_device(t, t, t, t, k, k)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_rounds_match_two_calls_and_oracle(cuda, seed):
+    """Seeded random rounds over a small pool: lengths shrink and grow, some
+    sequences finish (and start again from 0), starts are the committed lengths
+    or not, blocks of 2 to 16, chunks of 1 to 9; a round whose append runs the
+    pool out is checked and the trace restarts from a fresh pool."""
+    rng = random.Random(1000 + seed)
+    bs = rng.choice([2, 4, 16])
+    C = rng.randint(1, 9)
+    H, d, B = rng.choice([1, 2]), rng.choice([64, 128]), rng.randint(1, 40)
+    cap = rng.randint(B * 2, B * (-(-(300 + 2 * C) // bs)) + 8)
+    dtype = rng.choice([torch.bfloat16, torch.float32])
+    g = torch.Generator(device=cuda).manual_seed(seed)
+    pools = _pools(cuda, H, d, cap, bs, dtype, B, maxb=-(-(300 + 4 * C) // bs) + 2)
+    lens = [0] * B
+    for rnd in range(8):
+        sids = rng.sample(range(B), rng.randint(1, B))
+        new_lens = [max(-1, lens[s] + rng.randint(-40, 2 * C)) if rng.random() < 0.8 else -1 for s in sids]
+        fin = [1 if rng.random() < 0.1 else 0 for _ in sids]
+        after = [0 if f else (nl if nl >= 0 else lens[s]) for s, nl, f in zip(sids, new_lens, fin)]
+        starts = [a if rng.random() < 0.7 else max(0, a - rng.randint(0, C)) for a in after]
+        starts = [min(x, 300) for x in starts]
+        k = torch.randn(len(sids), C, H, d, generator=g, device=cuda).to(dtype)
+        v = torch.randn(len(sids), C, H, d, generator=g, device=cuda).to(dtype)
+        ex = _round(cuda, pools, sids, new_lens, fin, starts, k, v)
+        _check(pools, exhausted=ex)
+        if ex:
+            return
+        for s, a, st in zip(sids, after, starts):
+            lens[s] = max(a, st + C)
