@@ -499,6 +499,13 @@ class PagedKVCache:
         if not 0 <= int(layer) < self.num_layers:
             raise IndexError("layer {} out of range".format(layer))
         B, chunk = int(k_new.shape[0]), int(k_new.shape[1])
+        shape = (B, chunk, self.num_kv_heads, self.head_dim)
+        if tuple(k_new.shape) != shape or tuple(v_new.shape) != shape:
+            raise ValueError("k/v must have shape {}".format(shape))
+        for name, t in (("seq_ids", seq_ids), ("start_positions", start_positions), ("new_lens", new_lens),
+                        ("finished", finished)):
+            if t is not None and (t.dtype != torch.int32 or t.numel() != B or t.device != self.device):
+                raise ValueError("{} must be {} int32 entries on {}".format(name, B, self.device))
         if B == 0:
             return
         k_new, v_new = self._new_kv(k_new, v_new)

@@ -303,3 +303,19 @@ def test_random_rounds_match_two_calls_and_oracle(cuda, seed):
             return
         for s, a, st in zip(sids, after, starts):
             lens[s] = max(a, st + C)
+
+
+def test_mismatched_inputs_are_refused(cuda):
+    kv = PagedKVCache(1, 2, 64, 32, 16, cuda, torch.bfloat16)
+    kv.add_sequence(0)
+    kv.add_sequence(1)
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=cuda)  # noqa: E731
+    k = torch.zeros(2, 3, 2, 64, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):  # one start for two sequences
+        kv.rewind_append_device(i32([0, 1]), None, None, i32([0]), k, k)
+    with pytest.raises(ValueError):  # int64 new lengths
+        kv.rewind_append_device(i32([0, 1]), torch.zeros(2, dtype=torch.int64, device=cuda), None, i32([0, 0]), k, k)
+    with pytest.raises(ValueError):  # wrong head count
+        kv.rewind_append_device(i32([0, 1]), None, None, i32([0, 0]), k[:, :, :1], k[:, :, :1])
+    kv.rewind_append_device(i32([0, 1]), None, None, i32([0, 0]), k, k)
+    assert kv.seq_lengths == [3, 3]
