@@ -56,6 +56,10 @@ def test_argument_validation_needs_no_gpu(lib):
     assert lib.spv_kv_rewind(None, 1, None, None, None, None, None, None, None, None, 1, 8, 16, 0, None) == ARG
     assert lib.spv_kv_rewind_append(None, None, 1, None, None, None, 4, None, None, None, None, None, None, None,
                                     None, None, 1, 1, 0, 8, 16, 2, 8, None, None) == ARG
+    # an fp8 pool is refused before anything is launched (no device memory is touched)
+    fake = ctypes.c_void_p(16)
+    assert lib.spv_kv_rewind_append(fake, fake, _hip.SPV_FP8E4M3, fake, fake, fake, 4, fake, fake, fake, fake,
+                                    fake, fake, None, None, fake, 1, 1, 0, 8, 16, 2, 64, None, None) == ARG
     assert lib.spv_kv_append(None, None, 1, None, None, None, 4, None, None, None, None, None, None,
                              None, 1, 1, 0, 8, 16, 2, 8, 1, 1, None) == ARG
     assert lib.spv_verify_sample(None, None, 0, 1.0, None, None, None, None, None, -1, 1, 5, 8,
