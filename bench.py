@@ -89,9 +89,16 @@ def attention_bytes(lens, chunk=C, hq=HQ, hkv=HKV, d=D, bs=BS):
     return total
 
 
-def sample_bytes(batch):
-    """Algorithmic bytes of one fused sampling call (T > 0)."""
-    return batch * ((C + GAMMA) * VOCAB * 4 + VOCAB * 4 + GAMMA * 8 + 12)
+def sample_bytes(batch, draft_stats=True):
+    """Algorithmic bytes of one fused sampling call (T > 0): per sequence the
+    target rows, the noise row and the raced draft row (a rejection), the
+    uniforms, proposals and the draft entries at them, and the start / outputs.
+    Without the draft rows' statistics (kept by the draft sampler that drew
+    the proposals) every draft row is read in full as well."""
+    if not draft_stats:
+        return batch * ((C + GAMMA) * VOCAB * 4 + VOCAB * 4 + GAMMA * 8 + 12)
+    # target rows, noise row, raced draft row; per position u, proposal, q[x], (max, sum)
+    return batch * ((C + 2) * VOCAB * 4 + GAMMA * 20 + 12)
 
 
 def workload_lens(seed=0):
@@ -188,13 +195,20 @@ def build_workload(dev, seed=0):
         "max_ctx": [max(lens) + C for lens in rlens],
         "logits": [],
     }
+    from engine.spec_scheduler import draft_sample
+
     for _ in range(LOGIT_SETS):
         target = torch.randn(B, C, VOCAB, generator=gd, device=dev) * 2.0
-        draft = target[:, :GAMMA] + torch.randn(B, GAMMA, VOCAB, generator=gd, device=dev)
-        probs_q = torch.softmax(draft, dim=-1)
-        proposals = torch.multinomial(probs_q.reshape(-1, VOCAB), 1, generator=gd).reshape(B, GAMMA)
-        w["logits"].append((target.contiguous(), draft.contiguous(), proposals.to(torch.int32)))
-        del probs_q
+        draft = (target[:, :GAMMA] + torch.randn(B, GAMMA, VOCAB, generator=gd, device=dev)).contiguous()
+        # the draft side: each draft step draws the batch's proposals from its
+        # logits and keeps the rows' softmax statistics (spec_scheduler.py:243-252)
+        proposals = torch.empty(B, GAMMA, dtype=torch.int32, device=dev)
+        dstats = torch.empty(B, GAMMA, 2, dtype=torch.float32, device=dev)
+        for j in range(GAMMA):
+            dn = torch.empty(B, VOCAB, device=dev).exponential_(1, generator=gd)
+            draft_sample(draft[:, j], 1.0, dn, out=proposals[:, j], stats=dstats[:, j])
+            del dn
+        w["logits"].append((target.contiguous(), draft, proposals, dstats))
     w["u"] = torch.rand(B, GAMMA, generator=gd, device=dev)
     w["noise"] = torch.empty(B, VOCAB, device=dev).exponential_(1, generator=gd)
     w["attn_out"] = torch.empty_like(w["q"])
@@ -226,10 +240,11 @@ def make_step(w):
         verify_attention(w["q"], kv, 0, w["sids"][r], w["start"][r], w["max_ctx"][r], out=w["attn_out"],
                          plan=plans[r])
 
-    def sample(t, r=0):
-        target, draft, proposals = w["logits"][t]
+    def sample(t, r=0, own_stats=False):
+        target, draft, proposals, dstats = w["logits"][t]
         verify_sample(target, draft, proposals, w["u"], w["noise"], 1.0,
-                      start_pos=w["start"][r], result=results[r], validate=False)
+                      start_pos=w["start"][r], result=results[r], validate=False,
+                      draft_stats=None if own_stats else dstats)
 
     def rewind(r):
         kv.rewind_device(w["sids"][r], results[r].new_len, results[r].finished)
@@ -375,8 +390,9 @@ def cpu_baseline(w, dev, budget_s=12.0):
     repeat_interleave + masked SDPA per sequence, logits_to_probs of every row
     and batch_accept with a live generator, and the commit's tail-first
     truncate with the free list's membership scan. Replica 0 of the workload,
-    fp32 K/V. ``value`` is the attention part in GB/s of the same algorithmic
-    bytes as the GPU headline."""
+    bf16 K/V and queries as on the GPU (and once with fp32 K/V on all threads).
+    ``value`` is the attention part in GB/s of the same algorithmic bytes as the
+    GPU headline."""
     import torch
 
     from oracle import attention as ref_attn
@@ -384,24 +400,25 @@ def cpu_baseline(w, dev, budget_s=12.0):
     from oracle import sampler as S
 
     lens = w["lens"]
-    cpu = ref.PagedKVCache(1, HKV, D, CAP, BS, dtype=torch.float32)
-    cpu.load_state(w["tables0"], lens, w["free"])
-    for s, L in enumerate(lens):
-        k, v = w["keys"][s].float().cpu(), w["values"][s].float().cpu()
-        for bi, phys in enumerate(w["tables0"][s]):
-            n = min(BS, L - bi * BS)
-            cpu.k[0, phys, :n] = k[bi * BS: bi * BS + n]
-            cpu.v[0, phys, :n] = v[bi * BS: bi * BS + n]
-    k_new = w["k_new"].float().cpu()
-    v_new = w["v_new"].float().cpu()
-    q = w["q"].float().cpu()
-    target, draft, proposals = (x.cpu() for x in w["logits"][0])
+    target, draft, proposals, _ = (x.cpu() for x in w["logits"][0])
     props = proposals.tolist()
     sids = list(range(B))
     nbytes = attention_bytes(lens)
     gen = torch.Generator().manual_seed(1234)
 
-    def one_step():
+    def pool(dtype):
+        """The oracle's pool of replica 0 in ``dtype`` (the GPU pool's bf16 values, exact in fp32)."""
+        cpu = ref.PagedKVCache(1, HKV, D, CAP, BS, dtype=dtype)
+        cpu.load_state(w["tables0"], lens, w["free"])
+        for s, L in enumerate(lens):
+            k, v = w["keys"][s].to(dtype).cpu(), w["values"][s].to(dtype).cpu()
+            for bi, phys in enumerate(w["tables0"][s]):
+                n = min(BS, L - bi * BS)
+                cpu.k[0, phys, :n] = k[bi * BS: bi * BS + n]
+                cpu.v[0, phys, :n] = v[bi * BS: bi * BS + n]
+        return cpu, w["k_new"].to(dtype).cpu(), w["v_new"].to(dtype).cpu(), w["q"].to(dtype).cpu()
+
+    def one_step(cpu, k_new, v_new, q):
         t = [time.perf_counter()]
         cpu.write_block(0, sids, lens, k_new, v_new)
         t.append(time.perf_counter())
@@ -417,12 +434,12 @@ def cpu_baseline(w, dev, budget_s=12.0):
         t.append(time.perf_counter())
         return [b - a for a, b in zip(t, t[1:])]
 
-    def run(threads, budget):
+    def run(args_, threads, budget):
         torch.set_num_threads(threads)
-        one_step()  # warm-up
+        one_step(*args_)  # warm-up
         rows, t_end = [], time.perf_counter() + budget
         while (time.perf_counter() < t_end or len(rows) < 3) and len(rows) < 200:
-            rows.append(one_step())
+            rows.append(one_step(*args_))
         med = [sorted(r[i] for r in rows)[len(rows) // 2] for i in range(4)]
         step_s = sorted(sum(r) for r in rows)[len(rows) // 2]
         return {
@@ -433,23 +450,29 @@ def cpu_baseline(w, dev, budget_s=12.0):
         }
 
     threads = os.cpu_count() or 1
-    allc = run(threads, budget_s * 0.6)
-    one = run(1, budget_s * 0.4)
+    bf16 = pool(torch.bfloat16)
+    allc = run(bf16, threads, budget_s * 0.45)
+    one = run(bf16, 1, budget_s * 0.25)
+    del bf16
+    f32 = run(pool(torch.float32), threads, budget_s * 0.3)
     torch.set_num_threads(threads)
     return {
         "value": allc["attn_gbs"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": "the oracle's whole verify step on replica 0 of the workload (32 sequences, 1 layer, fp32 K/V): "
-                  "per-token write loop, per-block gather + repeat_interleave + masked SDPA per sequence, "
-                  "softmax of all 352 logits rows + batch_accept with a live generator, tail-first truncate with "
-                  "the free-list scan over ~30k free blocks; medians of {} runs on {} threads and {} runs on 1 "
-                  "thread. value = the attention part in GB/s".format(allc["runs"], threads, one["runs"]),
+        "sample": "the oracle's whole verify step on replica 0 of the workload (32 sequences, 1 layer, bf16 K/V and "
+                  "queries as on the GPU): per-token write loop, per-block gather + repeat_interleave + masked SDPA "
+                  "per sequence, softmax of all 352 logits rows + batch_accept with a live generator, tail-first "
+                  "truncate with the free-list scan over ~30k free blocks; medians of {} runs on {} threads and {} "
+                  "runs on 1 thread (and {} runs with fp32 K/V on {} threads). value = the attention part in "
+                  "GB/s of bf16 bytes".format(allc["runs"], threads, one["runs"], f32["runs"], threads),
         "spec_step_us_per_seq": allc["spec_step_us_per_seq"],
         "parts_ms": allc["parts_ms"],
         "one_thread": {"value": one["attn_gbs"], "spec_step_us_per_seq": one["spec_step_us_per_seq"],
                        "parts_ms": one["parts_ms"]},
+        "fp32_kv": {"value": f32["attn_gbs"], "spec_step_us_per_seq": f32["spec_step_us_per_seq"],
+                    "parts_ms": f32["parts_ms"]},
     }
 
 
@@ -836,6 +859,9 @@ def main() -> int:
     del g_plan
     g_smp = graph_of(lambda: [parts["sample"](i % LOGIT_SETS, i % REPLICAS) for i in range(reps)], 1, torch)
     part_us["sample"] = time_graph(g_smp, 5, torch) * 1000.0 / reps
+    g_own = graph_of(lambda: [parts["sample"](i % LOGIT_SETS, i % REPLICAS, True) for i in range(reps)], 1, torch)
+    part_us["sample_own_draft_stats"] = time_graph(g_own, 5, torch) * 1000.0 / reps
+    del g_own
     g_ra = graph_of(lambda: [parts["rewind_append"](i % REPLICAS) for i in range(reps)], 1, torch)
     part_us["append_rewind"] = time_graph(g_ra, 5, torch) * 1000.0 / reps
     del g_ra
@@ -849,7 +875,7 @@ def main() -> int:
     fres = _new_result(B, GAMMA, dev)
     for name, tk, tp in (("sample_top_k50", 50, 1.0), ("sample_top_p0.9", 0, 0.9)):
         def filtered(i, tk=tk, tp=tp):
-            target, draft, proposals = w["logits"][i % LOGIT_SETS]
+            target, draft, proposals, _ = w["logits"][i % LOGIT_SETS]
             verify_sample(target, draft, proposals, w["u"], w["noise"], 1.0, start_pos=w["start"][0], result=fres,
                           validate=False, top_k=tk, top_p=tp)
         g_f = graph_of(lambda: [filtered(i) for i in range(4)], 1, torch)
@@ -865,6 +891,7 @@ def main() -> int:
     lens = w["lens"]
     all_lens = [L for r in rl for L in r]
     samp_gbs = sample_bytes(B) / (part_us["sample"] * 1e-6) / 1e9
+    samp_own_gbs = sample_bytes(B, False) / (part_us["sample_own_draft_stats"] * 1e-6) / 1e9
     accept = res.accept_len.float().mean().item()
 
     line = {
@@ -903,6 +930,8 @@ def main() -> int:
         "graph_spec_step_us_per_seq": round(graph_ms_per_step * 1000.0 / B, 3),
         "parts_us": {k: round(v, 2) for k, v in part_us.items()},
         "sample_gbs": round(samp_gbs, 1),
+        "sample_bytes": sample_bytes(B),
+        "sample_own_draft_stats_gbs": round(samp_own_gbs, 1),
         "mean_ctx": round(sum(all_lens) / len(all_lens), 1),
         "mean_accepted_drafts": round(accept, 3),
         "roofline": {

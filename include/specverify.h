@@ -396,6 +396,16 @@ int spv_prefill_attn(void* out, const void* q, const void* k, const void* v,
 #define SPV_SAMPLE_COUNTER_BYTES (1 << 19)
 size_t spv_verify_sample_workspace_bytes(int32_t B, int32_t gamma, int32_t V);
 
+/* Bits of a sequence's flag word (spv_verify_sample, spv_draft_sample). Given
+ * logits, this library forms p and q with its own fp32 softmax, which sits
+ * within a few 1e-6 of torch's; a flag marks a result that the reference,
+ * computing its own softmax, may have decided the other way. Unflagged
+ * results are the reference's. Given probabilities nothing but the draw's
+ * rounding is left (a re-raced draw within a few ulp of another key). */
+#define SPV_FLAG_ACCEPT_BAND 1 /* an examined u lay inside the error band of min(1, p/q) */
+#define SPV_FLAG_DRAW_BAND 2   /* the drawn token's key is within the keys' error bound of another key's */
+#define SPV_FLAG_TOP_P_BAND 4  /* (host) a filtered row's nucleus boundary is within rounding */
+
 /* One fused verify-sampling step: logits_to_probs (specdec/sampler.py:19-36)
  * on every row, then batch_accept (engine/spec_scheduler.py:46-88) with
  * acceptance_probability (specdec/sampler.py:86-92), residual_distribution
@@ -408,22 +418,29 @@ size_t spv_verify_sample_workspace_bytes(int32_t B, int32_t gamma, int32_t V);
  *     is accepted iff (double)u < acceptance probability; exp_noise (B, V) fp32
  *     Exp(1) variates for the one race per sequence (read only when sampling;
  *     must be finite and > 0);
+ *   draft_stats (B, gamma) float2 or NULL (logits only): the draft rows'
+ *     statistics as spv_draft_sample wrote them at the same temperature (the
+ *     draft loop keeps q's normaliser, spec_scheduler.py:243-252); the draft
+ *     rows are then read only at the proposals and at the raced row;
  *   start_pos / remaining (B) int32 or NULL, eos_id (-1 = none): commit cut.
  * Outputs (device, may be NULL except accept_len/out_tokens):
  *   accept_len[B] drafts accepted, out_tokens[B][gamma+1] (-1 padded),
  *   n_commit[B], finished[B] (budget or eos; 1 also when n_commit == 0),
  *   new_len[B] = start + n_commit, or -1 when n_commit == 0 (no truncate),
- *   accept_prob[B][gamma] float64 acceptance probabilities.
- * decide_only != 0 stops after accept_prob (no noise read, no outputs). */
+ *   accept_prob[B][gamma] float64 acceptance probabilities,
+ *   flags[B] SPV_FLAG_* words.
+ * decide_only != 0 stops after accept_prob (no noise read, no outputs but
+ * accept_prob and flags). */
 int spv_verify_sample(const float* target, const float* draft, int is_probs,
                       float temperature, const int32_t* proposals,
                       const float* u_accept, const float* exp_noise,
-                      const int32_t* start_pos, const int32_t* remaining,
-                      int32_t eos_id, int32_t B, int32_t gamma, int32_t V,
-                      int32_t* accept_len, int32_t* out_tokens,
-                      int32_t* n_commit, int32_t* finished, int32_t* new_len,
-                      double* accept_prob, int32_t decide_only,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      const float* draft_stats, const int32_t* start_pos,
+                      const int32_t* remaining, int32_t eos_id, int32_t B,
+                      int32_t gamma, int32_t V, int32_t* accept_len,
+                      int32_t* out_tokens, int32_t* n_commit, int32_t* finished,
+                      int32_t* new_len, double* accept_prob, int32_t* flags,
+                      int32_t decide_only, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* One draft step of the draft loop (engine/spec_scheduler.py:243-252): for
  * every row b of the draft logits (row b at logits + b * row_stride, V fp32
@@ -431,14 +448,19 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs,
  * (specdec/sampler.py:19-36, 59-69): argmax over i of q_i / exp_noise[b][i]
  * (q = softmax(z / max(T, 1e-12)), caller-supplied Exp(1) rows, lowest index
  * on ties), or, for temperature <= 0, the first-index argmax of the logits
- * (exp_noise not read). One launch for the batch; the workspace's first
+ * (exp_noise not read). row_stats (may be NULL): row b's softmax statistics
+ * (max, sum exp(x - max)) as a float2 at row_stats + 2 * b * out_stride, or
+ * (unused, argmax index) when greedy -- what spv_verify_sample takes as
+ * draft_stats. flags (may be NULL): row b's SPV_FLAG_* word at
+ * flags[b * out_stride]. One launch for the batch; the workspace's first
  * SPV_SAMPLE_COUNTER_BYTES hold arrival counters that must be zero when it is
- * first used and are zero after every call. V <= 4,194,304. */
+ * first used and are zero after every call. V <= 2,621,440. */
 size_t spv_draft_sample_workspace_bytes(int32_t B, int32_t V);
 int spv_draft_sample(const float* logits, int64_t row_stride, float temperature,
                      const float* exp_noise, int32_t B, int32_t V,
-                     int32_t* out_tokens, int32_t out_stride, void* workspace,
-                     size_t workspace_bytes, void* stream);
+                     int32_t* out_tokens, int32_t out_stride, float* row_stats,
+                     int32_t* flags, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* The top-k / top-p part of logits_to_probs (specdec/sampler.py:19-56) for
  * `rows` rows of V fp32 logits (row r at logits + r * in_stride, written at
@@ -449,12 +471,16 @@ int spv_draft_sample(const float* logits, int64_t row_stride, float temperature,
  * x where it stays and -inf elsewhere: softmax(out) is logits_to_probs, and
  * out is what spv_verify_sample / spv_draft_sample take at temperature 1.
  * Masses are summed in fp64; equal values at the nucleus boundary stay in
- * ascending index order. temperature must be > 0 (greedy rows are not
- * filtered). One workgroup per row; out may equal logits (same strides). */
+ * ascending index order. The reference decides the nucleus edge on torch's
+ * fp32 softmax, so values whose exact preceding mass lies within 5e-5 W of
+ * top_p W (W: the kept mass) can fall either way there: ambiguous (may be
+ * NULL) receives, per row, the count of such values (0 without top_p).
+ * temperature must be > 0 (greedy rows are not filtered). One workgroup per
+ * row; out may equal logits (same strides). */
 int spv_filter_logits(const float* logits, int64_t in_stride, float* out,
                       int64_t out_stride, int32_t rows, int32_t V,
                       float temperature, int32_t top_k, float top_p,
-                      void* stream);
+                      int32_t* ambiguous, void* stream);
 
 /* logits_to_probs (specdec/sampler.py:19-36) on `rows` rows of V fp32 logits. */
 int spv_logits_to_probs(const float* logits, float* probs, int32_t rows, int32_t V,

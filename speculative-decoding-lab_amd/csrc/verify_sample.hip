@@ -1,5 +1,6 @@
 // Fused verify sampling on gfx950: softmax / greedy rows, rejection decisions,
-// residual race and the commit cut of one speculative round.
+// residual race and the commit cut of one speculative round; and the draft
+// loop's per-step sampling.
 //
 // Reference semantics (per sequence, in batch order; engine/spec_scheduler.py:
 // 46-88 and 269-303, specdec/sampler.py:19-92):
@@ -15,18 +16,34 @@
 // raced row pair and its noise row once more by the race pass):
 //   1. row_stats  grid (B * rows), one workgroup per logits row: the row's max
 //                 and sum exp (or argmax); the last workgroup of each sequence
-//                 gathers p[x], q[x] and decides k (greedy: also commits)
+//                 gathers p[x], q[x] and decides k (greedy: also commits). The
+//                 draft rows' statistics may come from the draft sampler (which
+//                 read those rows when it drew the proposals); then only the
+//                 target rows are read here.
 //   1'. decide    grid (B): the decision alone, for probability inputs
-//   2. race       grid (chunks, B): residual sum and the top-2 of r/E per chunk;
-//                 the last workgroup of each sequence makes the draw and the
-//                 accepted list, budget/eos cut and new_len
+//   2. race       grid (chunks, B): residual sum and the best key of r/E per
+//                 chunk; the last workgroup of each sequence makes the draw and
+//                 the accepted list, budget/eos cut and new_len
 // Workgroups hand their per-chunk results to the last one of a sequence through
 // coherent stores and an arrival counter per sequence (spv_common.h).
-// The race compares r/E instead of (r/t)/E (t, the residual sum, is only known
-// after the pass). Both orders agree whenever the two best r/E differ by more
-// than 1e-6 relative (rounding moves a key by at most 2^-23); a closer pair, or
-// an empty residual (t <= 1e-12), is re-raced exactly by the finalizing workgroup.
+//
+// Exactness. Given probabilities the arithmetic is the reference's. Given
+// logits, p and q are this kernel's fp32 softmax, which sits within a few 1e-6
+// of torch's (another summation order, fast exp2). Every place where that can
+// change a result is bounded and either resolved exactly or reported:
+//   * the race keeps, per chunk, the best key, an upper bound of its error and
+//     the largest upper bound of every other key (not only the runner-up: a
+//     cancelling p - q can round to zero and still hide a winning key). When
+//     the best key's lower bound does not clear the others' upper bounds by the
+//     race's own rounding (kTieRel), the finalizing workgroup re-races the row
+//     with torch's arithmetic;
+//   * a decision u < min(1, p/q) with u inside the error band of p/q, and a
+//     re-raced draw whose best key is still within the keys' bound of another,
+//     set SPV_FLAG_ACCEPT_BAND / SPV_FLAG_DRAW_BAND in the sequence's flag word:
+//     the reference, computing its own fp32 softmax, may decide the other way.
 #include <math.h>
+
+#include <algorithm>
 
 #include "spv_common.h"
 
@@ -34,20 +51,43 @@ using namespace spv;
 
 namespace {
 
-// Elements of a row per race workgroup: 19,456 (8 chunks at V = 151,936, so a
-// batch of 32 is one workgroup per CU) ran about 1 us faster per sampling call
-// than 16,384 (10 chunks) and 12,288; 16,384 had been about 1 us faster than
-// 8,192 or 32,768, and 4,096 3 us slower. A multiple of 4 x 256.
-constexpr int kChunk = 19456;
+// Elements of a row per race workgroup, a multiple of 4 x 256: 10,240 (15
+// chunks at V = 151,936) took 47.9 us per sampling call (B = 32, gamma = 5,
+// draft statistics given), 9,216 48.4 and 19,456 49.8.
+constexpr int kChunk = 10240;
 constexpr int kThreads = 256;
+static_assert(kChunk % (4 * kThreads) == 0, "every thread of a race chunk takes whole float4");
+// The row statistics split each row into up to kMaxSplit contiguous pieces,
+// floor(kStatGroups / rows) of them: a batch of 32 with the draft rows'
+// statistics given has 192 rows (3 pieces: 49.7 us per sampling call against
+// about 52 with whole rows; 8 pieces 56 us), with every row read 352 (whole
+// rows: 61 us; 2 pieces 63 us, 3 pieces 69 us).
+constexpr int kMaxSplit = 8;
+constexpr int kStatGroups = 640;
 constexpr int kVecPerThread = kChunk / 4 / kThreads;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr double kEps = 1e-12;     // specdec/sampler.py:16
-constexpr float kTieRel = 1e-6f;   // top-2 gap below which the race is redone exactly
-// Relative error of p (and q) in logits mode against torch's softmax (fast
-// exp2, another summation order): r = p - q then carries up to
-// kProbRel (p + q) of absolute error, which a near cancellation does not shrink.
+// Relative rounding of the race's fast keys against the same key formed with
+// torch's arithmetic on the same p and q (hardware reciprocal of E, x / T as a
+// product, r / E against (r / t) / E): a few ulp, well inside 1e-6.
+constexpr float kTieRel = 1e-6f;
+// Error of p (and q) in logits mode against torch's softmax, relative: the
+// normaliser (another summation order of fast-exp2 terms) and the per-element
+// exp. The race's fused exponent fma(x, log2 e, -m log2 e) adds |m| 2^-22
+// (kMRel: the rounding of m log2 e, and with T != 1 the product x * (1/T)
+// against torch's x / T) and a part proportional to |x - m|, at most
+// 6 2^-24 |x - m|; since p = e^(x - m) / s and y e^-y <= 1/e, that part is an
+// absolute error below kDAbs / s (kDAbs = 2^-21 / e).
 constexpr float kProbRel = 4e-6f;
+constexpr float kMRel = 2.384185791015625e-07f;  // 2^-22
+constexpr float kDAbs = 1.7542e-07f;             // 2^-21 / e, rounded up
+// Band of a decision: the relative error of p / q (twice kProbRel, plus the
+// rounding of the quotient).
+constexpr double kDecideRel = 2.0 * 4e-6 + 2.384185791015625e-07;
+// Exact re-races: keys formed with torch's arithmetic on this kernel's p, q and
+// normalisers differ from torch's own by a few roundings (exp, the divisions):
+// 8 ulp covers them.
+constexpr float kExactRel = 9.5367431640625e-07f;  // 2^-20
 
 enum RaceMode : int { RACE_NONE = 0, RACE_RESIDUAL = 1, RACE_BONUS = 2 };
 
@@ -55,22 +95,20 @@ struct RaceInfo {
   int k;       // first rejected position (gamma if none)
   int mode;    // RaceMode
   int token;   // greedy: the drawn token
-  int pad;
+  int flags;   // SPV_FLAG_ACCEPT_BAND when a decision fell inside its band
   float mp, sp, mq, sq;  // softmax normalisers of the raced rows (logits mode)
 };
 
 struct RacePart {
-  float v1, v2;  // best and second-best r / E of the chunk
-  int i1, i2;
+  float v, u, uo;  // the chunk's best key r / E, its upper bound, the largest upper bound of the others
+  int i;
   double rsum, psum;
-  float e1, e2;  // their error weights (p + q) / E (logits mode)
-  int pad[2];
-};  // 48 bytes: three coherent 16-byte stores
+};  // 32 bytes: two coherent 16-byte stores
 
 struct SampleWs {
   int* cnt_stats;  // [B] row-stats workgroups of each sequence that have finished
   int* cnt_race;   // [B] race workgroups of each sequence that have finished
-  float2* stat;    // [B][2 gamma + 1]: (max, sum exp), or (max, argmax index bits) when greedy
+  float2* stat;    // [B][2 gamma + 1][kMaxSplit]: per row piece (max, sum exp), or (max, argmax index bits) when greedy
   RaceInfo* info;  // [B]
   RacePart* race;  // [B][nch]
 };
@@ -93,7 +131,7 @@ size_t ws_layout(int B, int gamma, int V, SampleWs* ws, void* base) {
     return o;
   };
   const size_t o_cnt = take(SPV_SAMPLE_COUNTER_BYTES);
-  const size_t o_stat = take(rows * sizeof(float2));
+  const size_t o_stat = take(rows * kMaxSplit * sizeof(float2));
   const size_t o_info = take((size_t)B * sizeof(RaceInfo));
   const size_t o_race = take((size_t)B * nch * sizeof(RacePart));
   if (ws && base) {
@@ -148,83 +186,77 @@ __device__ __forceinline__ void block_argmax(float& v, int& i) {
   __syncthreads();
 }
 
-// Top-2 (value, index) under `better`; the verify race also carries each
-// key's error weight (e1, e2), which moves with its key.
-struct Top2 {
-  float v1, v2;
-  int i1, i2;
-  float e1, e2;
+// The best key (torch.argmax order) with an upper bound u of its true value,
+// and uo, the largest upper bound over every other key seen. The best key is
+// certain when its lower bound v - (u - v) clears uo: no other key can be
+// above it, whatever its rounding. With exact keys (u = v) uo is the
+// runner-up's value.
+struct Top1 {
+  float v, u, uo;
+  int i;
   __device__ __forceinline__ void init() {
-    v1 = v2 = -INFINITY;
-    i1 = i2 = 0x7fffffff;
-    e1 = e2 = 0.f;
+    v = u = uo = -INFINITY;
+    i = 0x7fffffff;
   }
-  __device__ __forceinline__ void push(float v, int i) {
-    if (better(v, i, v1, i1)) {
-      v2 = v1;
-      i2 = i1;
-      v1 = v;
-      i1 = i;
-    } else if (better(v, i, v2, i2)) {
-      v2 = v;
-      i2 = i;
-    }
+  // A key of a higher index than every key pushed before (a thread's keys come
+  // in rising index order, so an equal key never takes the lead). NaN keys are
+  // tracked apart by the caller (lead_nan).
+  __device__ __forceinline__ void push(float key, float ub, int idx) {
+    const bool c1 = key > v;
+    uo = fmaxf(uo, c1 ? u : ub);
+    u = c1 ? ub : u;
+    v = c1 ? key : v;
+    i = c1 ? idx : i;
   }
-  __device__ __forceinline__ void merge(float w1, int j1, float w2, int j2) {
-    if (better(w1, j1, v1, i1)) {  // the other side's best leads
-      if (better(v1, i1, w2, j2)) {
-        v2 = v1;
-        i2 = i1;
-      } else {
-        v2 = w2;
-        i2 = j2;
-      }
-      v1 = w1;
-      i1 = j1;
-    } else if (better(w1, j1, v2, i2)) {
-      v2 = w1;
-      i2 = j1;
+  __device__ __forceinline__ void merge(float w, float wu, float wuo, int j) {
+    if (better(w, j, v, i)) {
+      uo = fmaxf(fmaxf(uo, u), wuo);
+      v = w;
+      u = wu;
+      i = j;
+    } else {
+      uo = fmaxf(fmaxf(uo, wu), wuo);
     }
   }
   __device__ __forceinline__ void wave_reduce() {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float w1 = __shfl_xor(v1, o, 64), w2 = __shfl_xor(v2, o, 64);
-      const int j1 = __shfl_xor(i1, o, 64), j2 = __shfl_xor(i2, o, 64);
-      merge(w1, j1, w2, j2);
-    }
+    for (int o = 32; o > 0; o >>= 1)
+      merge(__shfl_xor(v, o, 64), __shfl_xor(u, o, 64), __shfl_xor(uo, o, 64), __shfl_xor(i, o, 64));
   }
-  // merge and wave_reduce with the error weights
-  __device__ __forceinline__ void merge_e(float w1, int j1, float f1, float w2, int j2, float f2) {
-    if (better(w1, j1, v1, i1)) {
-      if (better(v1, i1, w2, j2)) {
-        v2 = v1;
-        i2 = i1;
-        e2 = e1;
-      } else {
-        v2 = w2;
-        i2 = j2;
-        e2 = f2;
-      }
-      v1 = w1;
-      i1 = j1;
-      e1 = f1;
-    } else if (better(w1, j1, v2, i2)) {
-      v2 = w1;
-      i2 = j1;
-      e2 = f1;
-    }
+  // The first NaN key of the thread (index nan_i) leads its list, as in torch.argmax.
+  __device__ __forceinline__ void lead_nan(int nan_i) {
+    if (nan_i == 0x7fffffff) return;
+    uo = fmaxf(uo, u);
+    v = u = __uint_as_float(0x7fc00000u);
+    i = nan_i;
   }
-  __device__ __forceinline__ void wave_reduce_e() {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float w1 = __shfl_xor(v1, o, 64), w2 = __shfl_xor(v2, o, 64);
-      const int j1 = __shfl_xor(i1, o, 64), j2 = __shfl_xor(i2, o, 64);
-      const float f1 = __shfl_xor(e1, o, 64), f2 = __shfl_xor(e2, o, 64);
-      merge_e(w1, j1, f1, w2, j2, f2);
-    }
+  // The best key is above every other by more than the bounds and `slack`
+  // (a NaN key is certain: it wins outright).
+  __device__ __forceinline__ bool certain(float slack) const {
+    return isnan(v) || (v - (u - v)) - uo > slack;
   }
 };
+
+// Top1 over the workgroup; every thread gets the result.
+__device__ __forceinline__ void block_top1(Top1& t) {
+  __shared__ float sv[16], su[16], suo[16];
+  __shared__ int si[16];
+  t.wave_reduce();
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[w] = t.v;
+    su[w] = t.u;
+    suo[w] = t.uo;
+    si[w] = t.i;
+  }
+  __syncthreads();
+  t.v = sv[0];
+  t.u = su[0];
+  t.uo = suo[0];
+  t.i = si[0];
+  for (int k = 1; k < nw; ++k) t.merge(sv[k], su[k], suo[k], si[k]);
+  __syncthreads();
+}
 
 // Combine (m, s) pairs of sum exp(x - m) (natural-log units).
 __device__ __forceinline__ void lse_combine(float& m, float& s, float m2, float s2) {
@@ -266,6 +298,14 @@ __device__ __forceinline__ double block_sum_f64(double x) {
 // x = z / T in float32 (torch divides the fp32 tensor by the scalar in fp32).
 __device__ __forceinline__ float scaled(float z, float tf, bool unit) { return unit ? z : z / tf; }
 
+// z / T from the product z * (1/T) and one correction step (the remainder
+// z - x T is exact in an fma): the correctly rounded quotient but for rare
+// near-halfway cases, a few instructions instead of a division.
+__device__ __forceinline__ float div_fast(float z, float tf, float rtf) {
+  const float x = z * rtf;
+  return fmaf(fmaf(-x, tf, z), rtf, x);
+}
+
 // Element i of this thread's slice of a chunk: 8 float4 per thread.
 __device__ __forceinline__ int vec_index(int c, int k) { return c * (kChunk / 4) + threadIdx.x + k * kThreads; }
 
@@ -273,12 +313,15 @@ __device__ __forceinline__ int vec_index(int c, int k) { return c * (kChunk / 4)
 struct DecideArgs {
   const float* target;
   const float* draft;
+  const float* dstats;  // (B, gamma) float2 statistics of the draft rows, or null
   const int32_t* proposals;
   const float* u;
   double* accept_prob;
   int32_t* accept_len;
   int32_t* out_tokens;
+  int32_t* flags;
   int B, gamma, V, is_probs, greedy, decide_only;
+  int split;  // pieces per statistics row
   float tf;
 };
 
@@ -325,13 +368,27 @@ __device__ __forceinline__ void commit_cut(const DecideArgs& a, const CommitArgs
   if (cm.new_len) cm.new_len[b] = n > 0 ? st + n : -1;
 }
 
+// Whether the reference's decision `u < min(1, p/q)` (both 1e-12 branches) can
+// differ from this one when its p and q may each lie a relative `beta`/2 away
+// from pd and qd (beta: the band of the quotient).
+__device__ __forceinline__ bool decision_in_band(double pd, double qd, double u, double beta) {
+  const double lo_eps = kEps / (1.0 + beta), hi_eps = kEps * (1.0 + beta);
+  if (qd >= lo_eps && qd <= hi_eps) return true;  // the q <= 1e-12 branch itself
+  if (qd < lo_eps) return pd >= lo_eps && pd <= hi_eps;  // a = 1 or 0 by p > 1e-12
+  const double rho = pd / qd;
+  const double lo = rho * (1.0 - beta);
+  if (lo >= 1.0) return false;  // a = 1 for both, and u < 1
+  return u >= lo && u < fmin(1.0, rho * (1.0 + beta));
+}
+
 // ------------------------------------------------------------- decision
 // Decision of sequence b (spec_scheduler.py:60-77): accept x_j while
 // (double)u_j < min(1, p_j[x_j] / q_j[x_j]), and record the draw to make.
 // Runs in one whole workgroup. In logits mode the row statistics of the
 // sequence were published by the row-stats workgroups with coherent stores and
-// are read the same way here. In greedy mode the draw is the target row's
-// argmax, so the commit is finished here as well.
+// are read the same way here (the draft rows' from the caller's buffer when it
+// gave one). In greedy mode the draw is the target row's argmax, so the commit
+// is finished here as well.
 enum InputMode : int { IN_PROBS = 0, IN_LOGITS = 1, IN_GREEDY = 2 };
 
 template <int MODE>
@@ -357,12 +414,30 @@ __device__ __forceinline__ void decide_seq(const DecideArgs& a, const CommitArgs
     if (cm.start) st = cm.start[b];
   }
   if (MODE != IN_PROBS && t < nrows) {
-    const u32x2_t v = load_coherent_b64(coherent_rsrc(ws.stat), ((size_t)b * nrows + t) * sizeof(float2));
-    if (greedy) {
-      s_am[t] = (int)v.y;
+    float m = -INFINITY, s = 0.f, bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (t >= C && a.dstats) {
+      const float2 d = reinterpret_cast<const float2*>(a.dstats)[(size_t)b * a.gamma + (t - C)];
+      m = bv = d.x;
+      s = d.y;
+      bi = __float_as_int(d.y);
     } else {
-      s_m[t] = __uint_as_float(v.x);
-      s_s[t] = __uint_as_float(v.y);
+      // the row's pieces in index order: first-index argmax, or their (max, sum exp)
+      const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(ws.stat);
+      for (int pc = 0; pc < a.split; ++pc) {
+        const u32x2_t v = load_coherent_b64(rs, (((size_t)b * nrows + t) * kMaxSplit + pc) * sizeof(float2));
+        if (greedy) {
+          if (better(__uint_as_float(v.x), (int)v.y, bv, bi)) bv = __uint_as_float(v.x), bi = (int)v.y;
+        } else {
+          lse_combine(m, s, __uint_as_float(v.x), __uint_as_float(v.y));
+        }
+      }
+    }
+    if (greedy) {
+      s_am[t] = bi;
+    } else {
+      s_m[t] = m;
+      s_s[t] = s;
     }
   }
   if (t < a.gamma) {
@@ -377,7 +452,7 @@ __device__ __forceinline__ void decide_seq(const DecideArgs& a, const CommitArgs
   }
   __syncthreads();
   if (t == 0) {
-    int k = a.gamma;
+    int k = a.gamma, dflag = 0;
     for (int j = 0; j < a.gamma; ++j) {
       const int xj = s_x[j];
       float pp, qq;
@@ -396,9 +471,20 @@ __device__ __forceinline__ void decide_seq(const DecideArgs& a, const CommitArgs
       const double qd = (double)qq, pd = (double)pp;
       const double acc = qd <= kEps ? (pd > kEps ? 1.0 : 0.0) : fmin(1.0, pd / qd);
       if (a.accept_prob) a.accept_prob[(size_t)b * a.gamma + j] = acc;
-      if (k == a.gamma && !((double)s_u[j] < acc)) {
-        k = j;
-        if (!a.accept_prob) break;
+      if (k == a.gamma) {  // an examined position
+        if (MODE == IN_LOGITS && (unsigned)xj < (unsigned)a.V) {
+          double beta = kDecideRel;
+          // T != 1: torch may form x / T as a product with 1 / T (one ulp of x
+          // and of the row max on each side)
+          if (a.tf != 1.0f)
+            beta += (double)kMRel * ((double)fabsf(s_zp[j] / a.tf) + fabs((double)s_m[j]) +
+                                     (double)fabsf(s_zq[j] / a.tf) + fabs((double)s_m[C + j]));
+          if (decision_in_band(pd, qd, (double)s_u[j], beta)) dflag |= SPV_FLAG_ACCEPT_BAND;
+        }
+        if (!((double)s_u[j] < acc)) {
+          k = j;
+          if (!a.accept_prob) break;
+        }
       }
     }
     s_k = k;
@@ -406,11 +492,13 @@ __device__ __forceinline__ void decide_seq(const DecideArgs& a, const CommitArgs
     // when both rows agree), and the bonus row is one-hot: the draw is the
     // target row's argmax for any positive finite E.
     s_tok = greedy ? s_am[k] : -1;
+    if (a.flags && (greedy || a.decide_only)) a.flags[b] = dflag;
     if (!a.decide_only) {
       RaceInfo info{};
       info.k = k;
       info.mode = greedy ? RACE_NONE : k < a.gamma ? RACE_RESIDUAL : RACE_BONUS;
       info.token = s_tok;
+      info.flags = dflag;
       if (MODE == IN_LOGITS) {
         info.mp = s_m[k];
         info.sp = s_s[k];
@@ -431,22 +519,24 @@ __device__ __forceinline__ void decide_seq(const DecideArgs& a, const CommitArgs
 }
 
 // ------------------------------------------------------------- 1. row stats
-// One workgroup per row: grid (B * (2 gamma + 1)), sequence b's rows
-// consecutive (row r < gamma + 1 is target row r, row gamma + 1 + j is draft
-// row j). The row streams through the workgroup in steps of kStepVec float4
-// per thread, the next step's loads in flight while one is reduced. The last
-// row of a sequence to finish makes its decision. Four float4 per step was
-// the fastest of 2, 3, 4, 6, 8 and 16 (B = 32, gamma = 5, V = 151,936: 60.6
-// against 65.0 us per sampling call at 8): with 352 rows in flight HBM is
-// saturated either way, and the shorter steps keep the workgroups' requests
-// more evenly spread.
+// One workgroup per row: grid (B * nr) with nr = 2 gamma + 1, or gamma + 1
+// when the draft rows' statistics are given; sequence b's rows consecutive
+// (row r < gamma + 1 is target row r, row gamma + 1 + j is draft row j). The
+// row streams through the workgroup in steps of kStepVec float4 per thread,
+// the next step's loads in flight while one is reduced. The last row of a
+// sequence to finish makes its decision. Four float4 per step was the fastest
+// of 2, 3, 4, 6, 8 and 16 (B = 32, gamma = 5, V = 151,936: 60.6 against 65.0
+// us per sampling call at 8): with 352 rows in flight HBM is saturated either
+// way, and the shorter steps keep the workgroups' requests more evenly spread.
 constexpr int kStepVec = 4;
 
 template <int MODE, bool UNIT>
 __global__ __launch_bounds__(kThreads) void row_stats_kernel(DecideArgs a, CommitArgs cm, SampleWs ws) {
   constexpr bool GREEDY = MODE == IN_GREEDY;
   const int nrows = 2 * a.gamma + 1, C = a.gamma + 1;
-  const int b = blockIdx.x / nrows, r = blockIdx.x - b * nrows;
+  const int nr = a.dstats ? C : nrows;
+  const int row = blockIdx.x / a.split, pc = blockIdx.x - row * a.split;
+  const int b = row / nr, r = row - b * nr;
   const float* z = r < C ? a.target + ((size_t)b * C + r) * a.V : a.draft + ((size_t)b * a.gamma + (r - C)) * a.V;
   const int V = a.V;
   const float tf = a.tf;
@@ -468,8 +558,11 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(DecideArgs a, Commi
     if (!(v <= bv) && better(v, i, bv, bi)) bv = v, bi = i;
   };
   if ((V & 3) == 0) {
-    const int n4 = V >> 2;
-    const __amdgpu_buffer_rsrc_t rz = span_rsrc(z, (uint32_t)V * 4u);
+    // this piece's float4 range [j0, n4) of the row; the buffer spans it alone,
+    // so loads past its end return zero without touching the next piece
+    const int nv = V >> 2;
+    const int j0 = (int)((long long)nv * pc / a.split), n4 = (int)((long long)nv * (pc + 1) / a.split) - j0;
+    const __amdgpu_buffer_rsrc_t rz = span_rsrc(z + 4 * (size_t)j0, (uint32_t)n4 * 16u);
     constexpr int kStep = kStepVec * kThreads;
     const int nstep = (n4 + kStep - 1) / kStep;
     u32x4_t cur[kStepVec], nxt[kStepVec];
@@ -490,7 +583,7 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(DecideArgs a, Commi
         for (int e = 0; e < 4; ++e) {
           const float v = __uint_as_float(cur[k][e]);
           if (GREEDY) {
-            if (ok) greedy_visit(v, 4 * i4 + e);
+            if (ok) greedy_visit(v, 4 * (j0 + i4) + e);
           } else {
             xs[4 * k + e] = ok ? (UNIT ? v : v / tf) : -INFINITY;
           }
@@ -501,7 +594,8 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(DecideArgs a, Commi
       for (int k = 0; k < kStepVec; ++k) cur[k] = nxt[k];
     }
   } else {
-    for (int i = threadIdx.x; i < V; i += kThreads) {
+    const int i0 = (int)((long long)V * pc / a.split), i1 = (int)((long long)V * (pc + 1) / a.split);
+    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
       const float zi = z[i];
       if (GREEDY) {
         greedy_visit(zi, i);
@@ -511,7 +605,7 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(DecideArgs a, Commi
       }
     }
   }
-  const size_t slot = ((size_t)b * nrows + r) * sizeof(float2);
+  const size_t slot = (((size_t)b * nrows + r) * kMaxSplit + pc) * sizeof(float2);
   if (GREEDY) {
     block_argmax(bv, bi);
     if (threadIdx.x == 0) store_coherent_b64(coherent_rsrc(ws.stat), slot, u32x2_t{__float_as_uint(bv), (unsigned)bi});
@@ -529,7 +623,7 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(DecideArgs a, Commi
     }
   }
   __shared__ int s_last;
-  if (arrive_last(ws.cnt_stats + b, nrows, &s_last)) decide_seq<MODE>(a, cm, ws, b);
+  if (arrive_last(ws.cnt_stats + b, nr * a.split, &s_last)) decide_seq<MODE>(a, cm, ws, b);
 }
 
 // Decision without row statistics (probability inputs): grid (B).
@@ -544,10 +638,27 @@ __device__ __forceinline__ float exact_prob(float z, float m, float s, float tf,
   return probs ? z : softmax_at(z, m, s, tf);
 }
 
+// Per-row error bounds of the raced rows' probabilities (logits mode): relative
+// ep (p) and eq (q), absolute kap (both). The fast race's fused exponent adds
+// the |m| and |x - m| terms; the exact race forms x - m as torch does, so only
+// the normaliser and the exp are left (kProbRel).
+struct ProbBound {
+  float ep, eq, kap;
+};
+__device__ __forceinline__ ProbBound prob_bound(const RaceInfo& info, bool resid, bool probs, bool exact) {
+  ProbBound pb{0.f, 0.f, 0.f};
+  if (probs) return pb;
+  pb.ep = kProbRel + (exact ? 0.f : kMRel * fabsf(info.mp));
+  pb.eq = resid ? kProbRel + (exact ? 0.f : kMRel * fabsf(info.mq)) : 0.f;
+  pb.kap = exact ? 0.f : kDAbs * (1.f / info.sp + (resid ? 1.f / info.sq : 0.f));
+  return pb;
+}
+
 // The draw and the commit of sequence b, in the workgroup that completed its
-// race: combine the per-chunk top-2 (coherent loads), re-race exactly when the
-// best two keys are within kTieRel plus their own error bound (logits mode:
-// kProbRel (p + q) / E each) or the residual is empty, then cut.
+// race: combine the chunks' best keys (coherent loads); re-race the row with
+// torch's arithmetic when the best key is not certain (its lower bound within
+// kTieRel of the others' upper bounds) or the residual is empty; flag a draw
+// that is still not certain after the exact race; then cut.
 __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitArgs& cm, const SampleWs& ws, int b,
                                              const RaceInfo& info) {
   const int C = a.gamma + 1, nch = num_chunks(a.V);
@@ -564,19 +675,17 @@ __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitAr
     if (threadIdx.x == 0) s_token = info.token, s_exact = 0;
   } else if (threadIdx.x < 64) {
     const __amdgpu_buffer_rsrc_t rr = coherent_rsrc(ws.race);
-    Top2 t2;
-    t2.init();
+    Top1 t1;
+    t1.init();
     double rs = 0.0, ps = 0.0;
     for (int c = threadIdx.x; c < nch; c += 64) {
       const size_t o = ((size_t)b * nch + c) * sizeof(RacePart);
-      const u32x4_t lo = load_coherent_b128(rr, o), hi = load_coherent_b128(rr, o + 16),
-                    ew = load_coherent_b128(rr, o + 32);
-      t2.merge_e(__uint_as_float(lo.x), (int)lo.z, __uint_as_float(ew.x), __uint_as_float(lo.y), (int)lo.w,
-                 __uint_as_float(ew.y));
+      const u32x4_t lo = load_coherent_b128(rr, o), hi = load_coherent_b128(rr, o + 16);
+      t1.merge(__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z), (int)lo.w);
       rs += __hiloint2double((int)hi.y, (int)hi.x);
       ps += __hiloint2double((int)hi.w, (int)hi.z);
     }
-    t2.wave_reduce_e();
+    t1.wave_reduce();
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       rs += __shfl_xor(rs, o, 64);
@@ -584,10 +693,7 @@ __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitAr
     }
     if (threadIdx.x == 0) {
       int exact = 0;
-      // The two best keys' own error in logits mode: kProbRel (p + q) / E
-      // each, their weights carried with them through the chunks' partials.
-      const float werr = a.is_probs ? 0.f : kProbRel * (t2.e1 + t2.e2);
-      const bool tie = !isnan(t2.v1) && !(t2.v1 - t2.v2 > kTieRel * t2.v1 + werr);
+      const bool tie = !t1.certain(kTieRel * t1.v);
       if (info.mode == RACE_RESIDUAL) {
         const float t = (float)rs;  // fp32 sum, accumulated in fp64 and rounded once
         s_t = t;
@@ -598,52 +704,67 @@ __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitAr
         exact = 3;  // bonus row
       }
       s_exact = exact;
-      s_token = t2.i1;
+      s_token = t1.i;
     }
   }
   __syncthreads();
-  int token = s_token;
+  int token = s_token, rflag = 0;
   if (s_exact) {
-    // Exact race over the whole row with torch's arithmetic (rare).
+    // Exact race over the whole row with torch's arithmetic (rare), each key
+    // with its bound: the probabilities' own (logits mode) over t E, plus
+    // kExactRel of the key.
     const int k = info.k;
     const float* pr = a.target + ((size_t)b * C + k) * a.V;
     const float* qr = k < a.gamma ? a.draft + ((size_t)b * a.gamma + k) * a.V : nullptr;
     const float* e = cm.noise + (size_t)b * a.V;
     const bool probs = a.is_probs;
+    const ProbBound pb = prob_bound(info, s_exact == 1, probs, true);
     const float t = s_t, psum = s_psum;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    const float div = s_exact == 1 ? t : s_exact == 2 ? psum : 1.f;
+    Top1 t1;
+    t1.init();
+    int nan_i = 0x7fffffff;
     for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
       const float p = exact_prob(pr[i], info.mp, info.sp, a.tf, probs);
-      float rhat;
+      float rhat, q = 0.f, d = p;
       if (s_exact == 3) {
         rhat = p;
       } else if (s_exact == 2) {
         rhat = p / psum;
       } else {
-        const float d = p - exact_prob(qr[i], info.mq, info.sq, a.tf, probs);
+        q = exact_prob(qr[i], info.mq, info.sq, a.tf, probs);
+        d = p - q;
         rhat = (d < 0.f ? 0.f : d) / t;
       }
       const float key = rhat / e[i];
-      if (better(key, i, bv, bi)) bv = key, bi = i;
+      // upper bound: the residual (or p) plus the probabilities' error, over
+      // the normaliser and E, and a few roundings of the key
+      const float hi = fmaxf(d + fmaf(pb.ep, p, fmaf(pb.eq, q, pb.kap)), 0.f) / (div * e[i]);
+      t1.push(key, fmaxf(fmaf(key, kExactRel, key), fmaf(hi, kExactRel, hi)), i);
+      if (key != key && nan_i == 0x7fffffff) nan_i = i;
     }
-    block_argmax(bv, bi);
-    token = bi;
+    t1.lead_nan(nan_i);
+    block_top1(t1);
+    token = t1.i;
+    if (!t1.certain(0.f)) rflag = SPV_FLAG_DRAW_BAND;
   }
   if (threadIdx.x != 0) return;
   a.out_tokens[(size_t)b * C + info.k] = token;
+  if (a.flags) a.flags[b] = info.flags | rflag;
   commit_cut(a, cm, b, info.k, token, s_x, rem, st);
 }
 
 // ---------------------------------------------------------------- 2. race
 // Residual (or bonus) race of one chunk: p (and q) from the row statistics,
-// the residual (p - q)+ formed on the fly, keys r / E kept as their top two.
-// Keys use x * (1 / T) and a hardware reciprocal of E: they differ from the
-// exact keys by a few ulp, and best pairs closer than kTieRel are re-raced
-// exactly. All loads of the chunk are issued before the first is used (buffer
-// loads past the row end return zero and count as absent).
+// the residual (p - q)+ formed on the fly, keys r / E kept as the chunk's best
+// with its bound and the others' largest bound. Keys use x * (1 / T) and a
+// hardware reciprocal of E: they differ from keys formed with torch's
+// arithmetic by a few ulp (kTieRel). In logits mode each key also carries the
+// error of its p and q against torch's softmax: (ep p + eq q + kap) / E. All
+// loads of the chunk are issued before the first is used (buffer loads past
+// the row end return zero and count as absent).
 template <bool RESID, bool UNIT, bool PROBS>
-__device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& info, int b, int c, Top2& t2,
+__device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& info, int b, int c, Top1& t1,
                                            float& rs, float& ps, const float* __restrict__ e) {
   const int C = a.gamma + 1, V = a.V;
   const float* pr = a.target + ((size_t)b * C + info.k) * V;
@@ -651,6 +772,7 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
   const float rtf = 1.f / a.tf;
   const float mp = info.mp * kLog2e, isp = 1.f / info.sp;
   const float mq = info.mq * kLog2e, isq = RESID ? 1.f / info.sq : 0.f;
+  const ProbBound pb = prob_bound(info, RESID, PROBS, false);
   // p and q are each rounded before p - q is formed, as torch forms them as
   // tensors first (a contracted fma would leave a residual of ~1 ulp where
   // p == q).
@@ -661,17 +783,16 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
     asm("" : "+v"(pv));  // opaque: the product is not fused into p - q
     return pv;
   };
-  // Branch-free visit in rising index order: a strictly larger key takes a
-  // place (an equal later key never wins), NaN keys are tracked apart (the
-  // first NaN wins, as torch.argmax), and entries past the row end
-  // (ok == false) add nothing and carry key -1, below every real key.
+  // Branch-free visit in rising index order (Top1::push); NaN keys are tracked
+  // apart (the first NaN wins, as torch.argmax), and entries past the row end
+  // (ok == false) add nothing and carry key and bound -1, below every real key.
   int nan_i = 0x7fffffff;
   auto visit = [&](int i, bool ok, float zp, float zq, float ei) {
     float p = prob(zp, mp, isp);
-    float r = p, qv = 0.f;
+    float r = p, qv = 0.f, d = p;
     if (RESID) {
       qv = prob(zq, mq, isq);
-      const float d = p - qv;
+      d = p - qv;
       r = d < 0.f ? 0.f : d;  // torch.clamp(p - q, min=0): NaN stays NaN
     }
     r = ok ? r : 0.f;
@@ -681,15 +802,11 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
     }
     const float re = __builtin_amdgcn_rcpf(ei);
     const float key = ok ? r * re : -1.f;
-    // error weight (p + q) / E of the key (logits mode)
-    const float ew = PROBS ? 0.f : (p + qv) * re;
-    const bool c1 = key > t2.v1, c2 = key > t2.v2;
-    t2.v2 = c1 ? t2.v1 : (c2 ? key : t2.v2);
-    t2.i2 = c1 ? t2.i1 : (c2 ? i : t2.i2);
-    t2.e2 = c1 ? t2.e1 : (c2 ? ew : t2.e2);
-    t2.v1 = c1 ? key : t2.v1;
-    t2.i1 = c1 ? i : t2.i1;
-    t2.e1 = c1 ? ew : t2.e1;
+    // the true residual is at most max(p - q + err, 0): a token whose q is
+    // above p by more than the error bound has a true key of 0
+    float ub = key;
+    if (!PROBS) ub = ok ? fmaxf(d + fmaf(pb.ep, p, fmaf(pb.eq, qv, pb.kap)), 0.f) * re : -1.f;
+    t1.push(key, ub, i);
     nan_i = (key != key && nan_i == 0x7fffffff) ? i : nan_i;
   };
   if ((V & 3) == 0) {
@@ -717,14 +834,7 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
     const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
     for (int i = i0 + threadIdx.x; i < i1; i += kThreads) visit(i, true, pr[i], RESID ? qr[i] : 0.f, e[i]);
   }
-  if (nan_i != 0x7fffffff) {  // a NaN key leads the thread's list
-    t2.v2 = t2.v1;
-    t2.i2 = t2.i1;
-    t2.e2 = t2.e1;
-    t2.v1 = __uint_as_float(0x7fc00000u);
-    t2.i1 = nan_i;
-    t2.e1 = 0.f;
-  }
+  t1.lead_nan(nan_i);
 }
 
 // grid (chunks, B). The last workgroup of a sequence to finish makes its draw
@@ -734,34 +844,31 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
   const int c = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
   const RaceInfo info = ws.info[b];
   const float* e = cm.noise + (size_t)b * a.V;
-  Top2 t2;
-  t2.init();
+  Top1 t1;
+  t1.init();
   float rs = 0.f, ps = 0.f;
-  if (info.mode == RACE_RESIDUAL) race_chunk<true, UNIT, PROBS>(a, info, b, c, t2, rs, ps, e);
-  else if (info.mode == RACE_BONUS) race_chunk<false, UNIT, PROBS>(a, info, b, c, t2, rs, ps, e);
-  t2.wave_reduce_e();
-  __shared__ float s_v1[kWaves], s_v2[kWaves], s_e1[kWaves], s_e2[kWaves];
-  __shared__ int s_i1[kWaves], s_i2[kWaves];
+  if (info.mode == RACE_RESIDUAL) race_chunk<true, UNIT, PROBS>(a, info, b, c, t1, rs, ps, e);
+  else if (info.mode == RACE_BONUS) race_chunk<false, UNIT, PROBS>(a, info, b, c, t1, rs, ps, e);
+  t1.wave_reduce();
+  __shared__ float s_v[kWaves], s_u[kWaves], s_uo[kWaves];
+  __shared__ int s_i[kWaves];
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
-    s_v1[w] = t2.v1;
-    s_v2[w] = t2.v2;
-    s_i1[w] = t2.i1;
-    s_i2[w] = t2.i2;
-    s_e1[w] = t2.e1;
-    s_e2[w] = t2.e2;
+    s_v[w] = t1.v;
+    s_u[w] = t1.u;
+    s_uo[w] = t1.uo;
+    s_i[w] = t1.i;
   }
   const double rsum = block_sum_f64((double)rs);
   const double psum = block_sum_f64((double)ps);
   if (threadIdx.x == 0) {
-    for (int k = 1; k < kWaves; ++k) t2.merge_e(s_v1[k], s_i1[k], s_e1[k], s_v2[k], s_i2[k], s_e2[k]);
+    for (int k = 1; k < kWaves; ++k) t1.merge(s_v[k], s_u[k], s_uo[k], s_i[k]);
     const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(ws.race);
     const size_t o = ((size_t)b * nch + c) * sizeof(RacePart);
-    store_coherent_b128(rp, o, u32x4_t{__float_as_uint(t2.v1), __float_as_uint(t2.v2), (unsigned)t2.i1,
-                                       (unsigned)t2.i2});
+    store_coherent_b128(rp, o, u32x4_t{__float_as_uint(t1.v), __float_as_uint(t1.u), __float_as_uint(t1.uo),
+                                       (unsigned)t1.i});
     store_coherent_b128(rp, o + 16, u32x4_t{(unsigned)__double2loint(rsum), (unsigned)__double2hiint(rsum),
                                             (unsigned)__double2loint(psum), (unsigned)__double2hiint(psum)});
-    store_coherent_b128(rp, o + 32, u32x4_t{__float_as_uint(t2.e1), __float_as_uint(t2.e2), 0u, 0u});
   }
   __shared__ int s_last;
   if (arrive_last(ws.cnt_race + b, nch, &s_last)) finalize_seq(a, cm, ws, b, info);
@@ -771,22 +878,47 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
 // One draft step of the reference's draft loop (engine/spec_scheduler.py:
 // 243-252): for every row b, token[b] = sample_token(logits_to_probs(z_b))
 // (specdec/sampler.py:19-36, 59-69) = argmax(q_b / E_b) with the caller's
-// Exp(1) row E_b, or the first-index argmax of z_b when greedy. grid (chunks,
-// B): each chunk workgroup reads its slice of z_b and E_b once and keeps the
-// slice's max m_c, sum of exp(x - m_c) and the top two keys exp(x - m_c) / E
-// (x = z / T); the last workgroup of a row to arrive combines them (keys
-// rescaled by exp(m_c - M)) and, when the two best keys are within kTieRel or
-// a NaN is involved, re-races the row exactly with torch's arithmetic, q =
-// exp(x - M) / S, key = q / E. Greedy rows keep the slice's argmax instead.
+// Exp(1) row E_b, or the first-index argmax of z_b when greedy.
+//
+// The race runs on log2 keys: argmax_i q_i / E_i = argmax_i x_i log2 e -
+// log2 E_i (x = z / T; q = e^(x - M) / S and S are common to all keys), one
+// fma after the hardware log2, so a row needs one pass and no maximum first.
+// Each key carries a bound of its distance from the log2 of torch's key
+// q / E: 2^-21 (|x| + |log2 E| + |key|) (the rounding of x log2 e, of log2 E
+// and of the fma, and torch's own exp(x - M) rounding, at most (|x| + |M|)
+// 2^-24 relative), plus 2^-21 |M| + 2^-20 common to all keys. The same pass
+// keeps the row's softmax statistics (max, sum exp(x - max)), which the
+// verify step's decisions use instead of reading the draft rows again.
+// grid (chunks, B); the last workgroup of a row to arrive combines the
+// chunks and, when the best key is not certain or a NaN is involved,
+// re-races the row exactly with torch's arithmetic, q = exp(x - M) / S,
+// key = q / E (flagging a draw still within a few ulp of another key).
+// Greedy rows keep the chunk's first-index argmax; their statistics are
+// (max, argmax index), the verify step's greedy format.
+// Elements of a row per workgroup, a multiple of 4 x kThreads: 10,240 (15
+// chunks at V = 151,936) drew 32 rows in 16.6 us, 19,456 in 17.3, 5,120 in
+// 20.2 and 2,048 in 36.7; four float4 per step instead of two measured the same.
+constexpr int kDraftChunk = 10240;
+static_assert(kDraftChunk % (4 * kThreads) == 0, "every thread of a draft chunk takes whole float4");
+constexpr int kDraftStep = 2;        // float4 of logits and of noise per thread per step
+constexpr float kKeyRel = 4.76837158203125e-07f;  // 2^-21
+constexpr float kKeyAbs = 9.5367431640625e-07f;   // 2^-20
+
+__host__ __device__ inline int draft_chunks(int V) { return (V + kDraftChunk - 1) / kDraftChunk; }
+
 struct DraftPart {
-  float m, s, v1, v2;  // slice max, sum exp(x - m), best two keys (relative to m)
-  int i1, i2, pad0, pad1;
+  float m, s;      // chunk max of x and sum exp(x - m) (greedy: max logit, unused)
+  float v, u;      // best log2 key (greedy: logit) and its upper bound
+  float uo;        // largest upper bound of the chunk's other keys
+  int i, pad0, pad1;
 };  // 32 bytes: two coherent 16-byte stores
 
 struct DraftArgs {
   const float* logits;
   const float* noise;
   int32_t* out;
+  float* stats;    // row b's (max, sum exp) at stats[2 b out_stride], or null
+  int32_t* flags;  // row b's flag word at flags[b out_stride], or null
   DraftPart* part;
   int* cnt;
   long long row_stride;
@@ -800,195 +932,187 @@ __global__ __launch_bounds__(kThreads) void draft_race_kernel(DraftArgs a) {
   const float* z = a.logits + (size_t)b * a.row_stride;
   const float* e = a.noise + (size_t)b * a.V;
   const int V = a.V;
-  const float rtf = 1.f / a.tf;
+  const float tf = a.tf, rtf = 1.f / a.tf;
   float m = -INFINITY, sum = 0.f;
-  Top2 t2;
-  t2.init();
+  Top1 t1;
+  t1.init();
   int nan_i = 0x7fffffff;
+  const int i0 = c * kDraftChunk, i1 = min(V, i0 + kDraftChunk);
+  // One element (sampled): the online statistics are updated per float4 by the caller.
+  auto key_visit = [&](int i, bool ok, float x, float ev) {
+    const float l = __builtin_amdgcn_logf(ev);
+    float lk = fmaf(x, kLog2e, -l);
+    float ub = fmaf(fabsf(x) + fabsf(l) + fabsf(lk), kKeyRel, lk);
+    lk = ok ? lk : -INFINITY;
+    ub = ok ? ub : -INFINITY;
+    t1.push(lk, ub, i);
+    nan_i = (lk != lk && nan_i == 0x7fffffff) ? i : nan_i;
+  };
+  auto absorb4 = [&](const float* xs) {  // (m, sum) over 4 values (-inf for absent ones)
+    const float mx = fmaxf(fmaxf(m, fmaxf(xs[0], xs[1])), fmaxf(xs[2], xs[3]));
+    const float f = mx == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m - mx) * kLog2e);
+    const float ms = mx == -INFINITY ? 0.f : mx;
+    sum *= f;
+    m = mx;
+    // (x - max) first, as the row statistics and torch form it: no |max| term
+#pragma unroll
+    for (int t = 0; t < 4; ++t) sum += __builtin_amdgcn_exp2f((xs[t] - ms) * kLog2e);
+  };
   if ((V & 3) == 0 && (a.row_stride & 3) == 0) {
-    const int n4 = V >> 2;
+    const int n4 = i1 >> 2, j0 = i0 >> 2;
     const uint32_t row_bytes = (uint32_t)V * 4u;
     const __amdgpu_buffer_rsrc_t bz = span_rsrc(z, row_bytes), be = span_rsrc(e, row_bytes);
-    u32x4_t zv[kVecPerThread], ev[kVecPerThread];
+    constexpr int kStep = kDraftStep * kThreads;  // float4 per step and workgroup
+    const int nstep = (n4 - j0 + kStep - 1) / kStep;
+    // Vector j of the chunk, or the row's end (the load returns zero without a
+    // memory access) for vectors beyond the chunk, which belong to the next one.
+    auto off_of = [&](int j) { return j < n4 ? (uint32_t)j * 16u : row_bytes; };
+    u32x4_t zc[kDraftStep], ec[kDraftStep], zn[kDraftStep], en[kDraftStep];
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const uint32_t off = (uint32_t)vec_index(c, k) * 16u;
-      zv[k] = load_b128(bz, off);
-      if (!a.greedy) ev[k] = load_b128(be, off);
+    for (int k = 0; k < kDraftStep; ++k) {
+      const uint32_t o = off_of(j0 + threadIdx.x + k * kThreads);
+      zc[k] = load_b128(bz, o);
+      if (!a.greedy) ec[k] = load_b128(be, o);
     }
-    if (a.greedy) {
-      // first-index argmax of the raw logits (torch.argmax: NaN wins)
+    for (int stp = 0; stp < nstep; ++stp) {
+      const int base = j0 + stp * kStep;
+      if (stp + 1 < nstep) {
 #pragma unroll
-      for (int k = 0; k < kVecPerThread; ++k) {
-        const int i4 = vec_index(c, k);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float v = __uint_as_float(zv[k][t]);
-          if (i4 < n4 && better(v, 4 * i4 + t, t2.v1, t2.i1)) t2.v1 = v, t2.i1 = 4 * i4 + t;
+        for (int k = 0; k < kDraftStep; ++k) {
+          const uint32_t o = off_of(base + kStep + threadIdx.x + k * kThreads);
+          zn[k] = load_b128(bz, o);
+          if (!a.greedy) en[k] = load_b128(be, o);
         }
       }
-    } else {
 #pragma unroll
-      for (int k = 0; k < kVecPerThread; ++k) {
-        const int i4 = vec_index(c, k);
+      for (int k = 0; k < kDraftStep; ++k) {
+        const int j = base + threadIdx.x + k * kThreads;
+        const bool ok = j < n4;
+        if (a.greedy) {
+          // first-index argmax of the raw logits (torch.argmax: NaN wins)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float x = UNIT ? __uint_as_float(zv[k][t]) : __uint_as_float(zv[k][t]) * rtf;
-          if (i4 < n4) m = fmaxf(m, x);
+          for (int t = 0; t < 4; ++t) {
+            const float v = __uint_as_float(zc[k][t]);
+            if (ok && better(v, 4 * j + t, t1.v, t1.i)) t1.v = v, t1.i = 4 * j + t;
+          }
+        } else {
+          float xs[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float zv = __uint_as_float(zc[k][t]);
+            xs[t] = ok ? (UNIT ? zv : div_fast(zv, tf, rtf)) : -INFINITY;
+          }
+          absorb4(xs);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) key_visit(4 * j + t, ok, xs[t], __uint_as_float(ec[k][t]));
         }
       }
-      // the slice max across the workgroup, so every thread's keys share it
-      m = fmaxf(m, __shfl_xor(m, 32, 64));
-      m = fmaxf(m, __shfl_xor(m, 16, 64));
-      m = fmaxf(m, __shfl_xor(m, 8, 64));
-      m = fmaxf(m, __shfl_xor(m, 4, 64));
-      m = fmaxf(m, __shfl_xor(m, 2, 64));
-      m = fmaxf(m, __shfl_xor(m, 1, 64));
-      __shared__ float s_m[kWaves];
-      if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
-      __syncthreads();
-      m = s_m[0];
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) m = fmaxf(m, s_m[w]);
-      const float ml = m == -INFINITY ? 0.f : m * kLog2e;
-#pragma unroll
-      for (int k = 0; k < kVecPerThread; ++k) {
-        const int i4 = vec_index(c, k);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int i = 4 * i4 + t;
-          const bool ok = i4 < n4;
-          const float x = UNIT ? __uint_as_float(zv[k][t]) : __uint_as_float(zv[k][t]) * rtf;
-          const float q = ok ? __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -ml)) : 0.f;
-          sum += q;
-          const float key = ok ? q * __builtin_amdgcn_rcpf(__uint_as_float(ev[k][t])) : -1.f;
-          const bool c1 = key > t2.v1, c2 = key > t2.v2;
-          t2.v2 = c1 ? t2.v1 : (c2 ? key : t2.v2);
-          t2.i2 = c1 ? t2.i1 : (c2 ? i : t2.i2);
-          t2.v1 = c1 ? key : t2.v1;
-          t2.i1 = c1 ? i : t2.i1;
-          nan_i = (key != key && nan_i == 0x7fffffff) ? i : nan_i;
-        }
+      for (int k = 0; k < kDraftStep; ++k) {
+        zc[k] = zn[k];
+        ec[k] = en[k];
       }
     }
   } else {
-    // unaligned rows: element loads, two passes
-    const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
-    if (a.greedy) {
-      for (int i = i0 + threadIdx.x; i < i1; i += kThreads)
-        if (better(z[i], i, t2.v1, t2.i1)) t2.v1 = z[i], t2.i1 = i;
-    } else {
-      for (int i = i0 + threadIdx.x; i < i1; i += kThreads) m = fmaxf(m, UNIT ? z[i] : z[i] * rtf);
-      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      __shared__ float s_m2[kWaves];
-      if ((threadIdx.x & 63) == 0) s_m2[threadIdx.x >> 6] = m;
-      __syncthreads();
-      m = s_m2[0];
-      for (int w = 1; w < kWaves; ++w) m = fmaxf(m, s_m2[w]);
-      const float ml = m == -INFINITY ? 0.f : m * kLog2e;
-      for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
-        const float x = UNIT ? z[i] : z[i] * rtf;
-        const float q = __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -ml));
-        sum += q;
-        t2.push(q * __builtin_amdgcn_rcpf(e[i]), i);
-        if (q != q && nan_i == 0x7fffffff) nan_i = i;
+    // unaligned rows: element loads
+    for (int i = i0 + threadIdx.x; i < i1; i += kThreads) {
+      const float zv = z[i];
+      if (a.greedy) {
+        if (better(zv, i, t1.v, t1.i)) t1.v = zv, t1.i = i;
+      } else {
+        const float x = UNIT ? zv : zv / tf;
+        const float xs[4] = {x, -INFINITY, -INFINITY, -INFINITY};
+        absorb4(xs);
+        key_visit(i, true, x, e[i]);
       }
     }
   }
-  if (nan_i != 0x7fffffff) {  // a NaN key leads the thread's list
-    t2.v2 = t2.v1;
-    t2.i2 = t2.i1;
-    t2.v1 = __uint_as_float(0x7fc00000u);
-    t2.i1 = nan_i;
-  }
-  t2.wave_reduce();
-  __shared__ float s_v1[kWaves], s_v2[kWaves];
-  __shared__ int s_i1[kWaves], s_i2[kWaves];
-  __shared__ float s_sum[kWaves];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  if (!a.greedy) t1.lead_nan(nan_i);
+  // chunk result: Top1 (greedy: argmax) and the online statistics
+  t1.wave_reduce();
+  wave_lse(m, sum);
+  __shared__ float s_v[kWaves], s_u[kWaves], s_uo[kWaves], s_m[kWaves], s_s[kWaves];
+  __shared__ int s_i[kWaves];
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
-    s_v1[w] = t2.v1;
-    s_v2[w] = t2.v2;
-    s_i1[w] = t2.i1;
-    s_i2[w] = t2.i2;
-    s_sum[w] = sum;
+    s_v[w] = t1.v;
+    s_u[w] = t1.u;
+    s_uo[w] = t1.uo;
+    s_i[w] = t1.i;
+    s_m[w] = m;
+    s_s[w] = sum;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float st = 0.f;
-    for (int k = 1; k < kWaves; ++k) t2.merge(s_v1[k], s_i1[k], s_v2[k], s_i2[k]);
-    for (int k = 0; k < kWaves; ++k) st += s_sum[k];
+    for (int k = 1; k < kWaves; ++k) {
+      t1.merge(s_v[k], s_u[k], s_uo[k], s_i[k]);
+      lse_combine(m, sum, s_m[k], s_s[k]);
+    }
     const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(a.part);
     const size_t o = ((size_t)b * nch + c) * sizeof(DraftPart);
-    store_coherent_b128(rp, o, u32x4_t{__float_as_uint(m), __float_as_uint(st), __float_as_uint(t2.v1),
-                                       __float_as_uint(t2.v2)});
-    store_coherent_b128(rp, o + 16, u32x4_t{(unsigned)t2.i1, (unsigned)t2.i2, 0u, 0u});
+    store_coherent_b128(rp, o, u32x4_t{__float_as_uint(m), __float_as_uint(sum), __float_as_uint(t1.v),
+                                       __float_as_uint(t1.u)});
+    store_coherent_b128(rp, o + 16, u32x4_t{__float_as_uint(t1.uo), (unsigned)t1.i, 0u, 0u});
   }
   __shared__ int s_last;
   if (!arrive_last(a.cnt + b, nch, &s_last)) return;
 
-  // The row's last workgroup: combine the slices (one wave), then the draw.
+  // The row's last workgroup: combine the chunks (one wave), then the draw.
   __shared__ int s_tok, s_exact;
   __shared__ float s_M, s_S;
   if (threadIdx.x < 64) {
     const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(a.part);
-    float M = -INFINITY;
-    float pm[4], ps[4], pv1[4], pv2[4];
-    int pi1[4], pi2[4];
-    int np = 0;
-    for (int k = threadIdx.x; k < nch; k += 64, ++np) {  // nch <= 256 at V <= 4M
+    Top1 r1;
+    r1.init();
+    float M = -INFINITY, S = 0.f;
+    for (int k = threadIdx.x; k < nch; k += 64) {  // nch <= 256 at V <= 4M
       const size_t o = ((size_t)b * nch + k) * sizeof(DraftPart);
       const u32x4_t lo = load_coherent_b128(rp, o), hi = load_coherent_b128(rp, o + 16);
-      pm[np] = __uint_as_float(lo.x);
-      ps[np] = __uint_as_float(lo.y);
-      pv1[np] = __uint_as_float(lo.z);
-      pv2[np] = __uint_as_float(lo.w);
-      pi1[np] = (int)hi.x;
-      pi2[np] = (int)hi.y;
-      M = fmaxf(M, pm[np]);
+      r1.merge(__uint_as_float(lo.z), __uint_as_float(lo.w), __uint_as_float(hi.x), (int)hi.y);
+      lse_combine(M, S, __uint_as_float(lo.x), __uint_as_float(lo.y));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    Top2 r2;
-    r2.init();
-    float S = 0.f;
-    for (int k = 0; k < np; ++k) {
-      if (a.greedy) {
-        r2.merge(pv1[k], pi1[k], -INFINITY, 0x7fffffff);
-      } else {
-        const float f = pm[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((pm[k] - M) * kLog2e);
-        S += ps[k] * f;
-        r2.merge(pv1[k] * f, pi1[k], pv2[k] * f, pi2[k]);
-      }
-    }
-    r2.wave_reduce();
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) S += __shfl_xor(S, o, 64);
+    r1.wave_reduce();
+    wave_lse(M, S);
     if (threadIdx.x == 0) {
-      s_tok = r2.i1;
+      s_tok = r1.i;
       s_M = M;
       s_S = S;
-      s_exact = !a.greedy && (isnan(r2.v1) || !(r2.v1 - r2.v2 > kTieRel * r2.v1));
+      // the bound's part common to every key, on both sides
+      const float common = fmaf(fabsf(M), kKeyRel, kKeyAbs);
+      // a NaN key: the exact race, where torch's softmax makes every key NaN
+      s_exact = !a.greedy && (isnan(r1.v) || !r1.certain(2.f * common));
     }
   }
   __syncthreads();
-  int token = s_tok;
+  int token = s_tok, rflag = 0;
   if (s_exact) {
     // torch's arithmetic: q = exp(x - M) / S, key = q / E, first max wins
     const float M = s_M, S = s_S;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    Top1 t2;
+    t2.init();
+    int nan2 = 0x7fffffff;
     for (int i = threadIdx.x; i < V; i += blockDim.x) {
-      const float x = UNIT ? z[i] : z[i] / a.tf;
+      const float x = UNIT ? z[i] : z[i] / tf;
       const float key = (expf(x - M) / S) / e[i];
-      if (better(key, i, bv, bi)) bv = key, bi = i;
+      t2.push(key, fmaf(key, kExactRel, key), i);
+      if (key != key && nan2 == 0x7fffffff) nan2 = i;
     }
-    block_argmax(bv, bi);
-    token = bi;
+    t2.lead_nan(nan2);
+    block_top1(t2);
+    token = t2.i;
+    if (!t2.certain(0.f)) rflag = SPV_FLAG_DRAW_BAND;
   }
-  if (threadIdx.x == 0) a.out[(size_t)b * a.out_stride] = token;
+  if (threadIdx.x == 0) {
+    const size_t ob = (size_t)b * a.out_stride;
+    a.out[ob] = token;
+    if (a.flags) a.flags[ob] = rflag;
+    if (a.stats) {
+      // (max, sum exp) of x; greedy rows: (max logit, argmax index bits)
+      const float2 st = a.greedy ? make_float2(__uint_as_float(0u), __int_as_float(token))
+                                 : make_float2(s_M, s_S);
+      reinterpret_cast<float2*>(a.stats)[ob] = st;
+    }
+  }
 }
 
 // ------------------------------------------------------- single-row helpers
@@ -1130,14 +1254,15 @@ size_t spv_verify_sample_workspace_bytes(int32_t B, int32_t gamma, int32_t V) {
 
 int spv_verify_sample(const float* target, const float* draft, int is_probs, float temperature,
                       const int32_t* proposals, const float* u_accept, const float* exp_noise,
-                      const int32_t* start_pos, const int32_t* remaining, int32_t eos_id, int32_t B, int32_t gamma,
-                      int32_t V, int32_t* accept_len, int32_t* out_tokens, int32_t* n_commit, int32_t* finished,
-                      int32_t* new_len, double* accept_prob, int32_t decide_only, void* workspace,
-                      size_t workspace_bytes, void* stream) {
+                      const float* draft_stats, const int32_t* start_pos, const int32_t* remaining, int32_t eos_id,
+                      int32_t B, int32_t gamma, int32_t V, int32_t* accept_len, int32_t* out_tokens,
+                      int32_t* n_commit, int32_t* finished, int32_t* new_len, double* accept_prob, int32_t* flags,
+                      int32_t decide_only, void* workspace, size_t workspace_bytes, void* stream) {
   if (!target || !draft || !proposals || !u_accept || B < 0 || B > 65535 || gamma < 1 || gamma > 32 || V < 1)
     return SPV_ERR_ARG;
   if (decide_only && !accept_prob) return SPV_ERR_ARG;
   if (!decide_only && (!accept_len || !out_tokens)) return SPV_ERR_ARG;
+  if (draft_stats && is_probs) return SPV_ERR_ARG;  // statistics of logits rows only
   if (B == 0) return SPV_OK;
   const bool greedy = !is_probs && !(temperature > 0.f);
   if (!decide_only && !greedy && !exp_noise) return SPV_ERR_ARG;
@@ -1148,15 +1273,17 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
   hipStream_t s = (hipStream_t)stream;
   const int nch = num_chunks(V);
   // Race partials and rows are addressed with 32-bit buffer offsets.
-  if ((size_t)B * nch * sizeof(RacePart) > 0x7fffffffu || (size_t)V * 4 > 0xffffffffu) return SPV_ERR_ARG;
+  if ((size_t)B * nch * sizeof(RacePart) > 0x7fffffffu || (size_t)V * 4 > 0x7fffffffu) return SPV_ERR_ARG;
   DecideArgs a{};
   a.target = target;
   a.draft = draft;
+  a.dstats = draft_stats;
   a.proposals = proposals;
   a.u = u_accept;
   a.accept_prob = accept_prob;
   a.accept_len = accept_len;
   a.out_tokens = out_tokens;
+  a.flags = flags;
   a.B = B;
   a.gamma = gamma;
   a.V = V;
@@ -1171,7 +1298,9 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
   // greedy or decide-only, the race, whose last workgroup per sequence commits.
   const bool unit = a.tf == 1.0f;
   if (!is_probs) {
-    const dim3 grid(B * (2 * gamma + 1));
+    const int rows = B * (draft_stats ? gamma + 1 : 2 * gamma + 1);
+    a.split = std::max(1, std::min(kMaxSplit, kStatGroups / rows));
+    const dim3 grid(rows * a.split);
     if (greedy)
       hipLaunchKernelGGL((row_stats_kernel<IN_GREEDY, true>), grid, dim3(kThreads), 0, s, a, cm, ws);
     else if (unit)
@@ -1195,16 +1324,16 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs, flo
 }
 
 size_t spv_draft_sample_workspace_bytes(int32_t B, int32_t V) {
-  if (B < 1 || B > 65535 || V < 1 || num_chunks(V) > 256) return 0;
-  return (size_t)SPV_SAMPLE_COUNTER_BYTES + (size_t)B * num_chunks(V) * sizeof(DraftPart);
+  if (B < 1 || B > 65535 || V < 1 || draft_chunks(V) > 256) return 0;
+  return (size_t)SPV_SAMPLE_COUNTER_BYTES + (size_t)B * draft_chunks(V) * sizeof(DraftPart);
 }
 
 int spv_draft_sample(const float* logits, int64_t row_stride, float temperature, const float* exp_noise,
-                     int32_t B, int32_t V, int32_t* out_tokens, int32_t out_stride, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     int32_t B, int32_t V, int32_t* out_tokens, int32_t out_stride, float* row_stats,
+                     int32_t* flags, void* workspace, size_t workspace_bytes, void* stream) {
   const bool greedy = !(temperature > 0.f);
   if (!logits || !out_tokens || B < 0 || B > 65535 || V < 1 || row_stride < V || out_stride < 1 ||
-      num_chunks(V) > 256 || (!greedy && !exp_noise))
+      draft_chunks(V) > 256 || (!greedy && !exp_noise))
     return SPV_ERR_ARG;
   if ((size_t)V * 4 > 0x7fffffffu) return SPV_ERR_ARG;
   if (B == 0) return SPV_OK;
@@ -1213,6 +1342,8 @@ int spv_draft_sample(const float* logits, int64_t row_stride, float temperature,
   a.logits = logits;
   a.noise = exp_noise;
   a.out = out_tokens;
+  a.stats = row_stats;
+  a.flags = flags;
   a.cnt = static_cast<int*>(workspace);
   a.part = reinterpret_cast<DraftPart*>(static_cast<char*>(workspace) + SPV_SAMPLE_COUNTER_BYTES);
   a.row_stride = row_stride;
@@ -1221,7 +1352,7 @@ int spv_draft_sample(const float* logits, int64_t row_stride, float temperature,
   a.out_stride = out_stride;
   a.greedy = greedy ? 1 : 0;
   a.tf = temperature_divisor(temperature);
-  const dim3 grid(num_chunks(V), B);
+  const dim3 grid(draft_chunks(V), B);
   if (a.tf == 1.0f)
     hipLaunchKernelGGL(draft_race_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
   else

@@ -24,6 +24,8 @@ SPV_ERR_UNSUPPORTED = -4
 SPV_CTR_WORDS = 16
 CTR_TOP, CTR_EXHAUSTED, CTR_SLOWPATH, CTR_PUSHED = 0, 1, 2, 3
 CTR_OVERFLOW, CTR_BAD_READ, CTR_ALIGN = 6, 7, 8  # sticky error words (see include/specverify.h)
+# bits of a sequence's flag word (sampling): a result the reference may have decided otherwise
+FLAG_ACCEPT_BAND, FLAG_DRAW_BAND, FLAG_TOP_P_BAND = 1, 2, 4
 
 SPV_F32, SPV_BF16, SPV_F16, SPV_FP8E4M3 = 0, 1, 2, 3
 _DTYPE_CODE = {torch.float32: SPV_F32, torch.bfloat16: SPV_BF16, torch.float16: SPV_F16}
@@ -68,10 +70,10 @@ SIGNATURES = {
     "spv_verify_attn_static_max_bytes": (S, []),
     "spv_verify_attn_static": (I, [P, P, I, P, P, I, P, P, I, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P]),
     "spv_verify_sample_workspace_bytes": (S, [I, I, I]),
-    "spv_verify_sample": (I, [P, P, I, F, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, I, P, S, P]),
+    "spv_verify_sample": (I, [P, P, I, F, P, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, P, I, P, S, P]),
     "spv_draft_sample_workspace_bytes": (S, [I, I]),
-    "spv_draft_sample": (I, [P, ctypes.c_int64, F, P, I, I, P, I, P, S, P]),
-    "spv_filter_logits": (I, [P, ctypes.c_int64, P, ctypes.c_int64, I, I, F, I, F, P]),
+    "spv_draft_sample": (I, [P, ctypes.c_int64, F, P, I, I, P, I, P, P, P, S, P]),
+    "spv_filter_logits": (I, [P, ctypes.c_int64, P, ctypes.c_int64, I, I, F, I, F, P, P]),
     "spv_logits_to_probs": (I, [P, P, I, I, F, P]),
     "spv_residual": (I, [P, P, P, I, P]),
     "spv_race_argmax": (I, [P, P, I, P, P]),
@@ -140,16 +142,21 @@ def filtering(top_k: int, top_p: float, vocab: int) -> bool:
     return (0 < int(top_k) < int(vocab)) or (0.0 < float(top_p) < 1.0)
 
 
-def filter_rows(z: torch.Tensor, temperature: float, top_k: int, top_p: float) -> torch.Tensor:
+def filter_rows(z: torch.Tensor, temperature: float, top_k: int, top_p: float, ambiguous: bool = False):
     """``spv_filter_logits`` over the rows of a float32 (..., V) tensor: the
-    scaled logits with what top-k / top-p drop set to -inf (a new tensor)."""
+    scaled logits with what top-k / top-p drop set to -inf (a new tensor).
+    With ``ambiguous``, also the int32 count per row (shape ``z.shape[:-1]``)
+    of values whose preceding mass lies within the rounding window of the
+    nucleus edge, where the reference's fp32 softmax may keep or drop them
+    otherwise: returns ``(out, counts)``."""
     z = z.float().contiguous()
     V = int(z.shape[-1])
     rows = z.numel() // V if V else 0
     out = torch.empty_like(z)
+    amb = torch.empty(z.shape[:-1], dtype=torch.int32, device=z.device) if ambiguous else None
     call("spv_filter_logits", ptr(z), V, ptr(out), V, rows, V, float(temperature), int(top_k), float(top_p),
-         stream_of(z.device))
-    return out
+         ptr(amb), stream_of(z.device))
+    return (out, amb) if ambiguous else out
 
 
 def i32(values, device: torch.device) -> torch.Tensor:

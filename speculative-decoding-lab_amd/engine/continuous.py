@@ -113,6 +113,10 @@ class DriverResult:
     draft_forward_calls: int = 0
     admitted: int = 0
     finished: int = 0
+    # sequence-rounds whose verify result, and draft draws, carry a flag: a
+    # result the reference's own fp32 softmax may have decided otherwise
+    flagged_rounds: int = 0
+    flagged_draws: int = 0
 
     @property
     def mean_tokens_per_round(self) -> float:
@@ -300,20 +304,24 @@ class SpecContinuousDriver:
             round_evs[0].record()
         sid_t = _hip.i32(sids, dev)
         st_t = _hip.i32(starts, dev)
-        d_outs = cu = None
+        d_outs = cu = d_stats = d_flags = None
         if self.draft_kv is not None:
-            # gamma draft steps from the draft cache's length (== start)
+            # gamma draft steps from the draft cache's length (== start); the
+            # draws keep each draft row's softmax statistics for the decisions
             max_ctx = max(starts)
             self.draft_kv._grow_width(self._blocks_for(max_ctx + self.gamma + 1, self.draft_kv))
             greedy = not self.temperature > 0
+            d_stats = torch.empty((B, self.gamma, 2), dtype=torch.float32, device=dev)
+            d_flags = torch.empty((B, self.gamma), dtype=torch.int32, device=dev)
             props, d_outs = self.draft_loop.run(
                 sid_t, st_t, max_ctx, inp["dq"], inp["dk"], inp["dv"],
-                [inp["draft"][:, j] for j in range(self.gamma)], None if greedy else inp["draft_noise"])
+                [inp["draft"][:, j] for j in range(self.gamma)], None if greedy else inp["draft_noise"],
+                stats=d_stats, flags=d_flags)
             inp["proposals"] = props
             result.draft_forward_calls += self.gamma
         outs = self.step_fn.attend_layers(sids, starts, inp["q"], inp["k"], inp["v"], events=evs)
         res = self.step_fn.sample_and_commit(sids, starts, inp["target"], inp["draft"], inp["proposals"],
-                                             inp["u"], inp["noise"], remaining)
+                                             inp["u"], inp["noise"], remaining, draft_stats=d_stats)
         if self.draft_kv is not None:
             sid_l = sid_t.long()
             pending = self._pending[sid_l]
@@ -327,12 +335,16 @@ class SpecContinuousDriver:
         if round_evs is not None:
             round_evs[1].record()
         # the round's one host synchronisation
-        counts = [res.n_commit, res.finished] + ([cu.count] if cu is not None else [])
+        counts = [res.n_commit, res.finished, res.flags] + (
+            [cu.count, (d_flags != 0).any(1).to(torch.int32)] if cu is not None else [])
         host = torch.stack(counts).tolist()
         n_commit, finished = host[0], host[1]
+        result.flagged_rounds += sum(1 for f in host[2] if f)
+        if cu is not None:
+            result.flagged_draws += sum(host[4])
         cu_outs = cu_rows = None
-        if cu is not None and any(host[2]):
-            cu_outs, cu_rows = self._catch_up(cu, host[2], sids, inp, result)
+        if cu is not None and any(host[3]):
+            cu_outs, cu_rows = self._catch_up(cu, host[3], sids, inp, result)
         dt = time.perf_counter() - t0
         gms = None
         if round_evs is not None:

@@ -51,25 +51,39 @@ def _draw_uniform(generator: torch.Generator) -> float:
 
 @dataclass
 class VerifyResult:
-    """Device int32 outputs of one verify-sampling launch."""
+    """Device int32 outputs of one verify-sampling launch.
+
+    ``flags[b]`` is 0 when sequence b's accepted list is the reference's for
+    the same logits, uniforms and noise. Given logits, p and q are this
+    library's fp32 softmax, a few 1e-6 from torch's; a nonzero word marks a
+    result the reference may have decided otherwise (``_hip.FLAG_*`` bits: a
+    uniform inside the error band of ``min(1, p/q)``, a drawn token within the
+    keys' error of another, a filtered row whose nucleus edge lies within
+    rounding)."""
 
     accept_len: torch.Tensor   # (B,) drafts accepted
     out_tokens: torch.Tensor   # (B, gamma+1) accepted drafts then the drawn token, -1 padded
     n_commit: torch.Tensor     # (B,) tokens kept after the budget / eos cut
     finished: torch.Tensor     # (B,) 1 = sequence finished this round
     new_len: torch.Tensor      # (B,) cache length to rewind to, -1 = no truncate
+    flags: Optional[torch.Tensor] = None  # (B,) flag word, 0 = certain
 
     def accepted_lists(self) -> List[List[int]]:
         lens = self.accept_len.tolist()
         toks = self.out_tokens.tolist()
         return [row[: n + 1] for row, n in zip(toks, lens)]
 
+    def flagged(self) -> List[int]:
+        """Batch positions whose result the reference may have decided otherwise."""
+        return [] if self.flags is None else [b for b, f in enumerate(self.flags.tolist()) if f]
+
 
 def _launch_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Tensor,
                    u: torch.Tensor, noise: Optional[torch.Tensor], temperature: float,
                    is_probs: bool, start_pos: Optional[torch.Tensor], remaining: Optional[torch.Tensor],
                    eos_id: Optional[int], decide_only: bool, accept_prob: Optional[torch.Tensor],
-                   result: Optional[VerifyResult]) -> None:
+                   result: Optional[VerifyResult], draft_stats: Optional[torch.Tensor] = None,
+                   flags: Optional[torch.Tensor] = None) -> None:
     B, C, V = (int(x) for x in target.shape)
     gamma = C - 1
     dev = target.device
@@ -78,12 +92,14 @@ def _launch_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.T
         raise ValueError("unsupported verify-sampling shape B={} gamma={} V={}".format(B, gamma, V))
     ws = _workspace.get(ws_bytes, dev)
     r = result
+    if flags is None and r is not None:
+        flags = r.flags
     call("spv_verify_sample", ptr(target), ptr(draft), 1 if is_probs else 0, float(temperature),
-         ptr(proposals), ptr(u), ptr(noise), ptr(start_pos), ptr(remaining),
+         ptr(proposals), ptr(u), ptr(noise), ptr(draft_stats), ptr(start_pos), ptr(remaining),
          -1 if eos_id is None else int(eos_id), B, gamma, V,
          ptr(r.accept_len) if r else None, ptr(r.out_tokens) if r else None,
          ptr(r.n_commit) if r else None, ptr(r.finished) if r else None,
-         ptr(r.new_len) if r else None, ptr(accept_prob), 1 if decide_only else 0,
+         ptr(r.new_len) if r else None, ptr(accept_prob), ptr(flags), 1 if decide_only else 0,
          ptr(ws), int(ws_bytes), _hip.stream_of(dev))
 
 
@@ -126,7 +142,7 @@ def align_draft(draft_kv: PagedKVCache, seq_ids: torch.Tensor, start_pos: torch.
 
 def _new_result(B: int, gamma: int, dev: torch.device) -> VerifyResult:
     z = lambda *s: torch.empty(s, dtype=torch.int32, device=dev)  # noqa: E731
-    return VerifyResult(z(B), z(B, gamma + 1), z(B), z(B), z(B))
+    return VerifyResult(z(B), z(B, gamma + 1), z(B), z(B), z(B), z(B))
 
 
 def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Tensor,
@@ -134,7 +150,8 @@ def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Te
                   start_pos: Optional[torch.Tensor] = None, remaining: Optional[torch.Tensor] = None,
                   eos_id: Optional[int] = None, is_probs: bool = False,
                   result: Optional[VerifyResult] = None, validate: bool = True,
-                  top_k: int = 0, top_p: float = 1.0) -> VerifyResult:
+                  top_k: int = 0, top_p: float = 1.0,
+                  draft_stats: Optional[torch.Tensor] = None) -> VerifyResult:
     """Fused accept / resample / bonus / commit cut of one round (device in, device out).
 
     ``target`` (B, gamma+1, V) and ``draft`` (B, gamma, V) are fp32 logits (or
@@ -142,7 +159,13 @@ def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Te
     uniforms; ``noise`` (B, V) ``Exp(1)`` rows (unused for greedy logits).
     ``top_k``/``top_p`` filter both sides' logits first (logits_to_probs,
     specdec/sampler.py:19-56; sampling mode only): every row is scaled and
-    filtered in one launch, then sampled at temperature 1.
+    filtered in one launch, then sampled at temperature 1; with top_p a
+    sequence whose rows have values within rounding of the nucleus edge gets
+    ``FLAG_TOP_P_BAND``. ``draft_stats`` (B, gamma, 2) float32: the draft
+    rows' statistics as ``draft_sample`` / ``DraftLoop`` wrote them when they
+    drew the proposals at this temperature (the draft loop's q,
+    spec_scheduler.py:243-252), so only the target rows are read for their
+    normalisers (not used with filters, which this call applies itself).
     ``validate=False`` skips the proposal-range check (a host synchronisation).
     """
     dev = _hip.require_gpu(target.device)
@@ -158,10 +181,17 @@ def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Te
         raise ValueError("sampling needs the Exp(1) noise rows")
     t = target.float().contiguous()
     d = draft.float().contiguous()
+    amb = None
     if not greedy and not is_probs and _hip.filtering(top_k, top_p, V):
-        t = _hip.filter_rows(t, temperature, top_k, top_p)
-        d = _hip.filter_rows(d, temperature, top_k, top_p)
+        t, amb_t = _hip.filter_rows(t, temperature, top_k, top_p, ambiguous=True)
+        d, amb_d = _hip.filter_rows(d, temperature, top_k, top_p, ambiguous=True)
+        amb = amb_t.sum(1) + amb_d.sum(1)
         temperature = 1.0
+        draft_stats = None
+    if draft_stats is not None:
+        if is_probs or tuple(draft_stats.shape) != (B, gamma, 2) or draft_stats.dtype != torch.float32 \
+                or not draft_stats.is_contiguous() or draft_stats.device != dev:
+            raise ValueError("draft_stats must be a contiguous (B, gamma, 2) float32 device tensor of logits rows")
     x = _hip.i32(proposals, dev)
     if validate and (int(x.min().item()) < 0 or int(x.max().item()) >= V):
         raise IndexError("proposal token ids must lie in [0, V)")
@@ -171,7 +201,10 @@ def verify_sample(target: torch.Tensor, draft: torch.Tensor, proposals: torch.Te
     rem = None if remaining is None else _hip.i32(remaining, dev)
     if result is None:
         result = _new_result(int(B), int(gamma), dev)
-    _launch_sample(t, d, x, uf, nz, temperature, is_probs, sp, rem, eos_id, False, None, result)
+    _launch_sample(t, d, x, uf, nz, temperature, is_probs, sp, rem, eos_id, False, None, result,
+                   draft_stats=draft_stats)
+    if amb is not None:
+        result.flags.bitwise_or_((amb > 0).to(torch.int32) * _hip.FLAG_TOP_P_BAND)
     return result
 
 
@@ -323,16 +356,20 @@ class VerifyStep:
     def sample_and_commit(self, seq_ids: Sequence[int], start_positions: Sequence[int],
                           target_logits: torch.Tensor, draft_logits: torch.Tensor,
                           proposals: torch.Tensor, u: torch.Tensor, noise: Optional[torch.Tensor],
-                          remaining: Optional[Sequence[int]] = None, apply: bool = True) -> VerifyResult:
+                          remaining: Optional[Sequence[int]] = None, apply: bool = True,
+                          draft_stats: Optional[torch.Tensor] = None) -> VerifyResult:
         """Fused accept / resample / bonus and the commit cut; then the pool's
-        rewind, or (``apply=False``) the commit held for the next round."""
+        rewind, or (``apply=False``) the commit held for the next round.
+        ``draft_stats``: the draft rows' statistics from the draft loop
+        (``verify_sample``)."""
         self.flush()
         dev = self.kv.device
         sid_t = _hip.i32(seq_ids, dev)
         st_t = _hip.i32(start_positions, dev)
         rem_t = None if remaining is None else _hip.i32(remaining, dev)
         res = verify_sample(target_logits, draft_logits, proposals, u, noise, self.temperature,
-                            start_pos=st_t, remaining=rem_t, eos_id=self.eos_id, validate=False)
+                            start_pos=st_t, remaining=rem_t, eos_id=self.eos_id, validate=False,
+                            draft_stats=draft_stats)
         if apply:
             self.kv.rewind_device(sid_t, res.new_len, res.finished)
         else:
@@ -341,7 +378,8 @@ class VerifyStep:
 
 
 def draft_sample(logits: torch.Tensor, temperature: float, noise: Optional[torch.Tensor] = None,
-                 out: Optional[torch.Tensor] = None, top_k: int = 0, top_p: float = 1.0) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, top_k: int = 0, top_p: float = 1.0,
+                 stats: Optional[torch.Tensor] = None, flags: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One draft step's proposals for every row in one launch (spec_scheduler.py:243-252).
 
     ``logits`` (B, V) fp32 draft logits (rows may be strided, elements
@@ -350,7 +388,11 @@ def draft_sample(logits: torch.Tensor, temperature: float, noise: Optional[torch
     ``noise`` (B, V), or the first-index argmax when ``temperature <= 0``
     (``noise`` unused). ``out``: an int32 device view of B entries to write
     (e.g. column s of the (B, gamma) proposals), else a new tensor. ``top_k``
-    / ``top_p`` filter the rows first (sampling mode). No host synchronisation.
+    / ``top_p`` filter the rows first (sampling mode). ``stats``: a float32
+    (B, 2) view (e.g. ``draft_stats[:, s]``) for each row's softmax statistics,
+    what ``verify_sample`` takes as ``draft_stats``; ``flags``: an int32 view
+    of B entries for each draw's flag word (``_hip.FLAG_DRAW_BAND`` when the
+    token's key lies within rounding of another's). No host synchronisation.
     """
     dev = _hip.require_gpu(logits.device)
     if logits.dim() != 2 or logits.stride(1) != 1 or logits.dtype != torch.float32:
@@ -367,12 +409,20 @@ def draft_sample(logits: torch.Tensor, temperature: float, noise: Optional[torch
         out = torch.empty(B, dtype=torch.int32, device=dev)
     if out.dtype != torch.int32 or out.dim() != 1 or out.numel() != B or out.device != dev:
         raise ValueError("out must be an int32 device vector of B entries")
+    stride = int(out.stride(0))
+    # the statistics and flags share the tokens' row stride (in their own units)
+    if stats is not None and (stats.dtype != torch.float32 or tuple(stats.shape) != (B, 2) or stats.stride(1) != 1
+                              or stats.stride(0) != 2 * stride or stats.device != dev):
+        raise ValueError("stats must be a float32 (B, 2) device view with row stride 2 x out's stride")
+    if flags is not None and (flags.dtype != torch.int32 or flags.dim() != 1 or flags.numel() != B
+                              or flags.stride(0) != stride or flags.device != dev):
+        raise ValueError("flags must be an int32 device view of B entries with out's stride")
     ws_bytes = _hip.lib().spv_draft_sample_workspace_bytes(max(B, 1), V)
     if ws_bytes == 0:
         raise ValueError("unsupported draft-sampling shape B={} V={}".format(B, V))
     ws = _draft_workspace.get(ws_bytes, dev)
     call("spv_draft_sample", ptr(logits), int(logits.stride(0)), float(temperature),
-         None if greedy else ptr(noise), B, V, ptr(out), int(out.stride(0)), ptr(ws), int(ws_bytes),
+         None if greedy else ptr(noise), B, V, ptr(out), stride, ptr(stats), ptr(flags), ptr(ws), int(ws_bytes),
          _hip.stream_of(dev))
     return out
 
@@ -418,13 +468,16 @@ class DraftLoop:
             v_steps: Sequence[Sequence[torch.Tensor]], logits_steps: Sequence[torch.Tensor],
             noise_steps: Optional[Sequence[torch.Tensor]] = None,
             proposals: Optional[torch.Tensor] = None,
-            attn_out: Optional[Sequence[Sequence[torch.Tensor]]] = None):
+            attn_out: Optional[Sequence[Sequence[torch.Tensor]]] = None,
+            stats: Optional[torch.Tensor] = None, flags: Optional[torch.Tensor] = None):
         """``seq_ids``/``ctx`` (B,) int32 device: the sequences and their draft
         cache lengths before the loop; ``max_ctx`` >= max(ctx) (host int).
         ``q_steps[s][l]`` (B, 1, Hq, d), ``k_steps``/``v_steps[s][l]`` (B, 1,
         Hkv, d), ``logits_steps[s]`` (B, V) fp32, ``noise_steps[s]`` (B, V)
-        Exp(1) rows (None when greedy). Returns (proposals (B, gamma) int32,
-        attention outputs [s][l])."""
+        Exp(1) rows (None when greedy). ``stats`` (B, gamma, 2) float32 and
+        ``flags`` (B, gamma) int32, optional: each step's draft-row statistics
+        (``VerifyStep.sample_and_commit(draft_stats=...)``) and draw flags.
+        Returns (proposals (B, gamma) int32, attention outputs [s][l])."""
         kv = self.kv
         dev = kv.device
         B = int(seq_ids.numel())
@@ -445,5 +498,6 @@ class DraftLoop:
                                                plan=plan))
             outs.append(outs_s)
             draft_sample(logits_steps[s], self.temperature, None if noise_steps is None else noise_steps[s],
-                         out=proposals[:, s])
+                         out=proposals[:, s], stats=None if stats is None else stats[:, s],
+                         flags=None if flags is None else flags[:, s])
         return proposals, outs

@@ -32,7 +32,11 @@ def test_attention_bytes_follow_the_formula():
 
 def test_sample_bytes_follow_the_formula():
     B, C, G, V = 32, 6, 5, 151936
-    assert bench.sample_bytes(B) == B * ((C + G) * V * 4 + V * 4 + G * 8 + 12)
+    # every row read for its statistics, then the noise row
+    assert bench.sample_bytes(B, draft_stats=False) == B * ((C + G) * V * 4 + V * 4 + G * 8 + 12)
+    # the draft rows' statistics from the draft sampler: target rows, noise row,
+    # the raced draft row, and per position u, proposal, q at it and the statistics
+    assert bench.sample_bytes(B) == B * ((C + 2) * V * 4 + G * (4 + 4 + 4 + 8) + 12)
 
 
 def test_workload_lengths_are_seeded_and_in_range():

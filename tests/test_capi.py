@@ -62,8 +62,10 @@ def test_argument_validation_needs_no_gpu(lib):
                                     fake, fake, None, None, fake, 1, 1, 0, 8, 16, 2, 64, None, None) == ARG
     assert lib.spv_kv_append(None, None, 1, None, None, None, 4, None, None, None, None, None, None,
                              None, 1, 1, 0, 8, 16, 2, 8, 1, 1, None) == ARG
-    assert lib.spv_verify_sample(None, None, 0, 1.0, None, None, None, None, None, -1, 1, 5, 8,
-                                 None, None, None, None, None, None, 0, None, 0, None) == ARG
+    assert lib.spv_verify_sample(None, None, 0, 1.0, None, None, None, None, None, None, -1, 1, 5, 8,
+                                 None, None, None, None, None, None, None, 0, None, 0, None) == ARG
+    assert lib.spv_draft_sample(None, 8, 1.0, None, 1, 8, None, 1, None, None, None, 0, None) == ARG
+    assert lib.spv_filter_logits(None, 8, None, 8, 1, 8, 1.0, 2, 1.0, None, None) == ARG
     assert lib.spv_race_argmax(None, None, 8, None, None) == ARG
     # fp8 append: no scales, then an input dtype the quantiser does not take
     assert lib.spv_kv_append_fp8(None, None, None, 0, None, None, None, 4, None, None, None, None, None,
