@@ -483,9 +483,19 @@ FD_BUDGET = (32, 160)         # new tokens per request, uniform
 FD_RATE = 4.0                 # Poisson arrivals per step once the first batch is in
 FD_SIGMA = 1.05               # draft = target + N(0, sigma^2): acceptance ~0.6 per draft
 FD_BREAKDOWN_ROUNDS = 3       # rounds with events around every layer's append and attention
+# The draft model of the whole-round variant: Qwen2.5-0.5B-shaped layers.
+DD_LAYERS, DD_HQ, DD_HKV, DD_D = 24, 14, 2, 64
 
 
-def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
+def pool_partition_ok(kv, cap):
+    """The pool invariant after a run: the free list and the block tables
+    together hold every block of the pool exactly once."""
+    owned = [blk for tab in kv.block_tables for blk in tab]
+    free = kv.allocator.free_list()
+    return len(owned) + len(free) == cap and sorted(owned + free) == list(range(cap))
+
+
+def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75, draft=False):
     """Continuous batching at full depth on one GPU.
 
     A pool sized to most of the device's free HBM (its free list shuffled, as
@@ -498,7 +508,13 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
     rounds record events around every layer's append and attention for the
     per-layer figures (those events add their own gaps between the kernels:
     about 330 us per round of 36 layers, so they are kept out of the round
-    times).
+    times). With ``draft`` the rounds are whole speculative rounds: a
+    Qwen2.5-0.5B-shaped draft model's pool beside the target's (24 layers,
+    14q/2kv heads, head_dim 64), gamma draft steps per round (per draft layer
+    the token's append and decode attention, then the batch's draws, which
+    keep the draft rows' statistics for the verify decisions), the verify
+    layers, sampling and commit, and the draft cache's alignment. At the end
+    the pools must be partitioned by their free lists and tables.
     """
     import statistics
 
@@ -510,23 +526,34 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
 
     chunk = FD_GAMMA + 1
     model = SyntheticVerifyModel(FD_LAYERS, FD_HQ, FD_HKV, FD_D, VOCAB, FD_GAMMA, FD_BATCH, dev,
-                                 torch.bfloat16, seed=seed, draft_sigma=FD_SIGMA, prompt_cap=FD_CTX[1])
+                                 torch.bfloat16, seed=seed, draft_sigma=FD_SIGMA, prompt_cap=FD_CTX[1],
+                                 draft_layers=DD_LAYERS if draft else 0, draft_heads=(DD_HQ, DD_HKV, DD_D))
     # The pool: pool_frac of the free HBM, in blocks of all 36 layers' K and V
-    # (engine.scheduler's sizing of the reference's build_kv).
+    # (engine.scheduler's sizing of the reference's build_kv); with the draft
+    # model, its pool takes a share in proportion to its bytes per block.
     block_bytes = bytes_per_block(FD_LAYERS, FD_BS, FD_HKV, FD_D, torch.bfloat16)
+    dblock_bytes = bytes_per_block(DD_LAYERS, FD_BS, DD_HKV, DD_D, torch.bfloat16)
     _free, total = torch.cuda.mem_get_info(dev)
+    tshare = block_bytes / (block_bytes + dblock_bytes) if draft else 1.0
     cap = blocks_for_hbm(FD_LAYERS, FD_BS, FD_HKV, FD_D, torch.bfloat16, dev, reserve_bytes=0,
-                         fraction=pool_frac)
+                         fraction=pool_frac * tshare)
     maxb = -(-(FD_CTX[1] + FD_BUDGET[1] + chunk) // FD_BS) + 1
     n_req = FD_BATCH + int(FD_RATE * (rounds + warmup + FD_BREAKDOWN_ROUNDS)) + 16
     kv = PagedKVCache(FD_LAYERS, FD_HKV, FD_D, cap, FD_BS, dev, torch.bfloat16, max_seqs=n_req,
                       max_blocks_per_seq=maxb)
     g = torch.Generator().manual_seed(seed + 1)
     kv.allocator.load_free_list(torch.randperm(cap, generator=g).to(torch.int32))
+    dkv, dcap = None, 0
+    if draft:
+        dcap = blocks_for_hbm(DD_LAYERS, FD_BS, DD_HKV, DD_D, torch.bfloat16, dev, reserve_bytes=0,
+                              fraction=pool_frac * (1.0 - tshare) / (1.0 - pool_frac * tshare))
+        dkv = PagedKVCache(DD_LAYERS, DD_HKV, DD_D, dcap, FD_BS, dev, torch.bfloat16, max_seqs=n_req,
+                           max_blocks_per_seq=maxb + 1)
+        dkv.allocator.load_free_list(torch.randperm(dcap, generator=g).to(torch.int32))
     first = poisson_requests(FD_BATCH, 0.0, FD_CTX[0], FD_CTX[1], *FD_BUDGET, seed=seed + 2)
     stream = poisson_requests(n_req - FD_BATCH, FD_RATE, FD_CTX[0], FD_CTX[1], *FD_BUDGET, seed=seed + 3,
                               first_sid=FD_BATCH)
-    drv = SpecContinuousDriver(kv, model, FD_GAMMA, FD_BATCH, temperature=1.0)
+    drv = SpecContinuousDriver(kv, model, FD_GAMMA, FD_BATCH, temperature=1.0, draft_kv=dkv)
     per_round = []
 
     def on_round(info):
@@ -538,6 +565,9 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
     res = drv.run(first + stream, max_steps=rounds + warmup + FD_BREAKDOWN_ROUNDS, on_round=on_round,
                   sync_timing=True, gpu_timing=lambda step: "round" if step < warmup + rounds else "layers")
     torch.cuda.synchronize()
+    # the pools after the run: every block exactly once, in a table or free
+    if not pool_partition_ok(kv, cap) or (dkv is not None and not pool_partition_ok(dkv, dcap)):
+        raise AssertionError("full depth: a pool is not partitioned by its free list and tables")
     timed = per_round[warmup:warmup + rounds]
     brk = per_round[warmup + rounds:]
     med = statistics.median
@@ -585,8 +615,18 @@ def full_depth(dev, rounds, warmup, seed=0, pool_frac=0.75):
         "finished": res.finished,
         "pool_blocks": cap,
         "peak_blocks": res.kv_peak_blocks,
+        "pool_partitioned": True,
     }
-    del kv, model, drv
+    if draft:
+        out["workload"] += "; with the draft side: a Qwen2.5-0.5B-shaped draft model ({} layers, {}q/{}kv heads, " \
+            "head_dim {}) over its own pool of {} blocks: gamma draft steps, verify, commit and the draft " \
+            "cache's alignment per round".format(DD_LAYERS, DD_HQ, DD_HKV, DD_D, dcap)
+        out["draft_pool_blocks"] = dcap
+        out["draft_peak_blocks"] = res.draft_kv_peak_blocks
+        out["draft_forward_calls_per_round"] = round(res.draft_forward_calls / max(res.rounds, 1), 2)
+        out["flagged_draws"] = res.flagged_draws
+    out["flagged_rounds"] = res.flagged_rounds
+    del kv, dkv, model, drv
     torch.cuda.empty_cache()
     return out
 
@@ -958,6 +998,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         print("bench: full-depth continuous batching", file=sys.stderr, flush=True)
         line["full_depth"] = full_depth(dev, args.full_depth_rounds, 4, args.seed)
+        print("bench: full-depth continuous batching with the draft side", file=sys.stderr, flush=True)
+        line["full_depth_draft"] = full_depth(dev, args.full_depth_rounds, 4, args.seed, draft=True)
     if not args.no_long_context:
         if args.full_depth_rounds <= 0:
             del g_step, g_att, g_smp, step, parts, res, w

@@ -60,6 +60,10 @@ class BlockAllocator:
         self._out = torch.zeros(2, dtype=torch.int32, device=device)
         self._free_count = self.capacity  # host mirror of ctr[0]
         self._stale = False
+        # counts the calls that may free blocks (rewinds, clears, alignments,
+        # frees, re-initialisation): a write plan's rows stay valid within the
+        # epoch that recorded them (allocation never moves an existing row)
+        self.epoch = 0
         self.reinit()
 
     # -- internal -------------------------------------------------------------
@@ -70,6 +74,7 @@ class BlockAllocator:
         """Free list back to ``[0 .. capacity-1]`` (kv.py:52)."""
         call("spv_pool_init", ptr(self.free_stack), ptr(self.free_flag), ptr(self.ctr),
              self.capacity, self._stream())
+        self.epoch += 1
         self._free_count = self.capacity
         self._stale = False
 
@@ -107,6 +112,7 @@ class BlockAllocator:
             # device stack cannot hold it, so it is rejected instead.
             raise ValueError("block id {} outside the pool [0, {})".format(block, self.capacity))
         self._refresh()
+        self.epoch += 1
         call("spv_pool_free_one", ptr(self.free_stack), ptr(self.free_flag), ptr(self.ctr),
              self.capacity, block, ptr(self._out[1:]), self._stream())
         if int(self._out[1].item()):
@@ -131,6 +137,7 @@ class BlockAllocator:
                 raise ValueError("free list holds duplicate ids")
             self.free_stack[:n] = ids_t
         self.free_flag.copy_(flags)
+        self.epoch += 1
         self.ctr.zero_()
         self.ctr[_hip.CTR_TOP] = n
         self._free_count = n
@@ -361,7 +368,7 @@ class PagedKVCache:
                      ptr(a.free_stack), ptr(a.free_flag), ptr(a.ctr), ptr(seq_ids), ptr(start_positions), B, chunk,
                      int(layer), a.capacity, self.block_size, self.num_kv_heads, self.head_dim, 1, -1,
                      ptr(plan.rows), self._stream())
-                plan.ready = True
+                plan._record(self.allocator.epoch, seq_ids, start_positions)
                 self._stale = True
                 self.allocator._stale = True
                 return
@@ -369,6 +376,9 @@ class PagedKVCache:
                 if (B, chunk) != (plan.B, plan.C):
                     raise ValueError("the chunk ({}, {}) does not match its write plan ({}, {})".format(
                         B, chunk, plan.B, plan.C))
+                if plan.epoch != self.allocator.epoch or plan.key != WritePlan._key(seq_ids, start_positions):
+                    raise ValueError("the write plan was recorded for another chunk, or before a later "
+                                     "call that may have freed its blocks")
                 call("spv_kv_write_planned", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
                      ptr(plan.rows), B, chunk, int(layer), self.allocator.capacity, self.block_size,
                      self.num_kv_heads, self.head_dim, self._stream())
@@ -444,6 +454,7 @@ class PagedKVCache:
         sid_t = _hip.i32(seq_ids, self.device)
         nl_t = _hip.i32(nl, self.device)
         fin_t = _hip.i32(fin, self.device)
+        self.allocator.epoch += 1
         call("spv_kv_rewind", ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev),
              ptr(self.lens_dev), ptr(self.allocator.free_stack), ptr(self.allocator.free_flag),
              ptr(self.allocator.ctr), ptr(sid_t), ptr(nl_t), ptr(fin_t), n, self.allocator.capacity, self.block_size,
@@ -473,6 +484,7 @@ class PagedKVCache:
         n = int(seq_ids.numel())
         if n == 0:
             return
+        self.allocator.epoch += 1
         call("spv_kv_rewind", ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev),
              ptr(self.lens_dev), ptr(self.allocator.free_stack), ptr(self.allocator.free_flag),
              ptr(self.allocator.ctr), ptr(seq_ids), ptr(new_lens), ptr(finished), n,
@@ -514,13 +526,14 @@ class PagedKVCache:
             plan._reserve(B, chunk, self.device)
             rows = plan.rows
         a = self.allocator
+        a.epoch += 1
         call("spv_kv_rewind_append", ptr(self.k_pool), ptr(self.v_pool), self._dt, ptr(k_new), ptr(v_new),
              ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
              ptr(a.free_stack), ptr(a.free_flag), ptr(a.ctr), ptr(seq_ids), ptr(new_lens), ptr(finished),
              ptr(start_positions), B, chunk, int(layer), a.capacity, self.block_size, self.num_kv_heads,
              self.head_dim, ptr(rows), self._stream())
         if rows is not None:
-            plan.ready = True
+            plan._record(a.epoch, seq_ids, start_positions)
         self._stale = True
         self.allocator._stale = True
 
@@ -543,6 +556,7 @@ class PagedKVCache:
         C = int(chunk_tokens.shape[1])
         if max_len is not None:
             self._grow_width(-(-int(max_len) // self.block_size))
+        self.allocator.epoch += 1
         call("spv_kv_draft_align", ptr(self.tables_dev), self._maxb, ptr(self.nblocks_dev), ptr(self.lens_dev),
              ptr(self.allocator.free_stack), ptr(self.allocator.free_flag), ptr(self.allocator.ctr), ptr(self.scales),
              self.num_layers, ptr(seq_ids), ptr(start_pos), ptr(n_commit), ptr(finished), ptr(chunk_tokens), C,
@@ -678,15 +692,30 @@ class WritePlan:
     """The pool rows one round's chunk was written to by its first layer's
     append (``write_block_device(..., alloc=True, plan=...)``), for the same
     chunk's appends into the round's later layers. A buffer of B x C int32 on
-    the device, reused across rounds; ``ready`` once recorded."""
+    the device, reused across rounds; ``ready`` once recorded. A planned write
+    must pass the very ``seq_ids`` / ``start_positions`` tensors the recording
+    call took (unchanged since) and come before any later call that may free
+    blocks (a rewind, clear, alignment or free); otherwise it raises instead of
+    copying into rows that belong to another chunk."""
 
     def __init__(self):
         self.rows: Optional[torch.Tensor] = None
         self.B = self.C = 0
         self.ready = False
+        self.epoch = -1
+        self.key = None
+
+    @staticmethod
+    def _key(seq_ids: torch.Tensor, starts: torch.Tensor):
+        return (seq_ids.data_ptr(), seq_ids._version, starts.data_ptr(), starts._version)
 
     def _reserve(self, B: int, C: int, device) -> None:
         if self.rows is None or self.rows.numel() < B * C or self.rows.device != device:
             self.rows = torch.empty(max(B * C, 64), dtype=torch.int32, device=device)
         self.B, self.C = B, C
         self.ready = False
+
+    def _record(self, epoch: int, seq_ids: torch.Tensor, starts: torch.Tensor) -> None:
+        self.epoch = epoch
+        self.key = WritePlan._key(seq_ids, starts)
+        self.ready = True

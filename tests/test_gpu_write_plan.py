@@ -121,3 +121,24 @@ def test_plan_rejects_a_different_chunk(cuda):
     planned.write_block_device(0, sid_t, st_t, k, k, alloc=True, plan=plan)
     with pytest.raises(ValueError, match="write plan"):
         planned.write_block_device(1, sid_t[:3], st_t[:3], k[:3], k[:3], alloc=False, plan=plan)
+
+
+def test_plan_rejects_another_batch_of_the_same_shape_and_a_changed_pool(cuda):
+    """A plan is tied to the tensors its recording call took and to the pool
+    state after it: another batch of the same (B, C), or any later call that
+    may change the tables (here a rewind), makes a planned write raise instead
+    of copying into the recorded rows."""
+    _, planned = _pools(cuda, 2, 2, 64, 64, 16, torch.bfloat16, 8)
+    sid_t = torch.arange(4, dtype=torch.int32, device=cuda)
+    st_t = torch.zeros(4, dtype=torch.int32, device=cuda)
+    k = torch.randn(4, 5, 2, 64, device=cuda).to(torch.bfloat16)
+    plan = WritePlan()
+    planned.write_block_device(0, sid_t, st_t, k, k, alloc=True, plan=plan)
+    planned.write_block_device(1, sid_t, st_t, k, k, alloc=False, plan=plan)  # the recorded chunk: fine
+    other = torch.arange(4, 8, dtype=torch.int32, device=cuda)
+    with pytest.raises(ValueError, match="write plan"):
+        planned.write_block_device(1, other, st_t, k, k, alloc=False, plan=plan)
+    planned.rewind_device(sid_t, torch.full((4,), 2, dtype=torch.int32, device=cuda),
+                          torch.zeros(4, dtype=torch.int32, device=cuda))
+    with pytest.raises(ValueError, match="write plan"):
+        planned.write_block_device(1, sid_t, st_t, k, k, alloc=False, plan=plan)
