@@ -462,56 +462,76 @@ __global__ __launch_bounds__(kPlannedThreads) void kv_write_planned_kernel(
   const int vec = (d * ES) >> 4;  // 16-byte pieces of one row
   const int np = C * vec;         // pieces of the chunk's K (and of its V)
   const int nth = blockDim.x;
-  uint4 kreg[kPlannedItems], vreg[kPlannedItems];
-  int dreg[kPlannedItems];
-#pragma unroll
-  for (int k = 0; k < kPlannedItems; ++k) {
-    const int ip = (int)threadIdx.x + k * nth;
-    if (ip < np) {
-      const size_t src = (((size_t)b * C + ip / vec) * row_elems + (size_t)h * d) * ES;
-      kreg[k] = reinterpret_cast<const uint4*>(knew + src)[ip % vec];
-      vreg[k] = reinterpret_cast<const uint4*>(vnew + src)[ip % vec];
-      dreg[k] = wplan[(size_t)b * C + ip / vec];
+  // Item k of this thread: piece threadIdx.x + k * nth of the chunk's K and of
+  // its V, and the pool row of its token (named registers: as arrays they
+  // were kept in scratch memory). Items past the first are loaded only when
+  // the chunk has them (a uniform branch); indices are clamped, and every use
+  // checks that the piece exists.
+  static_assert(kPlannedItems == 4, "four named items");
+  const int nitems = (np + nth - 1) / nth;
+  auto item_of = [&](int k) { return min((int)threadIdx.x + k * nth, np - 1); };
+  auto src_of = [&](int ip) { return (((size_t)b * C + ip / vec) * row_elems + (size_t)h * d) * ES + (size_t)(ip % vec) * 16; };
+  auto load_k = [&](int k) { return *reinterpret_cast<const uint4*>(knew + src_of(item_of(k))); };
+  auto load_v = [&](int k) { return *reinterpret_cast<const uint4*>(vnew + src_of(item_of(k))); };
+  auto load_d = [&](int k) { return wplan[(size_t)b * C + item_of(k) / vec]; };
+  uint4 k0 = load_k(0), v0 = load_v(0), k1 = k0, v1 = v0, k2 = k0, v2 = v0, k3 = k0, v3 = v0;
+  int d0 = load_d(0), d1 = d0, d2 = d0, d3 = d0;
+  if (nitems > 1) {
+    k1 = load_k(1), v1 = load_v(1), d1 = load_d(1);
+    if (nitems > 2) {
+      k2 = load_k(2), v2 = load_v(2), d2 = load_d(2);
+      if (nitems > 3) k3 = load_k(3), v3 = load_v(3), d3 = load_d(3);
     }
   }
+  auto store_k = [&](int ip, int dest, const uint4& kv) {
+    const size_t slot = ((size_t)layer * cap + dest / bs) * hkv + h;
+    reinterpret_cast<uint4*>(kpool + (slot * bs + dest % bs) * (size_t)(d * ES))[ip % vec] = kv;
+  };
   if (C <= 2) {
     // One or two tokens: every thread stores its pieces straight from its
     // registers (no transposition through LDS, no barrier).
     constexpr int kPer = 16 / ES;  // elements of a piece
-#pragma unroll
-    for (int k = 0; k < kPlannedItems; ++k) {
+    auto store_item = [&](int k, const uint4& kv, const uint4& vv, int dest) {
       const int ip = (int)threadIdx.x + k * nth;
-      if (ip < np && dreg[k] >= 0) {
-        const int dest = dreg[k], c = ip % vec;
-        const size_t slot = ((size_t)layer * cap + dest / bs) * hkv + h;
-        reinterpret_cast<uint4*>(kpool + (slot * bs + dest % bs) * (size_t)(d * ES))[c] = kreg[k];
-        T* vdst = reinterpret_cast<T*>(vpool) + slot * (size_t)d * bs + dest % bs;
-        T ve[kPer];
-        __builtin_memcpy(ve, &vreg[k], 16);
+      if (ip >= np || dest < 0) return;
+      store_k(ip, dest, kv);
+      const int c = ip % vec;
+      const size_t slot = ((size_t)layer * cap + dest / bs) * hkv + h;
+      T* vdst = reinterpret_cast<T*>(vpool) + slot * (size_t)d * bs + dest % bs;
+      // the piece's elements by vector subscripts (no address of the item taken)
+      const u32x4_t words = __builtin_bit_cast(u32x4_t, vv);
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) vdst[(size_t)(c * kPer + j) * bs] = ve[j];
+      for (int j = 0; j < kPer; ++j) {
+        const uint32_t wj = words[j * ES / 4];
+        vdst[(size_t)(c * kPer + j) * bs] = ES == 4 ? (T)wj : (T)(wj >> (8 * ES * (j % (4 / ES))));
       }
-    }
+    };
+    store_item(0, k0, v0, d0);
+    store_item(1, k1, v1, d1);
+    store_item(2, k2, v2, d2);
+    store_item(3, k3, v3, d3);
     return;
   }
   for (int o = threadIdx.x; o < C; o += nth) s_dest[o] = wplan[(size_t)b * C + o];
-#pragma unroll
-  for (int k = 0; k < kPlannedItems; ++k) {
+  auto stage_v = [&](int k, const uint4& vv) {
     const int ip = (int)threadIdx.x + k * nth;
-    if (ip < np) reinterpret_cast<uint4*>(s_v)[ip] = vreg[k];
-  }
+    if (ip < np) reinterpret_cast<uint4*>(s_v)[ip] = vv;
+  };
+  stage_v(0, v0);
+  stage_v(1, v1);
+  stage_v(2, v2);
+  stage_v(3, v3);
   __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kPlannedItems; ++k) {
+  auto store_kitem = [&](int k, const uint4& kv) {
     const int ip = (int)threadIdx.x + k * nth;
-    if (ip < np) {
-      const int dest = s_dest[ip / vec];
-      if (dest >= 0) {
-        const size_t slot = ((size_t)layer * cap + dest / bs) * hkv + h;
-        reinterpret_cast<uint4*>(kpool + (slot * bs + dest % bs) * (size_t)(d * ES))[ip % vec] = kreg[k];
-      }
-    }
-  }
+    if (ip >= np) return;
+    const int dest = s_dest[ip / vec];
+    if (dest >= 0) store_k(ip, dest, kv);
+  };
+  store_kitem(0, k0);
+  store_kitem(1, k1);
+  store_kitem(2, k2);
+  store_kitem(3, k3);
   const T* sv = reinterpret_cast<const T*>(s_v);
   for (int iv = threadIdx.x; iv < C * d; iv += nth) {
     const int e = iv / C, o = iv - e * C;  // tokens fastest

@@ -769,7 +769,11 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
   const uint16_t* qbase = static_cast<const uint16_t*>(p.q);
   const float sl2 = p.scale_log2;
 
-  for (long long x = x_begin; x < x_stop;) {
+  // The share's units left, 32-bit (a share holds far fewer than 2^31): with
+  // the piece's position it replaces the share's 64-bit end, one register
+  // fewer across the walk.
+  int left = (int)(x_stop - x_begin);
+  for (long long x = x_begin; left > 0;) {
     // T is opaque here: what depends on it (its double) is recomputed per
     // piece, not hoisted out of the loop and held across the walk.
     if constexpr (BAL) asm volatile("" : "+s"(T));
@@ -777,13 +781,14 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // the number of pieces (arrivals) of its segment.
     const bool first = PL && x == x_begin;  // planned: the head gave it
     if (!first) {
-      pc = decode_piece<BAL>(x, x_stop, s_pref, s_kpref, p.B, HR, KPC, T, nw, wg);
+      pc = decode_piece<BAL>(x, x + left, s_pref, s_kpref, p.B, HR, KPC, T, nw, wg);
       start = uni(s_start[pc.b]);
       sid = uni(s_sid[pc.b]);
     }
     const int b = pc.b, hr = pc.hr, lp0 = pc.lp0, lp1 = pc.lp1, slot = pc.slot, narr = pc.narr;
     const int x0 = pc.x0, w_a = pc.w_a;
     const long long Gs = pc.Gs;
+    left -= (int)(pc.x_next - x);
     x = pc.x_next;
     const int h = hr / p.nrg, rg = hr - h * p.nrg;
     const int seg = b * (int)HR + hr;
@@ -815,10 +820,16 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       } else if constexpr (NT >= 4) {
         const __amdgpu_buffer_rsrc_t rk = span_rsrc(kbase + slot, BS * D * 2);
         const __amdgpu_buffer_rsrc_t rv = span_rsrc(vbase + slot, BS * D * 2);
+        // the lane offsets from an opaque thread index, per load: nothing of
+        // them lives across the walk (at 256 registers it would spill)
+        int ltid = threadIdx.x;
+        asm volatile("" : "+v"(ltid));
+        const uint32_t lk = (uint32_t)((ltid & 15) * D + 8 * ((ltid >> 4) & 3)) * 2u;
+        const uint32_t lv = (uint32_t)((ltid & 15) * BS + 4 * ((ltid >> 4) & 3)) * 2u;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint4, load_b128(rk, koff, 64u * ks));
+        for (int ks = 0; ks < KS; ++ks) f.k[ks] = __builtin_bit_cast(uint4, load_b128(rk, lk, 64u * ks));
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) f.v[mt] = __builtin_bit_cast(uint2, load_b64(rv, voff, 32u * BS * mt));
+        for (int mt = 0; mt < MT; ++mt) f.v[mt] = __builtin_bit_cast(uint2, load_b64(rv, lv, 32u * BS * mt));
       } else {
         const uint16_t* kp = kbase + slot;
         const uint16_t* vp = vbase + slot;
@@ -837,12 +848,26 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // With four query tiles the row index and the ratio are opaque here, so
     // that what derives from them (the rows 16 nt + i16, the divisor's
     // reciprocal) is recomputed per piece rather than held across the walk.
+    // (With four query tiles the rows are not held at all: the few pages that
+    // reach the chunk's own keys recompute them, which frees the registers
+    // that otherwise spilled at head_dim 128.)
     int jt = threadIdx.x, ratio = p.ratio;
     if constexpr (NT == 4) asm volatile("" : "+v"(jt), "+s"(ratio));
     const int ji16 = jt & 15;
-    int jrow[NT];  // chunk row j of query column 16 nt + i16 (rows past nr repeat the last)
+    int jrow[NT == 4 ? 1 : NT];  // chunk row j of query column 16 nt + i16 (rows past nr repeat the last)
+    if constexpr (NT != 4) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + ji16, nr - 1)) / ratio;
+      for (int nt = 0; nt < NT; ++nt) jrow[nt] = (qr0 + min(16 * nt + ji16, nr - 1)) / ratio;
+    }
+    auto row_of = [&](int nt) {
+      if constexpr (NT != 4) {
+        return jrow[nt];
+      } else {
+        int mtid = threadIdx.x;
+        asm volatile("" : "+v"(mtid));
+        return (qr0 + min(16 * nt + (mtid & 15), nr - 1)) / p.ratio;
+      }
+    };
 
     // Stage the segment's query rows (zero past nr) and the first block ids
     // once the previous segment's LDS readers are done. Batched: every load is
@@ -1021,7 +1046,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
           for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj)
-              if (kpos0 + jj > start + jrow[nt]) sc[nt][jj] = -INFINITY;
+              if (kpos0 + jj > start + row_of(nt)) sc[nt][jj] = -INFINITY;
         }
         // (one compare per tile, on the largest of the lane's four scores)
         const float rsp = __builtin_amdgcn_rcpf(spage);
@@ -1031,13 +1056,34 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
           grow |= fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])) > t;
         }
       } else {
+        if constexpr (NT == 4) {
+          // the mask only on the pages that reach the chunk (a uniform branch)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+          for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            x[nt][jj] = sc[nt][jj] * spage;
-            if (need_mask && kpos0 + jj > start + jrow[nt]) x[nt][jj] = -INFINITY;
-            grow |= x[nt][jj] > m[nt] + kSlack;
+            for (int jj = 0; jj < 4; ++jj) x[nt][jj] = sc[nt][jj] * spage;
+          if (need_mask) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              const int jr = row_of(nt);
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj)
+                if (kpos0 + jj > start + jr) x[nt][jj] = -INFINITY;
+            }
+          }
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) grow |= x[nt][jj] > m[nt] + kSlack;
+        } else {
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              x[nt][jj] = sc[nt][jj] * spage;
+              if (need_mask && kpos0 + jj > start + jrow[nt]) x[nt][jj] = -INFINITY;
+              grow |= x[nt][jj] > m[nt] + kSlack;
+            }
           }
         }
       }
@@ -1338,8 +1384,15 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         // workgroups w_a .. w_b -- slot 2w when the segment holds the
         // workgroup's first page, else 2w + 1.
         if constexpr (BAL) {
+          // the segment's first unit, recomputed from the prefix arrays (with
+          // four query tiles nothing 64-bit of the piece is held across the walk)
+          long long gs = Gs;
+          if constexpr (NT == 4) {
+            const int pb = uni(s_pref[b]), npw = uni(s_pref[b + 1] - pb);
+            gs = HR * pb + (long long)hr * npw;
+          }
           merge_segment<QT, RPG, D>(
-              p, [&](int k) { return 2 * (w_a + k) + (page_start(w_a + k) >= Gs ? 0 : 1); }, narr, b, h, qr0, nr);
+              p, [&](int k) { return 2 * (w_a + k) + (page_start(w_a + k) >= gs ? 0 : 1); }, narr, b, h, qr0, nr);
         } else {
           merge_segment<QT, RPG, D>(p, [&](int k) { return x0 + k; }, narr, b, h, qr0, nr);
         }
@@ -1473,6 +1526,9 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
     pl.nrg = (G + pl.rows_per_group - 1) / pl.rows_per_group;
     // One arrival counter per segment.
     if ((long long)B * Hkv * pl.nrg > kCounterWords) pl.mfma = false;
+    // The units of the batch (pages plus each segment's piece cost, per
+    // segment) fit 31 bits, so a share's units left are an int.
+    if ((long long)Hkv * pl.nrg * B * (max_pages + 256) >= (1LL << 31)) pl.mfma = false;
   }
   if (!pl.mfma) {
     pl.nt = 0;
