@@ -44,6 +44,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "spv_common.h"
 
@@ -65,6 +66,16 @@ static_assert(kChunk % (4 * kThreads) == 0, "every thread of a race chunk takes 
 constexpr int kMaxSplit = 8;
 constexpr int kStatGroups = 640;
 constexpr int kVecPerThread = kChunk / 4 / kThreads;
+// The race streams its chunk in steps of kRaceStep float4 of p, q and E per
+// thread, the next step's loads in flight while one is raced, and races the
+// steps that lie wholly inside the row without per-element masks (83 VGPRs,
+// 5 waves per SIMD; with masks everywhere the compiler took 181). Per
+// sampling call (B = 32, gamma = 5, V = 151,936, draft statistics given):
+// steps of 2 took 45.6 us, of 1 45.9, of 5 47.3; the whole chunk's loads
+// issued at once, with masks, 48.9.
+constexpr int kRaceStep = 2;
+constexpr int kRaceSteps = kVecPerThread / kRaceStep;
+static_assert(kVecPerThread % kRaceStep == 0, "whole race steps");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr double kEps = 1e-12;     // specdec/sampler.py:16
 // Relative rounding of the race's fast keys against the same key formed with
@@ -760,9 +771,9 @@ __device__ __forceinline__ void finalize_seq(const DecideArgs& a, const CommitAr
 // with its bound and the others' largest bound. Keys use x * (1 / T) and a
 // hardware reciprocal of E: they differ from keys formed with torch's
 // arithmetic by a few ulp (kTieRel). In logits mode each key also carries the
-// error of its p and q against torch's softmax: (ep p + eq q + kap) / E. All
-// loads of the chunk are issued before the first is used (buffer loads past
-// the row end return zero and count as absent).
+// error of its p and q against torch's softmax: (ep p + eq q + kap) / E. The
+// chunk streams in kRaceSteps steps (buffer loads past the row end return zero
+// and count as absent).
 template <bool RESID, bool UNIT, bool PROBS>
 __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& info, int b, int c, Top1& t1,
                                            float& rs, float& ps, const float* __restrict__ e) {
@@ -814,21 +825,35 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
     const uint32_t row_bytes = (uint32_t)V * 4u;
     const __amdgpu_buffer_rsrc_t bp = span_rsrc(pr, row_bytes), bq = span_rsrc(qr, row_bytes),
                                  be = span_rsrc(e, row_bytes);
-    u32x4_t zp[kVecPerThread], zq[kVecPerThread], ev[kVecPerThread];
+    u32x4_t zp[2][kRaceStep], zq[2][kRaceStep], ev[2][kRaceStep];
+    auto load_step = [&](int st, int slot) {
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const uint32_t off = (uint32_t)vec_index(c, k) * 16u;
-      zp[k] = load_b128(bp, off);
-      if (RESID) zq[k] = load_b128(bq, off);
-      ev[k] = load_b128(be, off);
-    }
+      for (int j = 0; j < kRaceStep; ++j) {
+        const uint32_t off = (uint32_t)vec_index(c, st * kRaceStep + j) * 16u;
+        zp[slot][j] = load_b128(bp, off);
+        if (RESID) zq[slot][j] = load_b128(bq, off);
+        ev[slot][j] = load_b128(be, off);
+      }
+    };
+    load_step(0, 0);
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i4 = vec_index(c, k);
-      const u32x4_t q4 = RESID ? zq[k] : zp[k];
+    for (int st = 0; st < kRaceSteps; ++st) {
+      const int cur = st & 1;
+      if (st + 1 < kRaceSteps) load_step(st + 1, cur ^ 1);
+      auto race_step = [&](auto full) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        visit(4 * i4 + t, i4 < n4, __uint_as_float(zp[k][t]), __uint_as_float(q4[t]), __uint_as_float(ev[k][t]));
+        for (int j = 0; j < kRaceStep; ++j) {
+          const int i4 = vec_index(c, st * kRaceStep + j);
+          const u32x4_t q4 = RESID ? zq[cur][j] : zp[cur][j];
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            visit(4 * i4 + t, full ? true : i4 < n4, __uint_as_float(zp[cur][j][t]), __uint_as_float(q4[t]),
+                  __uint_as_float(ev[cur][j][t]));
+        }
+      };
+      // only the row's last chunk has a step that reaches past its end
+      if (c * (kChunk / 4) + (st + 1) * kRaceStep * kThreads <= n4) race_step(std::true_type{});
+      else race_step(std::false_type{});
     }
   } else {
     const int i0 = c * kChunk, i1 = min(V, i0 + kChunk);
