@@ -74,6 +74,7 @@ constexpr int kVecPerThread = kChunk / 4 / kThreads;
 // steps of 2 took 45.6 us, of 1 45.9, of 5 47.3; the whole chunk's loads
 // issued at once, with masks, 48.9.
 constexpr int kRaceStep = 2;
+constexpr int kRaceRing = 2;  // steps in the register ring: kRaceRing - 1 in flight while one is raced
 constexpr int kRaceSteps = kVecPerThread / kRaceStep;
 static_assert(kVecPerThread % kRaceStep == 0, "whole race steps");
 constexpr float kLog2e = 1.4426950408889634f;
@@ -825,21 +826,24 @@ __device__ __forceinline__ void race_chunk(const DecideArgs& a, const RaceInfo& 
     const uint32_t row_bytes = (uint32_t)V * 4u;
     const __amdgpu_buffer_rsrc_t bp = span_rsrc(pr, row_bytes), bq = span_rsrc(qr, row_bytes),
                                  be = span_rsrc(e, row_bytes);
-    u32x4_t zp[2][kRaceStep], zq[2][kRaceStep], ev[2][kRaceStep];
+    u32x4_t zp[kRaceRing][kRaceStep], zq[kRaceRing][kRaceStep], ev[kRaceRing][kRaceStep];
+    // one lane offset for every load, the step's part in a scalar operand
+    const uint32_t lane_off = threadIdx.x * 16u;
     auto load_step = [&](int st, int slot) {
 #pragma unroll
       for (int j = 0; j < kRaceStep; ++j) {
-        const uint32_t off = (uint32_t)vec_index(c, st * kRaceStep + j) * 16u;
-        zp[slot][j] = load_b128(bp, off);
-        if (RESID) zq[slot][j] = load_b128(bq, off);
-        ev[slot][j] = load_b128(be, off);
+        const uint32_t off = (uint32_t)(c * (kChunk / 4) + (st * kRaceStep + j) * kThreads) * 16u;
+        zp[slot][j] = load_b128(bp, lane_off, off);
+        if (RESID) zq[slot][j] = load_b128(bq, lane_off, off);
+        ev[slot][j] = load_b128(be, lane_off, off);
       }
     };
-    load_step(0, 0);
+#pragma unroll
+    for (int st = 0; st < kRaceRing - 1; ++st) load_step(st, st);
 #pragma unroll
     for (int st = 0; st < kRaceSteps; ++st) {
-      const int cur = st & 1;
-      if (st + 1 < kRaceSteps) load_step(st + 1, cur ^ 1);
+      const int cur = st % kRaceRing;
+      if (st + kRaceRing - 1 < kRaceSteps) load_step(st + kRaceRing - 1, (st + kRaceRing - 1) % kRaceRing);
       auto race_step = [&](auto full) {
 #pragma unroll
         for (int j = 0; j < kRaceStep; ++j) {
@@ -922,7 +926,10 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
 // (max, argmax index), the verify step's greedy format.
 // Elements of a row per workgroup, a multiple of 4 x kThreads: 10,240 (15
 // chunks at V = 151,936) drew 32 rows in 16.6 us, 19,456 in 17.3, 5,120 in
-// 20.2 and 2,048 in 36.7; four float4 per step instead of two measured the same.
+// 20.2 and 2,048 in 36.7. The chunk streams in steps of kDraftStep float4 per
+// thread through a two-step ring of named slots: 16.2 us (one float4 per step
+// 16.4, five 16.4; the earlier loop, whose slot copies waited for the step in
+// flight, 16.5).
 constexpr int kDraftChunk = 10240;
 static_assert(kDraftChunk % (4 * kThreads) == 0, "every thread of a draft chunk takes whole float4");
 constexpr int kDraftStep = 2;        // float4 of logits and of noise per thread per step
@@ -988,55 +995,55 @@ __global__ __launch_bounds__(kThreads) void draft_race_kernel(DraftArgs a) {
     const uint32_t row_bytes = (uint32_t)V * 4u;
     const __amdgpu_buffer_rsrc_t bz = span_rsrc(z, row_bytes), be = span_rsrc(e, row_bytes);
     constexpr int kStep = kDraftStep * kThreads;  // float4 per step and workgroup
-    const int nstep = (n4 - j0 + kStep - 1) / kStep;
-    // Vector j of the chunk, or the row's end (the load returns zero without a
-    // memory access) for vectors beyond the chunk, which belong to the next one.
-    auto off_of = [&](int j) { return j < n4 ? (uint32_t)j * 16u : row_bytes; };
-    u32x4_t zc[kDraftStep], ec[kDraftStep], zn[kDraftStep], en[kDraftStep];
+    constexpr int kSteps = kDraftChunk / 4 / kStep;
+    static_assert(kDraftChunk % (4 * kStep) == 0, "whole steps per chunk");
+    // Named slots of a two-step ring, every load at one lane offset (the step's
+    // part in a scalar operand); vectors past the row end return zero without
+    // a memory access and count as absent. Steps wholly inside the row take no
+    // per-element masks.
+    const uint32_t lane_off = threadIdx.x * 16u;
+    u32x4_t zs[2][kDraftStep], es[2][kDraftStep];
+    auto load_step = [&](int st, int slot) {
 #pragma unroll
-    for (int k = 0; k < kDraftStep; ++k) {
-      const uint32_t o = off_of(j0 + threadIdx.x + k * kThreads);
-      zc[k] = load_b128(bz, o);
-      if (!a.greedy) ec[k] = load_b128(be, o);
-    }
-    for (int stp = 0; stp < nstep; ++stp) {
-      const int base = j0 + stp * kStep;
-      if (stp + 1 < nstep) {
+      for (int k = 0; k < kDraftStep; ++k) {
+        const uint32_t off = (uint32_t)(j0 + st * kStep + k * kThreads) * 16u;
+        zs[slot][k] = load_b128(bz, lane_off, off);
+        if (!a.greedy) es[slot][k] = load_b128(be, lane_off, off);
+      }
+    };
+    load_step(0, 0);
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      const int cur = st & 1;
+      if (st + 1 < kSteps) load_step(st + 1, cur ^ 1);
+      const int base = j0 + st * kStep;
+      auto visit_step = [&](auto full) {
 #pragma unroll
         for (int k = 0; k < kDraftStep; ++k) {
-          const uint32_t o = off_of(base + kStep + threadIdx.x + k * kThreads);
-          zn[k] = load_b128(bz, o);
-          if (!a.greedy) en[k] = load_b128(be, o);
-        }
-      }
+          const int j = base + threadIdx.x + k * kThreads;
+          const bool ok = full ? true : j < n4;
+          if (a.greedy) {
+            // first-index argmax of the raw logits (torch.argmax: NaN wins)
 #pragma unroll
-      for (int k = 0; k < kDraftStep; ++k) {
-        const int j = base + threadIdx.x + k * kThreads;
-        const bool ok = j < n4;
-        if (a.greedy) {
-          // first-index argmax of the raw logits (torch.argmax: NaN wins)
+            for (int t = 0; t < 4; ++t) {
+              const float v = __uint_as_float(zs[cur][k][t]);
+              if (ok && better(v, 4 * j + t, t1.v, t1.i)) t1.v = v, t1.i = 4 * j + t;
+            }
+          } else {
+            float xs[4];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float v = __uint_as_float(zc[k][t]);
-            if (ok && better(v, 4 * j + t, t1.v, t1.i)) t1.v = v, t1.i = 4 * j + t;
+            for (int t = 0; t < 4; ++t) {
+              const float zv = __uint_as_float(zs[cur][k][t]);
+              xs[t] = ok ? (UNIT ? zv : div_fast(zv, tf, rtf)) : -INFINITY;
+            }
+            absorb4(xs);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) key_visit(4 * j + t, ok, xs[t], __uint_as_float(es[cur][k][t]));
           }
-        } else {
-          float xs[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float zv = __uint_as_float(zc[k][t]);
-            xs[t] = ok ? (UNIT ? zv : div_fast(zv, tf, rtf)) : -INFINITY;
-          }
-          absorb4(xs);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) key_visit(4 * j + t, ok, xs[t], __uint_as_float(ec[k][t]));
         }
-      }
-#pragma unroll
-      for (int k = 0; k < kDraftStep; ++k) {
-        zc[k] = zn[k];
-        ec[k] = en[k];
-      }
+      };
+      if (base + kStep <= n4) visit_step(std::true_type{});
+      else visit_step(std::false_type{});
     }
   } else {
     // unaligned rows: element loads
