@@ -74,7 +74,9 @@ constexpr int kVecPerThread = kChunk / 4 / kThreads;
 // steps of 2 took 45.6 us, of 1 45.9, of 5 47.3; the whole chunk's loads
 // issued at once, with masks, 48.9.
 constexpr int kRaceStep = 2;
-constexpr int kRaceRing = 2;  // steps in the register ring: kRaceRing - 1 in flight while one is raced
+// Steps in the register ring, kRaceRing - 1 in flight while one is raced: 3
+// and 4 (with steps of 1 or 2 float4) measured the same as 2.
+constexpr int kRaceRing = 2;
 constexpr int kRaceSteps = kVecPerThread / kRaceStep;
 static_assert(kVecPerThread % kRaceStep == 0, "whole race steps");
 constexpr float kLog2e = 1.4426950408889634f;
