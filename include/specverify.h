@@ -454,7 +454,7 @@ int spv_verify_sample(const float* target, const float* draft, int is_probs,
  * draft_stats. flags (may be NULL): row b's SPV_FLAG_* word at
  * flags[b * out_stride]. One launch for the batch; the workspace's first
  * SPV_SAMPLE_COUNTER_BYTES hold arrival counters that must be zero when it is
- * first used and are zero after every call. V <= 2,621,440. */
+ * first used and are zero after every call. V <= 3,145,728. */
 size_t spv_draft_sample_workspace_bytes(int32_t B, int32_t V);
 int spv_draft_sample(const float* logits, int64_t row_stride, float temperature,
                      const float* exp_noise, int32_t B, int32_t V,

@@ -60,11 +60,11 @@ constexpr int kThreads = 256;
 static_assert(kChunk % (4 * kThreads) == 0, "every thread of a race chunk takes whole float4");
 // The row statistics split each row into up to kMaxSplit contiguous pieces,
 // floor(kStatGroups / rows) of them: a batch of 32 with the draft rows'
-// statistics given has 192 rows (3 pieces: 49.7 us per sampling call against
-// about 52 with whole rows; 8 pieces 56 us), with every row read 352 (whole
-// rows: 61 us; 2 pieces 63 us, 3 pieces 69 us).
+// statistics given has 192 rows (2 pieces: 43.4 us per sampling call against
+// 45.9 with 3 pieces, 48.4 with whole rows), with every row read 352 (whole
+// rows: 57.7 us; 2 pieces were slower).
 constexpr int kMaxSplit = 8;
-constexpr int kStatGroups = 640;
+constexpr int kStatGroups = 512;
 constexpr int kVecPerThread = kChunk / 4 / kThreads;
 // The race streams its chunk in steps of kRaceStep float4 of p, q and E per
 // thread, the next step's loads in flight while one is raced, and races the
@@ -926,13 +926,13 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
 // key = q / E (flagging a draw still within a few ulp of another key).
 // Greedy rows keep the chunk's first-index argmax; their statistics are
 // (max, argmax index), the verify step's greedy format.
-// Elements of a row per workgroup, a multiple of 4 x kThreads: 10,240 (15
-// chunks at V = 151,936) drew 32 rows in 16.6 us, 19,456 in 17.3, 5,120 in
-// 20.2 and 2,048 in 36.7. The chunk streams in steps of kDraftStep float4 per
-// thread through a two-step ring of named slots: 16.2 us (one float4 per step
-// 16.4, five 16.4; the earlier loop, whose slot copies waited for the step in
-// flight, 16.5).
-constexpr int kDraftChunk = 10240;
+// Elements of a row per workgroup, a multiple of 4 x kThreads x kDraftStep.
+// The chunk streams in steps of kDraftStep float4 per thread through a
+// two-step ring of named slots. 32 rows at V = 151,936: 12,288 (13 chunks)
+// 16.1 us, 10,240 16.3, 8,192 16.9, 16,384 16.9, 20,480 16.9; steps of one or
+// five float4 16.4 (at 10,240; the earlier loop, whose slot copies waited for
+// the step in flight, 16.5).
+constexpr int kDraftChunk = 12288;
 static_assert(kDraftChunk % (4 * kThreads) == 0, "every thread of a draft chunk takes whole float4");
 constexpr int kDraftStep = 2;        // float4 of logits and of noise per thread per step
 constexpr float kKeyRel = 4.76837158203125e-07f;  // 2^-21
