@@ -872,10 +872,11 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
     // Stage the segment's query rows (zero past nr) and the first block ids
     // once the previous segment's LDS readers are done. Batched: every load is
     // issued before that barrier and before any of them is stored, so the
-    // staging costs one round trip, not one per item. The head_dim-128
-    // kernels with four query tiles, or three in the cost-balanced split, keep
-    // the item-by-item loop: the batch's registers make them spill there.
-    constexpr bool kBatchStage = D == 64 || NT <= 2 || (NT == 3 && !BAL);
+    // staging costs one round trip, not one per item (with four query tiles
+    // at head_dim 128: 88 -> 87 us per layer at batch 128, Qwen2.5-3B heads).
+    // The head_dim-128 kernels with three query tiles in the cost-balanced
+    // split keep the item-by-item loop: the batch's registers make them spill.
+    constexpr bool kBatchStage = D == 64 || NT <= 2 || NT == 4 || (NT == 3 && !BAL);
     if constexpr (kBatchStage) {
       static_assert(kTabChunk == kMfmaThreads, "one block id per thread");
       constexpr int kQItems = (RPG * (D / 8) + kMfmaThreads - 1) / kMfmaThreads;
