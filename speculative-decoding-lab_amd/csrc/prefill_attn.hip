@@ -16,10 +16,16 @@
 // barrier per tile. Per 16-key part of a tile and query tile:
 //   S^T = K Q^T    v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims (LDS),
 //                  B = Q^T fragments held in registers for the whole walk;
-//   O^T += V^T P^T two v_mfma_f32_16x16x32_bf16 per pair of 16-key parts,
+//   O^T += V^T P^T one v_mfma_f32_16x16x32_f16 per pair of 16-key parts,
 //                  A = V^T (LDS, one 16-byte read: keys of both parts), B =
-//                  P_hi, then P_lo: P split into two bf16 halves, so P V
-//                  carries ~16 significant bits of P, not 8.
+//                  P in fp16 (11 significant bits; a bf16 P, 8 bits, missed
+//                  the bf16 output bar). V is staged as fp16 times 2^k, one
+//                  exponent k per workgroup chosen from the first key tile's
+//                  largest finite |v| (which lands in [2^8, 2^9)): every bf16
+//                  value in range is then exact in fp16. A later tile with a
+//                  value that would pass 65504 (128x the first tile's largest)
+//                  lowers k -- O is multiplied by the power of two, exactly --
+//                  and is staged again. Inf and NaN stay what they are.
 // The accumulator layout of S^T is the operand layout of P^T (lane l: keys
 // 4 (l / 16) .. + 3 of query column l % 16), so the softmax moves no data.
 // Online softmax with a per-column reference maximum that scores may exceed by
@@ -41,6 +47,9 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
@@ -64,6 +73,27 @@ struct PrefillParams {
 
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+__device__ __forceinline__ uint32_t pack2_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
+
+// Largest finite |v| of the bf16 values packed in w (two per word), as the
+// bits of a non-negative float (integer order is float order there).
+__device__ __forceinline__ uint32_t max_finite_abs2(uint32_t w, uint32_t m) {
+  const uint32_t lo = w & 0x7fffu, hi = (w >> 16) & 0x7fffu;
+  if ((lo & 0x7f80u) != 0x7f80u) m = max(m, lo);
+  if ((hi & 0x7f80u) != 0x7f80u) m = max(m, hi);
+  return m;
+}
+
+// The staging exponent for a largest finite |v| of mx: mx 2^k in [2^8, 2^9)
+// (k = 0 for an all-zero tile), within float's normal exponents.
+__device__ __forceinline__ int stage_exponent(float mx) {
+  if (!(mx > 0.f)) return 0;
+  int e;
+  frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1)
+  return min(126, max(-126, 9 - e));
 }
 
 template <int NT, int D>
@@ -161,7 +191,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
       }
     }
   };
-  auto store_tile = [&](int buf) {
+  float vs = 1.f, vlim = 65504.f;  // V staging factor 2^k, and the largest |v| it keeps in fp16
+  int vk = 0;
+  auto store_tile = [&](int buf) -> bool {
+    bool ovf = false;
 #pragma unroll
     for (int i = 0; i < kKPer; ++i) {
       const int c = threadIdx.x + i * kThreads;
@@ -179,16 +212,65 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
         const int pos = 32 * (k >> 5) + 8 * ((k >> 2) & 3) + 4 * ((k >> 4) & 1) + (k & 3);
         const uint32_t a[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
         const uint32_t bb[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
+        u16x2_t mx = u16x2_t{0, 0};  // largest |v| bits, per half
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // dims 8 col + 2 e (low halves) and + 1 (high halves): keys k, k + 1
-          const uint32_t lo = (a[e] & 0xffffu) | (bb[e] << 16);
-          const uint32_t hi = (a[e] >> 16) | (bb[e] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e) * VP + pos]) = lo;
-          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e + 1) * VP + pos]) = hi;
+          const float x0 = __uint_as_float(a[e] << 16), x1 = __uint_as_float(bb[e] << 16);
+          const float y0 = __uint_as_float(a[e] & 0xffff0000u), y1 = __uint_as_float(bb[e] & 0xffff0000u);
+          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e) * VP + pos]) = pack2_f16(x0 * vs, x1 * vs);
+          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e + 1) * VP + pos]) = pack2_f16(y0 * vs, y1 * vs);
+          mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, a[e] & 0x7fff7fffu));
+          mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, bb[e] & 0x7fff7fffu));
+        }
+        const uint32_t mh = max((uint32_t)mx[0], (uint32_t)mx[1]);
+        if (mh < 0x7f80u) {
+          ovf |= __uint_as_float(mh << 16) > vlim;
+        } else {
+          // an inf or NaN among them: a finite value past the fp16 range
+          // decides (inf and NaN pass as they are)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t w4[2] = {a[e], bb[e]};
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const uint32_t lo = w4[q] & 0x7fffu, hi = (w4[q] >> 16) & 0x7fffu;
+              ovf |= (lo < 0x7f80u && __uint_as_float(lo << 16) > vlim) |
+                     (hi < 0x7f80u && __uint_as_float(hi << 16) > vlim);
+            }
+          }
         }
       }
     }
+    return ovf;
+  };
+  // The workgroup's largest finite |v| of the staged tile (vreg), every thread.
+  __shared__ uint32_t s_vmax[kWaves];
+  auto tile_vmax = [&]() {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        m = max_finite_abs2(vreg[i][e].x, m);
+        m = max_finite_abs2(vreg[i][e].y, m);
+        m = max_finite_abs2(vreg[i][e].z, m);
+        m = max_finite_abs2(vreg[i][e].w, m);
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+    if (lane == 0) s_vmax[w] = m;
+    __syncthreads();
+    uint32_t mm = s_vmax[0];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) mm = max(mm, s_vmax[k]);
+    __syncthreads();  // s_vmax is reused by the next call
+    return __uint_as_float(mm << 16);
+  };
+  auto set_scale = [&](int k) {
+    vk = k;
+    vs = ldexpf(1.f, k);
+    vlim = ldexpf(65504.f, -k);
   };
 
   f32x4_t o[MT][NT];
@@ -208,6 +290,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
   const float sl2 = p.scale_log2, inv_sl2 = 1.f / p.scale_log2;
 
   load_tile(0);
+  set_scale(stage_exponent(tile_vmax()));
   store_tile(0);
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
@@ -267,14 +350,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
         thr[nt] = (m_new + kSlack) * inv_sl2;
       }
     }
-    // P = 2^(s sl2 - m) as hi + lo bf16 halves, two 16-key parts per operand;
-    // row sums take P itself.
+    // P = 2^(s sl2 - m) in fp16, two 16-key parts per operand; row sums take
+    // P itself.
     float mu[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) mu[nt] = m[nt] == -INFINITY ? 0.f : m[nt];
 #pragma unroll
     for (int q2 = 0; q2 < 2; ++q2) {
-      uint32_t ph[NT][4], pl[NT][4];
+      uint32_t ph[NT][4];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -284,34 +367,37 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[kt][nt][jj], sl2, -mu[nt]));
           l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
-          const bf16x2_t h01 = __builtin_convertvector(f32x2_t{e[0], e[1]}, bf16x2_t);
-          const bf16x2_t h23 = __builtin_convertvector(f32x2_t{e[2], e[3]}, bf16x2_t);
-          const f32x2_t r01 = f32x2_t{e[0], e[1]} - __builtin_convertvector(h01, f32x2_t);
-          const f32x2_t r23 = f32x2_t{e[2], e[3]} - __builtin_convertvector(h23, f32x2_t);
-          ph[nt][2 * h] = __builtin_bit_cast(uint32_t, h01);
-          ph[nt][2 * h + 1] = __builtin_bit_cast(uint32_t, h23);
-          pl[nt][2 * h] = pack2_bf16(r01[0], r01[1]);
-          pl[nt][2 * h + 1] = pack2_bf16(r23[0], r23[1]);
+          ph[nt][2 * h] = pack2_f16(e[0], e[1]);
+          ph[nt][2 * h + 1] = pack2_f16(e[2], e[3]);
         }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         // V^T row (dim 16 mt + i16): keys 4 g .. + 3 of parts 2 q2 and 2 q2 + 1
-        const bf16x8_t va =
-            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&Vt[(16 * mt + i16) * VP + 32 * q2 + 8 * g]));
+        const f16x8_t va =
+            __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(&Vt[(16 * mt + i16) * VP + 32 * q2 + 8 * g]));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              va, __builtin_bit_cast(bf16x8_t, make_uint4(ph[nt][0], ph[nt][1], ph[nt][2], ph[nt][3])), o[mt][nt],
-              0, 0, 0);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              va, __builtin_bit_cast(bf16x8_t, make_uint4(pl[nt][0], pl[nt][1], pl[nt][2], pl[nt][3])), o[mt][nt],
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              va, __builtin_bit_cast(f16x8_t, make_uint4(ph[nt][0], ph[nt][1], ph[nt][2], ph[nt][3])), o[mt][nt],
               0, 0, 0);
       }
     }
-    if (t + 1 < ntiles) store_tile(buf ^ 1);  // that buffer's readers finished before the last barrier
-    __syncthreads();
+    bool ovf = false;
+    if (t + 1 < ntiles) ovf = store_tile(buf ^ 1);  // that buffer's readers finished before the last barrier
+    if (__syncthreads_or(ovf)) {
+      // Tile t + 1 holds a value past fp16 at this k: a smaller k from its
+      // largest value, O into the new units (a power of two: exact), the tile
+      // staged again. The old k's stores are overwritten before the barrier.
+      const int k = min(vk, stage_exponent(tile_vmax()));
+      const float f = ldexpf(1.f, k - vk);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) o[mt][nt] *= f;
+      set_scale(k);
+      store_tile(buf ^ 1);
+      __syncthreads();
+    }
   }
 
   // Row sums over the four lane groups, then the normalised rows.
@@ -324,7 +410,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
   for (int nt = 0; nt < NT; ++nt) {
     const int R = (w * NT + nt) * 16 + i16;
     if (R / ratio >= p.BM || cpos[nt] >= Lc) continue;
-    const float inv = cvalid[nt] ? 1.f / l[nt] : 0.f;  // padded positions: zeros
+    const float inv = cvalid[nt] ? ldexpf(1.f / l[nt], -vk) : 0.f;  // padded positions: zeros
     uint16_t* orow = ob + (((size_t)b * Lc + cpos[nt]) * Hq + chead[nt]) * D;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {

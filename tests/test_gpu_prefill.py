@@ -10,6 +10,10 @@ engine/attention.py:121-167) against the oracle.
   against the oracle in fp32 on the same bf16 values at the bf16 bar (per row
   relative L2 <= 2e-3, every element within one bf16 ulp + 2e-3 max |ref|);
   the padding is filled with NaN and must not reach any output;
+* V of any magnitude on the MFMA path, which stages V in fp16 times a power of
+  two taken from the first key tile: tiles 10^6 apart (the later tile past
+  fp16 at the first tile's scale, so O is rescaled and the tile staged
+  again), values near 1e30 and near 1e-30, a first tile of zeros;
 * fp16 and fp32 inputs (VALU path);
 * the same keys attended by prefill and by paged verify attention from
   position 0 agree.
@@ -28,8 +32,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _bf16_check(out, want, lengths):
-    out = out.float().cpu()
-    want = want.float()
+    out = out.double().cpu()  # float64: the norms of outputs near 1e30 stay finite
+    want = want.double()
     for b, n in enumerate(lengths):
         if n == 0:
             continue
@@ -101,6 +105,29 @@ def test_bf16_head_ratios(cuda, Hq, Hkv, d, lengths):
     q, k, v = _chunk(B, Lc, Hq, Hkv, d, lengths, seed=Hq * 100 + d)
     out = paged_attention_prefill_chunk(q.to(cuda), k.to(cuda), v.to(cuda), Hq, lengths)
     _check_padding(out, lengths)
+    want = ref_attn.paged_attention_prefill_chunk(q.float(), k.float(), v.float(), Hq, lengths)
+    _bf16_check(out, want, lengths)
+
+
+@pytest.mark.parametrize("case", ["rising", "falling", "huge", "tiny", "zero_first"])
+@pytest.mark.parametrize("d", [128, 64])
+def test_bf16_value_magnitudes(cuda, case, d):
+    Hq, Hkv, lengths = 8, 2, [400, 190]
+    B, Lc = len(lengths), max(lengths)
+    q, k, v = _chunk(B, Lc, Hq, Hkv, d, lengths, seed=7 + d, nan_pad=False)
+    pos = torch.arange(Lc, dtype=torch.float32)[None, :, None, None]
+    if case == "rising":  # keys 0..63 small, later ones 10^6 larger: a rescale after the first tile
+        f = torch.where(pos < 64, 1e-3, 1e3)
+    elif case == "falling":
+        f = torch.where(pos < 64, 1e3, 1e-3)
+    elif case == "huge":
+        f = torch.full_like(pos, 1e30)
+    elif case == "tiny":
+        f = torch.full_like(pos, 1e-30)
+    else:  # the first tile all zero: its scale is 1, the next tile sets none smaller unless it must
+        f = torch.where(pos < 64, 0.0, 3e4)
+    v = (v.float() * f).to(torch.bfloat16)
+    out = paged_attention_prefill_chunk(q.to(cuda), k.to(cuda), v.to(cuda), Hq, lengths)
     want = ref_attn.paged_attention_prefill_chunk(q.float(), k.float(), v.float(), Hq, lengths)
     _bf16_check(out, want, lengths)
 
