@@ -46,7 +46,7 @@ import torch
 from . import _hip
 from .attention import verify_attention
 from .kv import PagedKVCache
-from .spec_scheduler import DraftCatchUp, DraftLoop, VerifyResult, VerifyStep, align_draft
+from .spec_scheduler import DraftCatchUp, DraftLoop, VerifyResult, VerifyStep, align_draft, draft_sample
 
 
 @dataclass
@@ -135,7 +135,9 @@ class SyntheticVerifyModel:
     Per layer one set of queries / keys / values for ``max_batch`` sequences is
     drawn once and its first ``B`` rows serve every round; ``n_sets`` sets of
     logits (with proposals, uniforms and noise) alternate between rounds. Prompt
-    K/V come from one bank of ``prompt_cap`` token rows.
+    K/V come from one bank of ``prompt_cap`` token rows. Without a draft side
+    the proposals are given, and so are the draft rows' softmax statistics at
+    ``temperature`` (as the draft sampler keeps them when it draws).
     """
 
     def __init__(self, num_layers: int, num_q_heads: int, num_kv_heads: int, head_dim: int, vocab: int,
@@ -146,6 +148,7 @@ class SyntheticVerifyModel:
         C = gamma + 1
         self.num_layers, self.gamma, self.vocab = num_layers, gamma, vocab
         self.draft_layers = draft_layers
+        self.temperature = float(temperature)
         self.q = [torch.randn(max_batch, C, num_q_heads, head_dim, device=device, generator=g).to(dtype)
                   for _ in range(num_layers)]
         self.k = [torch.randn(max_batch, C, num_kv_heads, head_dim, device=device, generator=g).to(dtype)
@@ -162,8 +165,15 @@ class SyntheticVerifyModel:
             proposals = torch.multinomial(probs, 1, generator=g).reshape(max_batch, gamma).to(torch.int32)
             u = torch.rand(max_batch, gamma, device=device, generator=g)
             noise = torch.empty(max_batch, vocab, device=device).exponential_(1, generator=g)
-            self.sets.append((target.contiguous(), draft.contiguous(), proposals, u, noise))
-            del probs
+            draft = draft.contiguous()
+            # the draft rows' statistics as the draft sampler writes them (its
+            # tokens are not used: the proposals above are the round's)
+            dstats = torch.empty(max_batch, gamma, 2, dtype=torch.float32, device=device)
+            scratch = torch.empty(max_batch, gamma, dtype=torch.int32, device=device)
+            for j in range(gamma):
+                draft_sample(draft[:, j], temperature, noise, out=scratch[:, j], stats=dstats[:, j])
+            self.sets.append((target.contiguous(), draft, proposals, u, noise, dstats))
+            del probs, scratch
         if draft_layers:
             # draft side: per step and draft layer one token's q / k / v (the
             # catch-up decode uses step 0's), a prompt bank, and per set the
@@ -188,10 +198,11 @@ class SyntheticVerifyModel:
 
     def round_inputs(self, round_idx: int, B: int) -> dict:
         i = round_idx % len(self.sets)
-        target, draft, proposals, u, noise = self.sets[i]
+        target, draft, proposals, u, noise, dstats = self.sets[i]
         inp = {
             "q": [x[:B] for x in self.q], "k": [x[:B] for x in self.k], "v": [x[:B] for x in self.v],
             "target": target[:B], "draft": draft[:B], "proposals": proposals[:B], "u": u[:B], "noise": noise[:B],
+            "draft_stats": dstats[:B],
         }
         if self.draft_layers:
             inp["dq"] = [[x[:B] for x in st] for st in self.dq]
@@ -320,6 +331,8 @@ class SpecContinuousDriver:
             inp["proposals"] = props
             result.draft_forward_calls += self.gamma
         outs = self.step_fn.attend_layers(sids, starts, inp["q"], inp["k"], inp["v"], events=evs)
+        if d_stats is None and self.model.temperature == self.temperature:
+            d_stats = inp["draft_stats"]  # the given proposals' draft statistics
         res = self.step_fn.sample_and_commit(sids, starts, inp["target"], inp["draft"], inp["proposals"],
                                              inp["u"], inp["noise"], remaining, draft_stats=d_stats)
         if self.draft_kv is not None:
