@@ -858,7 +858,7 @@ def main() -> int:
                     help="skip the 32768-token fp8 / bf16 verify-attention measurement")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: the library has no multi-GPU path "
               "(--gpus {} requested)".format(args.gpus), file=sys.stderr)
         return 2
 

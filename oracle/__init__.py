@@ -13,8 +13,8 @@ path the HIP library implements:
                           (engine/spec_scheduler.py:269-322)
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker (or the timed CPU
-baseline). The product path (``speculative-decoding-lab_amd``) never imports it
+``bench.py`` may import this package, and only to check results (or as the timed
+CPU baseline). The product path (``speculative-decoding-lab_amd``) never imports it
 and has no CPU fallback.
 
 Pinning status (what checks each function against something other than its own

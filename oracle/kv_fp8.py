@@ -1,7 +1,7 @@
 """CPU restatement of the fp8 (OCP e4m3) KV pool (test infrastructure only).
 
 The reference pool stores K/V in the model dtype (engine/kv.py:99-101); an fp8
-pool with one fp32 scale per (layer, block, K | V) is this build's storage
+pool with one fp32 scale per (layer, block, K | V) is the library's own storage
 format for long contexts. Its rule, restated here from the device kernels:
 
 * a stored code q means ``decode(q) * scale`` (fp32 product);
