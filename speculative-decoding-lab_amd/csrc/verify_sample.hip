@@ -932,9 +932,8 @@ __global__ __launch_bounds__(kThreads) void race_kernel(DecideArgs a, CommitArgs
 // Elements of a row per workgroup, a multiple of 4 x kThreads x kDraftStep.
 // The chunk streams in steps of kDraftStep float4 per thread through a
 // two-step ring of named slots. 32 rows at V = 151,936: 12,288 (13 chunks)
-// 16.1 us, 10,240 16.3, 8,192 16.9, 16,384 16.9, 20,480 16.9; steps of one or
-// five float4 16.4 (at 10,240; the earlier loop, whose slot copies waited for
-// the step in flight, 16.5).
+// 15.0 us, 8,192 16.1, 16,384 15.1; steps of one float4 15.0, three 15.5,
+// four 16.0 (four at 16,384: 16.1).
 constexpr int kDraftChunk = 12288;
 static_assert(kDraftChunk % (4 * kThreads) == 0, "every thread of a draft chunk takes whole float4");
 constexpr int kDraftStep = 2;        // float4 of logits and of noise per thread per step
