@@ -44,7 +44,7 @@ from typing import Callable, List, Optional, Sequence
 import torch
 
 from . import _hip
-from .attention import verify_attention
+from .attention import VerifyPlan, verify_attention
 from .kv import PagedKVCache
 from .spec_scheduler import DraftCatchUp, DraftLoop, VerifyResult, VerifyStep, align_draft, draft_sample
 
@@ -345,11 +345,9 @@ class SpecContinuousDriver:
         if per_layer:
             evs.append(torch.cuda.Event(enable_timing=True))
             evs[-1].record()
-        if round_evs is not None:
-            round_evs[1].record()
         # the round's one host synchronisation
         counts = [res.n_commit, res.finished, res.flags] + (
-            [cu.count, (d_flags != 0).any(1).to(torch.int32)] if cu is not None else [])
+            [cu.count, (d_flags != 0).any(1).to(torch.int32), cu.pos] if cu is not None else [])
         host = torch.stack(counts).tolist()
         n_commit, finished = host[0], host[1]
         result.flagged_rounds += sum(1 for f in host[2] if f)
@@ -357,7 +355,11 @@ class SpecContinuousDriver:
             result.flagged_draws += sum(host[4])
         cu_outs = cu_rows = None
         if cu is not None and any(host[3]):
-            cu_outs, cu_rows = self._catch_up(cu, host[3], sids, inp, result)
+            cu_outs, cu_rows = self._catch_up(host[3], host[5], sids, inp, result)
+        if round_evs is not None:
+            round_evs[1].record()
+        if sync_timing:
+            torch.cuda.synchronize(dev)  # the catch-up's launches are the round's too
         dt = time.perf_counter() - t0
         gms = None
         if round_evs is not None:
@@ -388,25 +390,36 @@ class SpecContinuousDriver:
         self.running = keep
         result.rounds += 1
 
-    def _catch_up(self, cu: DraftCatchUp, counts: List[int], sids: List[int], inp: dict,
-                  result: DriverResult):
-        """Decode the catch-up positions the alignment reported (their blocks
-        and lengths are in place): per draft layer a one-token write and decode
-        attention for the sequences concerned (spec_scheduler.py:308-319, here
-        batched over the sequences). Returns the attention outputs of the last
-        catch-up position per layer and the batch rows decoded."""
-        pos = cu.pos.tolist()
+    def _catch_up(self, counts: List[int], pos: List[int], sids: List[int], inp: dict, result: DriverResult):
+        """Decode the catch-up positions the alignment reported (``counts`` and
+        first positions ``pos`` per batch row, read with the round's host
+        synchronisation; their blocks and lengths are in place): per draft layer
+        a one-token write and decode attention for the sequences concerned
+        (spec_scheduler.py:308-319, here batched over the sequences). Per
+        catch-up position one pinned upload of the rows' ids and positions, then
+        only device-argument calls: no host synchronisation. Returns the
+        attention outputs of the last catch-up position per layer and the batch
+        rows decoded."""
+        dev = self.kv.device
         rows_all = [b for b, c in enumerate(counts) if c > 0]
         outs = None
         for j in range(max(counts)):
             rows = [b for b in rows_all if counts[b] > j]
-            idx = torch.tensor(rows, dtype=torch.long, device=self.kv.device)
-            rs = [sids[b] for b in rows]
             ps = [pos[b] + j for b in rows]
+            meta = torch.tensor([[sids[b] for b in rows], ps, rows], dtype=torch.int32, pin_memory=True)
+            meta = meta.to(dev, non_blocking=True)
+            rs_t, ps_t, idx = meta[0], meta[1], meta[2].long()
+            max_ctx = max(ps) + 1
+            plan = None
             outs = []
             for layer in range(self.model.draft_layers):
-                self.draft_kv.write_block(layer, rs, ps, inp["dk"][0][layer][idx], inp["dv"][0][layer][idx])
-                outs.append(verify_attention(inp["dq"][0][layer][idx], self.draft_kv, layer, rs, ps, max(ps) + 1))
+                q = inp["dq"][0][layer][idx]
+                # the alignment allocated these positions' blocks: no allocation here
+                self.draft_kv.write_block_device(layer, rs_t, ps_t, inp["dk"][0][layer][idx],
+                                                 inp["dv"][0][layer][idx], alloc=False)
+                if plan is None:
+                    plan = VerifyPlan(self.draft_kv, rs_t, ps_t, 1, int(q.shape[2]), max_ctx)
+                outs.append(verify_attention(q, self.draft_kv, layer, rs_t, ps_t, max_ctx, plan=plan))
             result.draft_forward_calls += 1
         return outs, rows_all
 
