@@ -105,8 +105,14 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
-    rc = getattr(lib(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != SPV_OK:
         raise HipLibraryError("{} failed: {} ({})".format(name, _ERRORS.get(rc, "error"), rc))
 
@@ -124,7 +130,12 @@ def require_gpu(device: torch.device) -> torch.device:
 
 
 def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of ``device``'s current stream (the capturing stream
+    inside a graph capture)."""
+    idx = device.index if isinstance(device, torch.device) else torch.device(device).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -182,12 +193,13 @@ class Workspace:
         self._retired: list = []
 
     @staticmethod
-    def _key(device: torch.device):
+    def _key(device: torch.device, stream: Optional[int] = None):
         device = torch.device(device)
-        return device.index, torch.cuda.current_stream(device).cuda_stream
+        return device.index, stream_of(device) if stream is None else stream
 
-    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
-        key = self._key(device)
+    def get(self, nbytes: int, device: torch.device, stream: Optional[int] = None) -> torch.Tensor:
+        """The buffer of ``stream`` (default: the current stream) on ``device``."""
+        key = self._key(device, stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
             if buf is not None:

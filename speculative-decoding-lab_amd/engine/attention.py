@@ -83,6 +83,7 @@ class VerifyPlan:
         self.start = _hip.i32(start_positions, kv.device)
         self.B = int(self.seq_ids.numel())
         self.chunk, self.num_q_heads, self.max_ctx = int(chunk), int(num_q_heads), int(max_ctx)
+        self.ws_bytes: Optional[int] = None  # the calls' workspace size, asked by the first
         if self.max_ctx > kv.max_blocks_per_seq * kv.block_size:
             kv._grow_width(-(-self.max_ctx // kv.block_size))
         nbytes = int(_hip.lib().spv_verify_attn_plan_bytes(max(self.B, 1)))
@@ -134,17 +135,24 @@ def verify_attention(query_3d: torch.Tensor, kv: PagedKVCache, layer: int,
     if max_ctx > kv.max_blocks_per_seq * kv.block_size:
         kv._grow_width(-(-max_ctx // kv.block_size))
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
-    ws_bytes = _hip.lib().spv_verify_attn_workspace_bytes(B, chunk, hq, kv.num_kv_heads, d,
-                                                          kv.block_size, int(max_ctx))
-    ws = _workspace.get(ws_bytes, kv.device) if ws_bytes else None
+    if plan is not None:  # a round's calls share their shapes: the size is asked once
+        if plan.ws_bytes is None:
+            plan.ws_bytes = int(_hip.lib().spv_verify_attn_workspace_bytes(B, chunk, hq, kv.num_kv_heads, d,
+                                                                         kv.block_size, int(max_ctx)))
+        ws_bytes = plan.ws_bytes
+    else:
+        ws_bytes = _hip.lib().spv_verify_attn_workspace_bytes(B, chunk, hq, kv.num_kv_heads, d,
+                                                              kv.block_size, int(max_ctx))
+    stream = _hip.stream_of(kv.device)
+    ws = _workspace.get(ws_bytes, kv.device, stream) if ws_bytes else None
     args = (ptr(out), ptr(q), _hip.dtype_code(q.dtype), ptr(kv.k_pool), ptr(kv.v_pool),
             kv._dt, ptr(kv.scales), ptr(kv.tables_dev), kv.max_blocks_per_seq, ptr(sid_t), ptr(start_t),
             ptr(kv.lens_dev), ptr(kv.allocator.ctr), B, chunk,
             hq, kv.num_kv_heads, d, kv.block_size, int(layer), kv.allocator.capacity, int(max_ctx), scale)
     if plan is not None and plan.buf is not None:
-        call("spv_verify_attn_planned", *args, ptr(plan.buf), ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
+        call("spv_verify_attn_planned", *args, ptr(plan.buf), ptr(ws), int(ws_bytes), stream)
     else:
-        call("spv_verify_attn", *args, ptr(ws), int(ws_bytes), _hip.stream_of(kv.device))
+        call("spv_verify_attn", *args, ptr(ws), int(ws_bytes), stream)
     # A read of unwritten keys is flagged on the device and raised (IndexError)
     # at the next metadata query, without a synchronisation here.
     kv._stale = True
