@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     }
     return ovf;
   };
-  // The workgroup's largest finite |v| of the staged tile (vreg), every thread.
+  // The workgroup's largest finite |v| of the tile in stage S, every thread.
   __shared__ uint32_t s_vmax[kWaves];
   auto tile_vmax = [&](const Stage& S) {
     uint32_t m = 0;
