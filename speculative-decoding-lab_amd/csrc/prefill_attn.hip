@@ -36,7 +36,8 @@
 // scores with a per-column threshold and P = 2^(s scale log2(e) - m) is one
 // fma and one exp2 per score (scale > 0); masks only on diagonal tiles.
 // Workgroups take position blocks from the last (longest key range) to the
-// first, so the long blocks start first.
+// first, so the long blocks start first; with prompts of one length each XCD
+// takes whole (sequence, kv head) slices (see the kernel's dispatch).
 //
 // VALU path (fp32 / fp16 / other head dims): one workgroup per (sequence, q
 // head, 64 positions), key tiles of 16 in LDS, fp32 online softmax.
@@ -111,8 +112,49 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int i16 = lane & 15, g = lane >> 4;
-  const int hk = blockIdx.y, b = blockIdx.z;
-  const int blk = p.nblk - 1 - (int)blockIdx.x;  // longest key ranges first
+  // The workgroup's (sequence, kv head, position block). Workgroups are
+  // dispatched round-robin over the 8 XCDs (id mod 8) and, within an XCD, to
+  // its CUs as they free up. Default order: (sequence, kv head) slices one
+  // after another, each from its longest block down, so an XCD's concurrent
+  // workgroups read the same K/V tiles. When all prompts have one length and
+  // the slices divide or are divided by 8, each XCD takes whole slices (or
+  // every n-th block of one): its L2 then holds one slice (four equal prompts
+  // of 2,048 / 4,096 / 8,192 tokens: 110 / 380 / 1,303 against 170 / 480 /
+  // 1,349 us). With unequal prompts the XCDs' shares could not be both equal
+  // and of mixed lengths, and the default order was the fastest tried.
+  const int S = p.B * p.Hkv, nblk = p.nblk, id = (int)blockIdx.x;
+  __shared__ int s_equal;
+  if (threadIdx.x < 64) {
+    int lo = 0x7fffffff, hi = -1;
+    for (int bb = (int)threadIdx.x; bb < p.B; bb += 64) {
+      const int Lb = min(max(p.lengths[bb], 0), p.Lc);
+      lo = min(lo, Lb);
+      hi = max(hi, Lb);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      lo = min(lo, __shfl_xor(lo, o, 64));
+      hi = max(hi, __shfl_xor(hi, o, 64));
+    }
+    if (threadIdx.x == 0) s_equal = lo == hi;
+  }
+  __syncthreads();
+  int sl, d;  // slice and its block, longest first
+  if (s_equal && S % 8 == 0) {  // XCD x: slices x, x + 8, ...
+    const int j = id >> 3;
+    sl = (id & 7) + 8 * (j / nblk);
+    d = j % nblk;
+  } else if (s_equal && 8 % S == 0) {  // n = 8 / S XCDs per slice, every n-th block each
+    const int x = id & 7, n = 8 / S;
+    sl = x % S;
+    d = x / S + n * (id >> 3);
+  } else {
+    sl = id / nblk;
+    d = id % nblk;
+  }
+  if (sl >= S || d >= nblk) return;  // the grid is padded to whole rounds of 8
+  const int b = __builtin_amdgcn_readfirstlane(sl / p.Hkv), hk = __builtin_amdgcn_readfirstlane(sl % p.Hkv);
+  const int blk = __builtin_amdgcn_readfirstlane(nblk - 1 - d);
   const int p0 = blk * p.BM;
   const int L = min(max(p.lengths[b], 0), p.Lc);  // never a key beyond the chunk
   const int ratio = p.ratio, Hq = p.Hq, Hkv = p.Hkv, Lc = p.Lc;
@@ -545,7 +587,8 @@ void launch_prefill_mfma(PrefillParams p, hipStream_t s) {
   const int rows = kWaves * NT * 16;
   p.BM = rows / p.ratio;
   p.nblk = (p.Lc + p.BM - 1) / p.BM;
-  hipLaunchKernelGGL((prefill_mfma_kernel<NT, D>), dim3(p.nblk, p.Hkv, p.B), dim3(kThreads), 0, s, p);
+  const long long items = (long long)p.B * p.Hkv * p.nblk;
+  hipLaunchKernelGGL((prefill_mfma_kernel<NT, D>), dim3((unsigned)((items + 7) / 8 * 8)), dim3(kThreads), 0, s, p);
 }
 
 }  // namespace
@@ -582,8 +625,10 @@ int spv_prefill_attn(void* out, const void* q, const void* k, const void* v, int
   // it takes a positive finite scale; any other scale takes the VALU path.
   // Its K/V tiles are read through 32-bit buffer ranges: a sequence's keys
   // and kv heads must span less than 4 GiB.
+  // Its grid numbers the (sequence, kv head, position block) items in 32 bits.
   if (dtype == SPV_BF16 && (head_dim == 128 || head_dim == 64) && p.ratio <= 256 && scale > 0.f &&
-      p.scale_log2 < INFINITY && (long long)Lc * num_kv_heads * head_dim * 2 < (1LL << 32)) {
+      p.scale_log2 < INFINITY && (long long)Lc * num_kv_heads * head_dim * 2 < (1LL << 32) &&
+      (long long)B * num_kv_heads * Lc < (1LL << 31)) {
     if (head_dim == 128) launch_prefill_mfma<2, 128>(p, s);
     else launch_prefill_mfma<2, 64>(p, s);
     SPV_CHECK_LAUNCH();

@@ -109,6 +109,25 @@ def test_bf16_head_ratios(cuda, Hq, Hkv, d, lengths):
     _bf16_check(out, want, lengths)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,d,L,Lc", [
+    (4, 16, 2, 128, 700, 1000),   # 8 slices: one per XCD
+    (8, 16, 2, 128, 300, 300),    # 16 slices: two per XCD, no padding block
+    (2, 16, 2, 128, 1500, 1600),  # 4 slices: every second block of one on each XCD
+    (1, 14, 2, 64, 999, 1203),    # 2 slices: every fourth block
+    (3, 16, 2, 128, 640, 700),    # 6 slices: the default order
+])
+def test_equal_prompt_dispatch(cuda, B, Hq, Hkv, d, L, Lc):
+    # Equal lengths select the XCD-affine dispatch when the slices divide or
+    # are divided by 8; every (sequence, kv head, block) must be computed once,
+    # the padding blocks past L included.
+    lengths = [L] * B
+    q, k, v = _chunk(B, Lc, Hq, Hkv, d, lengths, seed=B * 1000 + L)
+    out = paged_attention_prefill_chunk(q.to(cuda), k.to(cuda), v.to(cuda), Hq, lengths)
+    _check_padding(out, lengths)
+    want = ref_attn.paged_attention_prefill_chunk(q.float(), k.float(), v.float(), Hq, lengths)
+    _bf16_check(out, want, lengths)
+
+
 @pytest.mark.parametrize("case", ["rising", "falling", "huge", "tiny", "zero_first"])
 @pytest.mark.parametrize("d", [128, 64])
 def test_bf16_value_magnitudes(cuda, case, d):
