@@ -100,33 +100,53 @@ __device__ __forceinline__ int stage_exponent(float mx) {
   return min(126, max(-126, 9 - e));
 }
 
+// v_max3_f32 on raw scores: MFMA results are not known to be canonical, so
+// fmaxf would first canonicalise every input (one more instruction per score).
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
 template <int NT, int D>
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams p) {
+  static_assert(NT == 2, "two query tiles per wave");
   constexpr int KS = D / 32;          // 32-dim k-steps of S^T
   constexpr int MT = D / 16;          // 16-dim tiles of O^T
   constexpr int KP = D + 8;           // bf16 pitch of a K row in LDS (16 bytes of padding)
   constexpr int VP = kBK + 8;         // bf16 pitch of a V^T row in LDS (16 bytes of padding)
   constexpr int kKElems = kBK * KP, kVElems = D * VP;
+  // K tiles in 2 slots (tile x in slot x & 1), V^T tiles in 3 (slot x % 3):
+  // the two wave groups read a tile one phase apart (see the walk below).
   __shared__ __align__(16) uint16_t sK[2][kKElems];
-  __shared__ __align__(16) uint16_t sV[2][kVElems];
+  __shared__ __align__(16) uint16_t sV[3][kVElems];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int i16 = lane & 15, g = lane >> 4;
+  // Wave groups: waves 0-3 (group 0) and 4-7 (group 1), one of each per SIMD.
+  const int grp = __builtin_amdgcn_readfirstlane(w >> 2);
+  const int gt = threadIdx.x & 255;  // thread index within the group
+
   // The workgroup's (sequence, kv head, position block). Workgroups are
   // dispatched round-robin over the 8 XCDs (id mod 8) and, within an XCD, to
-  // its CUs as they free up. Default order: (sequence, kv head) slices one
-  // after another, each from its longest block down, so an XCD's concurrent
-  // workgroups read the same K/V tiles. When all prompts have one length and
-  // the slices divide or are divided by 8, each XCD takes whole slices (or
-  // every n-th block of one): its L2 then holds one slice (four equal prompts
-  // of 2,048 / 4,096 / 8,192 tokens: 110 / 380 / 1,303 against 170 / 480 /
-  // 1,349 us). With unequal prompts the XCDs' shares could not be both equal
-  // and of mixed lengths, and the default order was the fastest tried.
+  // its CUs as they free up. With at most 64 sequences the blocks go in
+  // longest-processing-time order: by tile count, most first (ties by
+  // sequence, kv head, then block from the last), the blocks without rows
+  // last. The blocks with the most tiles bound the call and start at launch,
+  // and each later one takes the longest work left (bench chunk: 233-243 us
+  // in (sequence, kv head) slice order with the longest slice first, 271 us in
+  // index order with the longest blocks starting 60 us late). When all
+  // prompts have one length and the slices divide or are divided by 8, each
+  // XCD takes whole slices (or every n-th block of one): its L2 then holds one
+  // slice (four equal prompts of 2,048 / 4,096 / 8,192 tokens: 110 / 380 /
+  // 1,303 against 170 / 480 / 1,349 us in slice order). Otherwise: slice
+  // order, each slice from its longest block down.
   const int S = p.B * p.Hkv, nblk = p.nblk, id = (int)blockIdx.x;
-  __shared__ int s_equal;
+  __shared__ int s_equal, s_sl, s_d;
   if (threadIdx.x < 64) {
+    const int i = (int)threadIdx.x;
     int lo = 0x7fffffff, hi = -1;
-    for (int bb = (int)threadIdx.x; bb < p.B; bb += 64) {
+    for (int bb = i; bb < p.B; bb += 64) {
       const int Lb = min(max(p.lengths[bb], 0), p.Lc);
       lo = min(lo, Lb);
       hi = max(hi, Lb);
@@ -136,10 +156,62 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
       lo = min(lo, __shfl_xor(lo, o, 64));
       hi = max(hi, __shfl_xor(hi, o, 64));
     }
-    if (threadIdx.x == 0) s_equal = lo == hi;
+    if (i == 0) s_equal = lo == hi;
+    if (p.B <= 64) {
+      // Lane i: sequence i's blocks with rows (nb) and its last block's tile
+      // count (T). Block j < nb has ceil(min(L, BM (j + 1)) / 64) tiles, so
+      // the blocks with at least c <= T tiles are j >= 64 (c - 1) / BM.
+      const int BM = p.BM, Hkv = p.Hkv;
+      const int Li = i < p.B ? min(max(p.lengths[i], 0), p.Lc) : 0;
+      const int nb = (Li + BM - 1) / BM, T = (Li + 63) / 64;
+      auto wsum = [](int x) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+        return x;
+      };
+      auto excl = [&](int x) {  // exclusive prefix sum over the lanes
+        int v = x;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(v, o, 64);
+          if (i >= o) v += y;
+        }
+        return v - x;
+      };
+      auto first = [&](int c) { return 64 * (c - 1) / BM; };
+      auto atleast = [&](int c) { return Hkv * wsum(c <= T ? nb - first(c) : 0); };  // items with >= c tiles
+      if (i == 0) s_sl = S;  // past every item (the grid is padded to whole rounds of 8)
+      const int total = atleast(1);
+      if (id < total) {
+        // the tile count c of item id: the largest c with more than id items of >= c tiles
+        int c = 1, top = T;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) top = max(top, __shfl_xor(top, o, 64));
+        while (c < top) {
+          const int mid = (c + top + 1) >> 1;
+          if (atleast(mid) > id) c = mid;
+          else top = mid - 1;
+        }
+        const int r = id - atleast(c + 1);
+        const int last = c < T ? first(c + 1) - 1 : nb - 1;
+        const int n = c <= T ? max(0, last - first(c) + 1) : 0;
+        const int pre = excl(Hkv * n);
+        if (r >= pre && r < pre + Hkv * n) {
+          s_sl = i * Hkv + (r - pre) / n;
+          s_d = nblk - 1 - (last - (r - pre) % n);
+        }
+      } else {
+        const int r = id - total, ne = nblk - nb;  // the blocks without rows
+        const int pre = excl(Hkv * ne);
+        if (r >= pre && r < pre + Hkv * ne) {
+          s_sl = i * Hkv + (r - pre) / ne;
+          s_d = nblk - 1 - (nb + (r - pre) % ne);
+        }
+      }
+    }
   }
   __syncthreads();
-  int sl, d;  // slice and its block, longest first
+  int sl, d;  // slice and its block (d = 0: the last block)
   if (s_equal && S % 8 == 0) {  // XCD x: slices x, x + 8, ...
     const int j = id >> 3;
     sl = (id & 7) + 8 * (j / nblk);
@@ -148,6 +220,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     const int x = id & 7, n = 8 / S;
     sl = x % S;
     d = x / S + n * (id >> 3);
+  } else if (p.B <= 64) {
+    sl = s_sl;
+    d = s_d;
   } else {
     sl = id / nblk;
     d = id % nblk;
@@ -202,38 +277,41 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
                                     qb + (((size_t)b * Lc + cpos[nt]) * Hq + chead[nt]) * D + 32 * ks + 8 * g)
                               : make_uint4(0u, 0u, 0u, 0u);
 
-  // Staging: K tile as 16-byte chunks (key, 8 dims), row-major. V tile as
-  // (key pair, 8 dims) items written transposed, one 32-bit word (two keys)
-  // per dim; the 32 pairs of one 8-dim column go to 32 consecutive lanes, so a
-  // wave's word stores cover the 64 banks. In a V^T row, key
-  // k = 32 q + 16 h + 4 g + j sits at 32 q + 8 g + 4 h + j: the 16-byte read of
-  // lane group g returns keys 4 g .. + 3 of the 16-key parts 2 q and 2 q + 1,
-  // the k-slots of the P^T operand below.
-  constexpr int kKChunks = kBK * D / 8, kKPer = (kKChunks + kThreads - 1) / kThreads;
+
+  // Staging: each wave group stages half of a tile -- K as 16-byte chunks
+  // (key, 8 dims), row-major; V as (key pair, 8 dims) items written
+  // transposed, one 32-bit word (two keys) per dim; the 32 pairs of one 8-dim
+  // column go to 32 consecutive lanes, so a wave's word stores cover the 64
+  // banks. In a V^T row, key k = 32 q + 16 h + 4 g + j sits at
+  // 32 q + 8 g + 4 h + j: the 16-byte read of lane group g returns keys
+  // 4 g .. + 3 of the 16-key parts 2 q and 2 q + 1, the k-slots of the P^T
+  // operand below.
+  constexpr int kKChunks = kBK * D / 8, kKHalf = kKChunks / 2, kKPer = (kKHalf + 255) / 256;
   constexpr int kPairs = kBK / 2;
-  constexpr int kVItems = kPairs * D / 8, kVPer = (kVItems + kThreads - 1) / kThreads;
+  constexpr int kVItems = kPairs * D / 8, kVHalf = kVItems / 2, kVPer = (kVHalf + 255) / 256;
+  static_assert(kKHalf % 256 == 0, "whole K chunks per thread");
   struct Stage {
     uint4 k[kKPer], v[kVPer][2];
   };
   // Every load is unconditional: a tile's buffers end at key kend, so loads of
   // keys past it return zeros (V of keys beyond the range stays zero, never
-  // NaN), and a thread without a V item re-reads one.
+  // NaN), and a thread without a V item re-reads one of its group's.
   const uint16_t* kseq = kb + ((size_t)b * Lc * Hkv + hk) * D;
   const uint16_t* vseq = vb + ((size_t)b * Lc * Hkv + hk) * D;
   const uint32_t key_bytes = (uint32_t)(Hkv * D * 2);
-  auto load_tile = [&](Stage& S, int t) {
+  auto load_half = [&](Stage& S, int t) {
     const int t0 = t * kBK;
     const __amdgpu_buffer_rsrc_t rk = span_rsrc(kseq + (size_t)t0 * Hkv * D, (uint32_t)(kend - t0) * key_bytes);
     const __amdgpu_buffer_rsrc_t rv = span_rsrc(vseq + (size_t)t0 * Hkv * D, (uint32_t)(kend - t0) * key_bytes);
 #pragma unroll
     for (int i = 0; i < kKPer; ++i) {
-      const int c = threadIdx.x + i * kThreads;
+      const int c = grp * kKHalf + gt + i * 256;
       const int key = c / (D / 8), col = c % (D / 8);
       S.k[i] = __builtin_bit_cast(uint4, load_b128(rk, (uint32_t)key * key_bytes + 16u * col));
     }
 #pragma unroll
     for (int i = 0; i < kVPer; ++i) {
-      const int c = (threadIdx.x + i * kThreads) % kVItems;
+      const int c = grp * kVHalf + (gt + i * 256) % kVHalf;
       const int pair = c % kPairs, col = c / kPairs;
 #pragma unroll
       for (int e = 0; e < 2; ++e)
@@ -242,42 +320,37 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
   };
   float vs = 1.f, vlim = 65504.f;  // V staging factor 2^k, and the largest |v| it keeps in fp16
   int vk = 0;
-  auto store_tile = [&](Stage& S, int buf) -> bool {
+  // Stores the group's half of a tile into K slot ks and V^T slot vsl; true
+  // when a finite V value would pass fp16's range at the current factor.
+  auto store_half = [&](const Stage& S, int ks, int vsl) -> bool {
     bool ovf = false;
 #pragma unroll
     for (int i = 0; i < kKPer; ++i) {
-      const int c = threadIdx.x + i * kThreads;
-      if (c < kKChunks) {
-        const int key = c / (D / 8), col = c % (D / 8);
-        *reinterpret_cast<uint4*>(&sK[buf][key * KP + 8 * col]) = S.k[i];
-      }
+      const int c = grp * kKHalf + gt + i * 256;
+      const int key = c / (D / 8), col = c % (D / 8);
+      *reinterpret_cast<uint4*>(&sK[ks][key * KP + 8 * col]) = S.k[i];
     }
 #pragma unroll
     for (int i = 0; i < kVPer; ++i) {
-      const int c = threadIdx.x + i * kThreads;
-      if (c < kVItems) {
+      if (gt + i * 256 < kVHalf) {
+        const int c = grp * kVHalf + gt + i * 256;
         const int pair = c % kPairs, col = c / kPairs;
         const int k = 2 * pair;
         const int pos = 32 * (k >> 5) + 8 * ((k >> 2) & 3) + 4 * ((k >> 4) & 1) + (k & 3);
         const uint32_t a[4] = {S.v[i][0].x, S.v[i][0].y, S.v[i][0].z, S.v[i][0].w};
         const uint32_t bb[4] = {S.v[i][1].x, S.v[i][1].y, S.v[i][1].z, S.v[i][1].w};
-        u16x2_t mx = u16x2_t{0, 0};  // largest |v| bits, per half
+        float mx = 0.f;  // largest scaled |v| (NaN when a NaN decides it)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // dims 8 col + 2 e (low halves) and + 1 (high halves): keys k, k + 1
-          const float x0 = __uint_as_float(a[e] << 16), x1 = __uint_as_float(bb[e] << 16);
-          const float y0 = __uint_as_float(a[e] & 0xffff0000u), y1 = __uint_as_float(bb[e] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e) * VP + pos]) = pack2_f16(x0 * vs, x1 * vs);
-          *reinterpret_cast<uint32_t*>(&sV[buf][(8 * col + 2 * e + 1) * VP + pos]) = pack2_f16(y0 * vs, y1 * vs);
-          mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, a[e] & 0x7fff7fffu));
-          mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, bb[e] & 0x7fff7fffu));
+          const float x0 = __uint_as_float(a[e] << 16) * vs, x1 = __uint_as_float(bb[e] << 16) * vs;
+          const float y0 = __uint_as_float(a[e] & 0xffff0000u) * vs, y1 = __uint_as_float(bb[e] & 0xffff0000u) * vs;
+          *reinterpret_cast<uint32_t*>(&sV[vsl][(8 * col + 2 * e) * VP + pos]) = pack2_f16(x0, x1);
+          *reinterpret_cast<uint32_t*>(&sV[vsl][(8 * col + 2 * e + 1) * VP + pos]) = pack2_f16(y0, y1);
+          mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(y0), fabsf(y1))));
         }
-        const uint32_t mh = max((uint32_t)mx[0], (uint32_t)mx[1]);
-        if (mh < 0x7f80u) {
-          ovf |= __uint_as_float(mh << 16) > vlim;
-        } else {
-          // an inf or NaN among them: a finite value past the fp16 range
-          // decides (inf and NaN pass as they are)
+        if (!(mx <= 65504.f)) {
+          // an inf, a NaN or a value past fp16: a finite input past the range decides
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const uint32_t w4[2] = {a[e], bb[e]};
@@ -293,19 +366,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     }
     return ovf;
   };
-  // The workgroup's largest finite |v| of the tile in stage S, every thread.
+  // The workgroup's largest of the per-thread values m (bits of a
+  // non-negative float), every thread.
   __shared__ uint32_t s_vmax[kWaves];
-  auto tile_vmax = [&](const Stage& S) {
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < kVPer; ++i)
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        m = max_finite_abs2(S.v[i][e].x, m);
-        m = max_finite_abs2(S.v[i][e].y, m);
-        m = max_finite_abs2(S.v[i][e].z, m);
-        m = max_finite_abs2(S.v[i][e].w, m);
-      }
+  auto wg_max = [&](uint32_t m) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
     if (lane == 0) s_vmax[w] = m;
@@ -316,6 +380,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     __syncthreads();  // s_vmax is reused by the next call
     return __uint_as_float(mm << 16);
   };
+  auto stage_max = [&](const Stage& S) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        m = max_finite_abs2(S.v[i][e].x, m);
+        m = max_finite_abs2(S.v[i][e].y, m);
+        m = max_finite_abs2(S.v[i][e].z, m);
+        m = max_finite_abs2(S.v[i][e].w, m);
+      }
+    return m;
+  };
   auto set_scale = [&](int k) {
     vk = k;
     vs = ldexpf(1.f, k);
@@ -323,37 +400,34 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
   };
 
   f32x4_t o[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // m: reference maximum in log2 units; thr: the raw score above which a
   // column's m must grow (scores become log2 units as s * sl2, sl2 > 0).
   float m[NT], l[NT], thr[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    m[nt] = -INFINITY;
-    l[nt] = 0.f;
-    thr[nt] = -INFINITY;
-  }
   const float sl2 = p.scale_log2, inv_sl2 = 1.f / p.scale_log2;
+  f32x4_t sc[4][NT];      // raw S^T of the tile in the walk, four 16-key parts
+  uint32_t ph[2][NT][4];  // P of the last softmax in fp16, two 16-key parts per operand
+  const f16x2_t ones = f16x2_t{(_Float16)1.f, (_Float16)1.f};
 
-  // Two register stages: tile t + 1 is in one while tile t is computed and
-  // tile t + 2 loads into the other (past the last tile the loads re-read it).
-  Stage st0, st1;
-  load_tile(st0, 0);
-  set_scale(stage_exponent(tile_vmax(st0)));
-  store_tile(st0, 0);
-  load_tile(st1, min(1, ntiles - 1));
-  __syncthreads();
-  auto tile_step = [&](int t, Stage& X, Stage& Y) {
-    const int buf = t & 1;
-    load_tile(Y, min(t + 2, ntiles - 1));  // in flight while this tile is computed
-    const int t0 = t * kBK;
-    const uint16_t* K = sK[buf];
-    const uint16_t* Vt = sV[buf];
-    // raw S^T for the four 16-key parts of the tile
-    f32x4_t sc[4][NT];
+  // O^T += V^T P^T for the tile whose P is held, from V^T slot vsl.
+  auto pv = [&](int vsl) {
+    const uint16_t* Vt = sV[vsl];
+#pragma unroll
+    for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        // V^T row (dim 16 mt + i16): keys 4 g .. + 3 of parts 2 q2 and 2 q2 + 1
+        const f16x8_t va =
+            __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(&Vt[(16 * mt + i16) * VP + 32 * q2 + 8 * g]));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              va, __builtin_bit_cast(f16x8_t, make_uint4(ph[q2][nt][0], ph[q2][nt][1], ph[q2][nt][2], ph[q2][nt][3])),
+              o[mt][nt], 0, 0, 0);
+      }
+  };
+  // raw S^T = K Q^T of the tile in K slot ks
+  auto qk = [&](int ks_) {
+    const uint16_t* K = sK[ks_];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
@@ -368,6 +442,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
                                                                0, 0);
       }
     }
+  };
+  // Online softmax of tile t's scores into ph (O, l rescaled when a column's
+  // reference maximum grows).
+  auto softmax = [&](int t) {
+    const int t0 = t * kBK;
     if (t0 + kBK - 1 > p0) {  // the tile crosses the block's diagonal: causal mask
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -382,12 +461,15 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     bool grow = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      float a = fmaxf(fmaxf(sc[0][nt][0], sc[0][nt][1]), fmaxf(sc[0][nt][2], sc[0][nt][3]));
-#pragma unroll
-      for (int kt = 1; kt < 4; ++kt)
-        a = fmaxf(a, fmaxf(fmaxf(sc[kt][nt][0], sc[kt][nt][1]), fmaxf(sc[kt][nt][2], sc[kt][nt][3])));
-      mx[nt] = a;
-      grow |= a > thr[nt];
+      float a0 = max3_raw(sc[0][nt][0], sc[0][nt][1], sc[0][nt][2]);
+      float a1 = max3_raw(sc[0][nt][3], sc[1][nt][0], sc[1][nt][1]);
+      float a2 = max3_raw(sc[1][nt][2], sc[1][nt][3], sc[2][nt][0]);
+      float a3 = max3_raw(sc[2][nt][1], sc[2][nt][2], sc[2][nt][3]);
+      float a4 = max3_raw(sc[3][nt][0], sc[3][nt][1], sc[3][nt][2]);
+      a0 = max3_raw(a0, a1, a2);
+      a3 = max3_raw(a3, a4, sc[3][nt][3]);
+      mx[nt] = fmaxf(a0, a3);
+      grow |= mx[nt] > thr[nt];
     }
     if (__any(grow)) {
 #pragma unroll
@@ -403,63 +485,113 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
         thr[nt] = (m_new + kSlack) * inv_sl2;
       }
     }
-    // P = 2^(s sl2 - m) in fp16, two 16-key parts per operand; row sums take
-    // P itself.
-    float mu[NT];
+    // P = 2^(s sl2 - m) in fp16; the row sums take P as it enters P V.
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) mu[nt] = m[nt] == -INFINITY ? 0.f : m[nt];
+    for (int nt = 0; nt < NT; ++nt) {
+      const float mu = m[nt] == -INFINITY ? 0.f : m[nt];
 #pragma unroll
-    for (int q2 = 0; q2 < 2; ++q2) {
-      uint32_t ph[NT][4];
+      for (int kt = 0; kt < 4; ++kt) {
+        float e[4];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int kt = 2 * q2 + h;
-          float e[4];
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[kt][nt][jj], sl2, -mu[nt]));
-          l[nt] += (e[0] + e[1]) + (e[2] + e[3]);
-          ph[nt][2 * h] = pack2_f16(e[0], e[1]);
-          ph[nt][2 * h + 1] = pack2_f16(e[2], e[3]);
-        }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        // V^T row (dim 16 mt + i16): keys 4 g .. + 3 of parts 2 q2 and 2 q2 + 1
-        const f16x8_t va =
-            __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(&Vt[(16 * mt + i16) * VP + 32 * q2 + 8 * g]));
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              va, __builtin_bit_cast(f16x8_t, make_uint4(ph[nt][0], ph[nt][1], ph[nt][2], ph[nt][3])), o[mt][nt],
-              0, 0, 0);
+        for (int jj = 0; jj < 4; ++jj) e[jj] = __builtin_amdgcn_exp2f(fmaf(sc[kt][nt][jj], sl2, -mu));
+        const uint32_t p01 = pack2_f16(e[0], e[1]), p23 = pack2_f16(e[2], e[3]);
+        ph[kt >> 1][nt][2 * (kt & 1)] = p01;
+        ph[kt >> 1][nt][2 * (kt & 1) + 1] = p23;
+        l[nt] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, p01), ones, l[nt], false);
+        l[nt] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, p23), ones, l[nt], false);
       }
     }
-    bool ovf = false;
-    if (t + 1 < ntiles) ovf = store_tile(X, buf ^ 1);  // that buffer's readers finished before the last barrier
-    if (__syncthreads_or(ovf)) {
-      // Tile t + 1 holds a value past fp16 at this k: a smaller k from its
-      // largest value, O into the new units (a power of two: exact), the tile
-      // staged again. The old k's stores are overwritten before the barrier.
-      const int k = min(vk, stage_exponent(tile_vmax(X)));
-      const float f = ldexpf(1.f, k - vk);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) o[mt][nt] *= f;
-      set_scale(k);
-      store_tile(X, buf ^ 1);
-      __syncthreads();
-    }
   };
-  // Whole pairs in the loop, an odd last tile after it: no step of the loop
-  // is conditional, so the compiler's wait counts see the stages in order.
-  int t = 0;
-  for (; t + 2 <= ntiles; t += 2) {
-    tile_step(t, st1, st0);
-    tile_step(t + 1, st0, st1);
+
+  // The walk. Group 0 runs phases M(0), V(0), M(1), V(1), ... and group 1 the
+  // same one phase later, a workgroup barrier after every phase, so on each
+  // SIMD one wave's softmax overlaps the other's MFMAs:
+  //   M(t): O^T += V^T P^T of tile t - 1, then S^T of tile t   (MFMA)
+  //   V(t): softmax of tile t; stage half of tile t + 1 + grp   (VALU)
+  // Tile x is complete in LDS after group 1 staged its half in V(x - 2) and
+  // group 0 in V(x - 1), before group 0 reads its K in M(x); group 1 reads K_x
+  // one phase later and V_x in M(x + 1) up to three phases after that, hence
+  // two K slots and three V^T slots. Register stage t & 1 holds the group's
+  // half of tile t + 1 + grp at V(t) and then loads tile t + 3 + grp.
+  // The staging factor 2^k comes from tile 0's largest |v|; a later value past
+  // fp16 at that k sets ovf and the block runs again with k from the largest
+  // |v| of its whole key range, which no value can pass.
+  // A phase ends at a workgroup barrier that no instruction is scheduled across.
+  auto phase_end = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  Stage st0, st1;
+  bool ovf;
+  for (int attempt = 0;; ++attempt) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      m[nt] = -INFINITY;
+      l[nt] = 0.f;
+      thr[nt] = -INFINITY;
+    }
+    load_half(st0, 0);
+    if (grp == 1) load_half(st1, min(1, ntiles - 1));
+    if (attempt == 0) {
+      set_scale(stage_exponent(wg_max(stage_max(st0))));
+    } else {
+      // the largest finite |v| of keys 0 .. kend - 1
+      uint32_t mv = 0;
+      const __amdgpu_buffer_rsrc_t rv = span_rsrc(vseq, (uint32_t)kend * key_bytes);
+      for (int c = threadIdx.x; c < kend * (D / 8); c += kThreads) {
+        const uint4 x = __builtin_bit_cast(uint4, load_b128(rv, (uint32_t)(c / (D / 8)) * key_bytes + 16u * (c % (D / 8))));
+        mv = max_finite_abs2(x.x, mv);
+        mv = max_finite_abs2(x.y, mv);
+        mv = max_finite_abs2(x.z, mv);
+        mv = max_finite_abs2(x.w, mv);
+      }
+      set_scale(stage_exponent(wg_max(mv)));
+    }
+    ovf = store_half(st0, 0, 0);
+    if (grp == 1) ovf |= store_half(st1, 1, 1);
+    load_half(st0, min(1 + grp, ntiles - 1));
+    load_half(st1, min(2 + grp, ntiles - 1));
+    phase_end();
+    if (grp == 1) phase_end();  // group 1 starts one phase later
+    qk(0);                          // M(0)
+    phase_end();
+    int ksl = (1 + grp) & 1;  // K slot of the tile staged in V(t)
+    int vst = 1 + grp;        // V^T slot of that tile
+    int vrd = 0;              // V^T slot of tile t, read in M(t + 1)
+    auto step = [&](int t, Stage& X) {
+      softmax(t);  // V(t)
+      ovf |= store_half(X, ksl, vst);
+      load_half(X, min(t + 3 + grp, ntiles - 1));
+      phase_end();
+      pv(vrd);  // M(t + 1)
+      qk((t + 1) & 1);
+      phase_end();
+      ksl ^= 1;
+      vst = vst == 2 ? 0 : vst + 1;
+      vrd = vrd == 2 ? 0 : vrd + 1;
+    };
+    // Whole pairs of steps in the loop, one more after it: no step of the loop
+    // is conditional, so the compiler's wait counts see the stages in order.
+    int t = 0;
+    for (; t + 2 < ntiles; t += 2) {
+      step(t, st0);
+      step(t + 1, st1);
+    }
+    if (t + 1 < ntiles) {
+      step(t, st0);
+      ++t;
+    }
+    softmax(t);  // V(ntiles - 1)
+    phase_end();
+    pv(vrd);  // the last tile's P V
+    if (grp == 0) phase_end();  // group 1's extra barrier at the start
+    if (attempt == 1 || !__syncthreads_or(ovf)) break;
   }
-  if (t < ntiles) tile_step(t, st1, st0);
 
   // Row sums over the four lane groups, then the normalised rows.
 #pragma unroll

@@ -12,8 +12,12 @@ engine/attention.py:121-167) against the oracle.
   the padding is filled with NaN and must not reach any output;
 * V of any magnitude on the MFMA path, which stages V in fp16 times a power of
   two taken from the first key tile: tiles 10^6 apart (the later tile past
-  fp16 at the first tile's scale, so O is rescaled and the tile staged
-  again), values near 1e30 and near 1e-30, a first tile of zeros;
+  fp16 at the first tile's scale, so the block runs again with the power of
+  two of its whole key range), values near 1e30 and near 1e-30, a first tile
+  of zeros;
+* the workgroup orders: equal prompts (XCD-affine), unequal prompts (longest
+  processing time first, ties, empty prompts, 64 prompts) and more than 64
+  prompts (slice order), every block computed exactly once;
 * fp16 and fp32 inputs (VALU path);
 * the same keys attended by prefill and by paged verify attention from
   position 0 agree.
@@ -122,6 +126,25 @@ def test_equal_prompt_dispatch(cuda, B, Hq, Hkv, d, L, Lc):
     # the padding blocks past L included.
     lengths = [L] * B
     q, k, v = _chunk(B, Lc, Hq, Hkv, d, lengths, seed=B * 1000 + L)
+    out = paged_attention_prefill_chunk(q.to(cuda), k.to(cuda), v.to(cuda), Hq, lengths)
+    _check_padding(out, lengths)
+    want = ref_attn.paged_attention_prefill_chunk(q.float(), k.float(), v.float(), Hq, lengths)
+    _bf16_check(out, want, lengths)
+
+
+@pytest.mark.parametrize("Hq,Hkv,d,lengths,Lc", [
+    (16, 2, 128, [0, 1200, 64, 1200, 333], 1300),  # equal longest prompts (ties), an empty one
+    (12, 2, 128, [901, 17, 450, 1, 1023, 640, 77, 2, 300], 1024),  # ratio 6: 42 positions per block
+    (24, 8, 64, [513, 100, 1999], 2000),  # ratio 3: 85 positions per block
+    (8, 2, 128, [(37 * i) % 101 for i in range(64)], 100),  # 64 prompts (the most ordered by length)
+    (4, 1, 64, [(13 * i) % 41 for i in range(70)], 40),  # 70 prompts: slice order
+])
+def test_unequal_prompt_dispatch(cuda, Hq, Hkv, d, lengths, Lc):
+    # Unequal lengths (up to 64 prompts) take the longest-processing-time
+    # order computed in every workgroup; every (sequence, kv head, block) must
+    # be computed exactly once, the blocks without rows included.
+    B = len(lengths)
+    q, k, v = _chunk(B, Lc, Hq, Hkv, d, lengths, seed=B * 7 + Lc)
     out = paged_attention_prefill_chunk(q.to(cuda), k.to(cuda), v.to(cuda), Hq, lengths)
     _check_padding(out, lengths)
     want = ref_attn.paged_attention_prefill_chunk(q.float(), k.float(), v.float(), Hq, lengths)
