@@ -113,8 +113,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
   static_assert(NT == 2, "two query tiles per wave");
   constexpr int KS = D / 32;          // 32-dim k-steps of S^T
   constexpr int MT = D / 16;          // 16-dim tiles of O^T
-  constexpr int KP = D + 8;           // bf16 pitch of a K row in LDS (16 bytes of padding)
-  constexpr int VP = kBK + 8;         // bf16 pitch of a V^T row in LDS (16 bytes of padding)
+  // bf16 pitches of a K row and a V^T row in LDS, 32 bytes of padding each:
+  // with 16 bytes the LDS reported 17.4 M bank-conflict cycles per call at
+  // the bench chunk, with 32 none (the time moved by about 1%).
+  constexpr int KP = D + 16;
+  constexpr int VP = kBK + 16;
   constexpr int kKElems = kBK * KP, kVElems = D * VP;
   // K tiles in 2 slots (tile x in slot x & 1), V^T tiles in 3 (slot x % 3):
   // the two wave groups read a tile one phase apart (see the walk below).
