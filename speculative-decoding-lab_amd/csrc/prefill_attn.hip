@@ -12,11 +12,12 @@
 // of BM consecutive positions and every q head of one kv head -- rows (position
 // p, head k) in the order p * ratio + k, 16 rows per MFMA tile, NT tiles per
 // wave -- so every K/V tile staged in LDS serves all heads of the group. Key
-// tiles of 64 are double-buffered in LDS (K row-major, V transposed), one
-// barrier per tile, and arrive through two register stages: tile t + 2 is
-// loaded while tile t is computed and tile t + 1 waits in the other stage
-// (one stage: 299 against 282 us for the bench chunk). Per 16-key part of a
-// tile and query tile:
+// tiles of 64 in LDS (K row-major, V transposed). Waves 0-3 and 4-7 (one of
+// each per SIMD) run the same phases one phase apart, a barrier after each:
+// an MFMA phase (P V of the previous tile, S^T of this one) and a VALU phase
+// (the softmax, and staging half of a later tile through two register
+// stages), so on every SIMD one wave's softmax overlaps the other's MFMAs (see
+// the walk in the kernel). Per 16-key part of a tile and query tile:
 //   S^T = K Q^T    v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims (LDS),
 //                  B = Q^T fragments held in registers for the whole walk;
 //   O^T += V^T P^T one v_mfma_f32_16x16x32_f16 per pair of 16-key parts,
@@ -25,19 +26,19 @@
 //                  the bf16 output bar). V is staged as fp16 times 2^k, one
 //                  exponent k per workgroup chosen from the first key tile's
 //                  largest finite |v| (which lands in [2^8, 2^9)): every bf16
-//                  value in range is then exact in fp16. A later tile with a
-//                  value that would pass 65504 (128x the first tile's largest)
-//                  lowers k -- O is multiplied by the power of two, exactly --
-//                  and is staged again. Inf and NaN stay what they are.
+//                  value in range is then exact in fp16. A later value that
+//                  would pass 65504 (128x the first tile's largest) makes the
+//                  block run again with k from the largest |v| of its whole
+//                  key range. Inf and NaN stay what they are.
 // The accumulator layout of S^T is the operand layout of P^T (lane l: keys
 // 4 (l / 16) .. + 3 of query column l % 16), so the softmax moves no data.
 // Online softmax with a per-column reference maximum that scores may exceed by
 // kSlack (log2 units) before O is rescaled; the growth test compares raw
 // scores with a per-column threshold and P = 2^(s scale log2(e) - m) is one
 // fma and one exp2 per score (scale > 0); masks only on diagonal tiles.
-// Workgroups take position blocks from the last (longest key range) to the
-// first, so the long blocks start first; with prompts of one length each XCD
-// takes whole (sequence, kv head) slices (see the kernel's dispatch).
+// Workgroups take the blocks in longest-processing-time order (most tiles
+// first) computed from the lengths; with prompts of one length each XCD takes
+// whole (sequence, kv head) slices (see the kernel's dispatch).
 //
 // VALU path (fp32 / fp16 / other head dims): one workgroup per (sequence, q
 // head, 64 positions), key tiles of 16 in LDS, fp32 online softmax.
