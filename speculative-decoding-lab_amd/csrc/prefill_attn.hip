@@ -8,7 +8,7 @@
 // as zeros. Nothing beyond L_b is read into a result (padding may hold
 // anything, NaN included).
 //
-// MFMA path (bf16, head_dim 64 or 128): one workgroup of 8 waves takes a block
+// MFMA path (bf16 or fp16, head_dim 64 or 128): one workgroup of 8 waves takes a block
 // of BM consecutive positions and every q head of one kv head -- rows (position
 // p, head k) in the order p * ratio + k, 16 rows per MFMA tile, NT tiles per
 // wave -- so every K/V tile staged in LDS serves all heads of the group. Key
@@ -23,7 +23,8 @@
 //   O^T += V^T P^T one v_mfma_f32_16x16x32_f16 per pair of 16-key parts,
 //                  A = V^T (LDS, one 16-byte read: keys of both parts), B =
 //                  P in fp16 (11 significant bits; a bf16 P, 8 bits, missed
-//                  the bf16 output bar). V is staged as fp16 times 2^k, one
+//                  the bf16 output bar). fp16 inputs: S^T takes the f16 MFMA
+//                  and V is staged as it is. bf16: V is staged as fp16 times 2^k, one
 //                  exponent k per workgroup chosen from the first key tile's
 //                  largest finite |v| (which lands in [2^8, 2^9)): every bf16
 //                  value in range is then exact in fp16. A later value that
@@ -40,7 +41,7 @@
 // first) computed from the lengths; with prompts of one length each XCD takes
 // whole (sequence, kv head) slices (see the kernel's dispatch).
 //
-// VALU path (fp32 / fp16 / other head dims): one workgroup per (sequence, q
+// VALU path (fp32, other head dims): one workgroup per (sequence, q
 // head, 64 positions), key tiles of 16 in LDS, fp32 online softmax.
 #include <math.h>
 
@@ -109,8 +110,12 @@ __device__ __forceinline__ float max3_raw(float a, float b, float c) {
   return d;
 }
 
-template <int NT, int D>
+// IT: SPV_BF16 or SPV_F16 inputs and output. fp16 V needs no staging factor
+// (every value is already fp16), so that path has no scale and no second run.
+template <int NT, int D, int IT>
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams p) {
+  static_assert(IT == SPV_BF16 || IT == SPV_F16, "bf16 or fp16 inputs");
+  constexpr bool kF16 = IT == SPV_F16;
   static_assert(NT == 2, "two query tiles per wave");
   constexpr int KS = D / 32;          // 32-dim k-steps of S^T
   constexpr int MT = D / 16;          // 16-dim tiles of O^T
@@ -343,6 +348,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
         const int pos = 32 * (k >> 5) + 8 * ((k >> 2) & 3) + 4 * ((k >> 4) & 1) + (k & 3);
         const uint32_t a[4] = {S.v[i][0].x, S.v[i][0].y, S.v[i][0].z, S.v[i][0].w};
         const uint32_t bb[4] = {S.v[i][1].x, S.v[i][1].y, S.v[i][1].z, S.v[i][1].w};
+        if constexpr (kF16) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            // dims 8 col + 2 e (low halves) and + 1 (high halves): keys k, k + 1
+            *reinterpret_cast<uint32_t*>(&sV[vsl][(8 * col + 2 * e) * VP + pos]) = (a[e] & 0xffffu) | (bb[e] << 16);
+            *reinterpret_cast<uint32_t*>(&sV[vsl][(8 * col + 2 * e + 1) * VP + pos]) =
+                (a[e] >> 16) | (bb[e] & 0xffff0000u);
+          }
+          continue;
+        }
         float mx = 0.f;  // largest scaled |v| (NaN when a NaN decides it)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -441,9 +456,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
         const uint4 kf = *reinterpret_cast<const uint4*>(&K[(16 * kt + i16) * KP + 32 * ks + 8 * g]);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          sc[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf),
-                                                               __builtin_bit_cast(bf16x8_t, qf[nt][ks]), sc[kt][nt], 0,
-                                                               0, 0);
+          sc[kt][nt] = kF16 ? __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, kf),
+                                                                      __builtin_bit_cast(f16x8_t, qf[nt][ks]),
+                                                                      sc[kt][nt], 0, 0, 0)
+                            : __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                                       __builtin_bit_cast(bf16x8_t, qf[nt][ks]),
+                                                                       sc[kt][nt], 0, 0, 0);
       }
     }
   };
@@ -541,7 +559,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
     }
     load_half(st0, 0);
     if (grp == 1) load_half(st1, min(1, ntiles - 1));
-    if (attempt == 0) {
+    if (kF16) {
+      set_scale(0);
+    } else if (attempt == 0) {
       set_scale(stage_exponent(wg_max(stage_max(st0))));
     } else {
       // the largest finite |v| of keys 0 .. kend - 1
@@ -612,7 +632,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillParams
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const f32x4_t v = o[mt][nt] * inv;
-      *reinterpret_cast<uint2*>(orow + 16 * mt + 4 * g) = make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+      *reinterpret_cast<uint2*>(orow + 16 * mt + 4 * g) =
+          kF16 ? make_uint2(pack2_f16(v[0], v[1]), pack2_f16(v[2], v[3]))
+               : make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
     }
   }
 }
@@ -718,13 +740,13 @@ __global__ __launch_bounds__(kValuThreads) void prefill_valu_kernel(PrefillParam
   }
 }
 
-template <int NT, int D>
+template <int NT, int D, int IT>
 void launch_prefill_mfma(PrefillParams p, hipStream_t s) {
   const int rows = kWaves * NT * 16;
   p.BM = rows / p.ratio;
   p.nblk = (p.Lc + p.BM - 1) / p.BM;
   const long long items = (long long)p.B * p.Hkv * p.nblk;
-  hipLaunchKernelGGL((prefill_mfma_kernel<NT, D>), dim3((unsigned)((items + 7) / 8 * 8)), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<NT, D, IT>), dim3((unsigned)((items + 7) / 8 * 8)), dim3(kThreads), 0, s, p);
 }
 
 }  // namespace
@@ -762,11 +784,16 @@ int spv_prefill_attn(void* out, const void* q, const void* k, const void* v, int
   // Its K/V tiles are read through 32-bit buffer ranges: a sequence's keys
   // and kv heads must span less than 4 GiB.
   // Its grid numbers the (sequence, kv head, position block) items in 32 bits.
-  if (dtype == SPV_BF16 && (head_dim == 128 || head_dim == 64) && p.ratio <= 256 && scale > 0.f &&
+  if ((dtype == SPV_BF16 || dtype == SPV_F16) && (head_dim == 128 || head_dim == 64) && p.ratio <= 256 && scale > 0.f &&
       p.scale_log2 < INFINITY && (long long)Lc * num_kv_heads * head_dim * 2 < (1LL << 32) &&
       (long long)B * num_kv_heads * Lc < (1LL << 31)) {
-    if (head_dim == 128) launch_prefill_mfma<2, 128>(p, s);
-    else launch_prefill_mfma<2, 64>(p, s);
+    if (dtype == SPV_BF16) {
+      if (head_dim == 128) launch_prefill_mfma<2, 128, SPV_BF16>(p, s);
+      else launch_prefill_mfma<2, 64, SPV_BF16>(p, s);
+    } else {
+      if (head_dim == 128) launch_prefill_mfma<2, 128, SPV_F16>(p, s);
+      else launch_prefill_mfma<2, 64, SPV_F16>(p, s);
+    }
     SPV_CHECK_LAUNCH();
     return SPV_OK;
   }

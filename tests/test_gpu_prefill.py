@@ -18,7 +18,9 @@ engine/attention.py:121-167) against the oracle.
 * the workgroup orders: equal prompts (XCD-affine), unequal prompts (longest
   processing time first, ties, empty prompts, 64 prompts) and more than 64
   prompts (slice order), every block computed exactly once;
-* fp16 and fp32 inputs (VALU path);
+* fp16 inputs on the MFMA path (Qwen2.5-3B and 0.5B heads, GQA ratios 1-7, V
+  near the top of fp16's range and in its subnormals), fp16 and fp32 inputs on
+  the VALU path (other head dims);
 * the same keys attended by prefill and by paged verify attention from
   position 0 agree.
 """
@@ -174,7 +176,7 @@ def test_bf16_value_magnitudes(cuda, case, d):
     _bf16_check(out, want, lengths)
 
 
-@pytest.mark.parametrize("dtype,d", [(torch.float32, 128), (torch.float16, 64), (torch.float32, 40)])
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 128), (torch.float16, 40), (torch.float32, 40)])
 def test_valu_path_matches_oracle(cuda, dtype, d):
     Hq, Hkv, lengths = 6, 2, [150, 1, 77]
     B, Lc = len(lengths), 160
@@ -185,6 +187,61 @@ def test_valu_path_matches_oracle(cuda, dtype, d):
     tol = 1e-5 if dtype == torch.float32 else 2e-3
     for b, n in enumerate(lengths):
         assert torch.allclose(out[b, :n].float().cpu(), want[b, :n], atol=tol, rtol=tol), b
+
+
+def _f16_check(out, want, lengths):
+    out = out.double().cpu()
+    want = want.double()
+    for b, n in enumerate(lengths):
+        if n == 0:
+            continue
+        o, w = out[b, :n], want[b, :n]
+        scale = float(w.abs().max())
+        err = (o - w).abs()
+        rel = float(err.norm() / w.norm())
+        assert rel <= 1e-3, (b, rel)
+        assert bool((err <= 2.0 ** -10 * w.abs() + 1e-3 * scale).all()), (b, float(err.max()), scale)
+
+
+@pytest.mark.parametrize("Hq,Hkv,d,lengths", [
+    (16, 2, 128, [512, 2999, 1200, 0]),  # Qwen2.5-3B heads (the reference runs fp16 on the GPU)
+    (14, 2, 64, [1, 100, 1000, 777]),    # Qwen2.5-0.5B heads, ratio 7
+    (12, 2, 128, [300, 64, 65, 1]),      # ratio 6
+    (4, 4, 128, [257, 31]),              # ratio 1
+])
+def test_fp16_mfma_path(cuda, Hq, Hkv, d, lengths):
+    # fp16 inputs take the MFMA kernel: S^T with the f16 MFMA, V staged as it is
+    B, Lc = len(lengths), max(lengths) + 3
+    q, k, v = _chunk(B, Lc, Hq, Hkv, d, lengths, seed=Hq * 10 + d + 1, dtype=torch.float16)
+    out = paged_attention_prefill_chunk(q.to(cuda), k.to(cuda), v.to(cuda), Hq, lengths)
+    assert out.dtype == torch.float16
+    _check_padding(out, lengths)
+    want = ref_attn.paged_attention_prefill_chunk(q.float(), k.float(), v.float(), Hq, lengths)
+    _f16_check(out, want, lengths)
+
+
+@pytest.mark.parametrize("case", ["large", "subnormal", "mixed"])
+def test_fp16_value_magnitudes(cuda, case):
+    # fp16 V near the top of the range, in the subnormals, and both within one prompt
+    Hq, Hkv, d, lengths = 8, 2, 128, [400, 190]
+    B, Lc = len(lengths), max(lengths)
+    q, k, v = _chunk(B, Lc, Hq, Hkv, d, lengths, seed=11, dtype=torch.float16, nan_pad=False)
+    pos = torch.arange(Lc, dtype=torch.float32)[None, :, None, None]
+    if case == "large":
+        f = torch.full_like(pos, 1.5e4)
+    elif case == "subnormal":
+        f = torch.full_like(pos, 2e-6)
+    else:
+        f = torch.where(pos < 64, 2e-6, 1.5e4)
+    v = (v.float().clamp(-4, 4) * f).to(torch.float16)
+    out = paged_attention_prefill_chunk(q.to(cuda), k.to(cuda), v.to(cuda), Hq, lengths)
+    want = ref_attn.paged_attention_prefill_chunk(q.float(), k.float(), v.float(), Hq, lengths)
+    out = out.double().cpu()
+    for b, n in enumerate(lengths):
+        o, w = out[b, :n], want[b, :n].double()
+        scale = float(w.abs().max())
+        # the output's own fp16 rounding, with the subnormals' absolute spacing 2^-24
+        assert bool(((o - w).abs() <= 2.0 ** -10 * w.abs() + 1e-3 * scale + 2.0 ** -23).all()), (b, case)
 
 
 def test_device_lengths_are_clamped_to_the_chunk(cuda):
