@@ -286,9 +286,10 @@ size_t spv_verify_attn_workspace_bytes(int32_t B, int32_t C, int32_t num_q_heads
  * head h / (Hq/Hkv) (attention.py:32-38). q/out are (B, C, Hq, d) in q_dtype
  * (f32/bf16/f16); the pool holds kv_dtype. For SPV_FP8E4M3 pools kv_scales is
  * [layers][capacity][2] fp32 (K, V scale of each block). max_ctx must be >=
- * start_b + C for every b. bf16 queries over bf16 or fp8 pools with head_dim
- * 128 or 64, block_size 16 and B <= 2048 take the MFMA path (any (Hq/Hkv)*C);
- * everything else (including larger batches) the VALU path.
+ * start_b + C for every b. bf16 queries over bf16 or fp8 pools, and fp16
+ * queries over fp16 pools, with head_dim 128 or 64, block_size 16 and
+ * B <= 2048 take the MFMA path (any (Hq/Hkv)*C); everything else (including
+ * larger batches and mixed bf16 / fp16 operands) the VALU path.
  * seq_lens / ctr (the pool's, both may be NULL): a read the contract forbids
  * -- a table entry outside [0, capacity), start_b + C > seq_lens[seq_ids[b]]
  * (keys not written yet), start_b < 0 or start_b + C > max_ctx -- sets
@@ -312,8 +313,9 @@ int spv_verify_attn(void* out, const void* q, int q_dtype,
  * of each workgroup's first pages -- is computed here once, after the round's
  * blocks are allocated, into `plan` (spv_verify_attn_plan_bytes(B) bytes,
  * caller-owned). The sequence-length check of spv_verify_attn (ctr[7]) is made
- * here, once. Shapes off the MFMA path need no plan: the call then does
- * nothing. */
+ * here, once. The plan is made for the MFMA path's query type of kv_dtype
+ * (fp16 for fp16 pools, else bf16). Shapes off the MFMA path need no plan:
+ * the call then does nothing. */
 size_t spv_verify_attn_plan_bytes(int32_t B);
 int spv_verify_attn_plan(const int32_t* block_tables, int32_t max_blocks_per_seq,
                          const int32_t* seq_ids, const int32_t* start_pos,

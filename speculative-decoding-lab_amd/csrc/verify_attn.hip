@@ -38,6 +38,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
@@ -281,6 +282,16 @@ constexpr float kSlack = 8.f;
 // Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+// Two floats -> packed fp16 pair, round to nearest even.
+__device__ __forceinline__ uint32_t pack2_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
+// Four output values as one 8-byte store: bf16 or fp16 outputs.
+template <int QT>
+__device__ __forceinline__ uint2 pack4_out(float a, float b, float c, float d) {
+  if constexpr (QT == SPV_F16) return make_uint2(pack2_f16(a, b), pack2_f16(c, d));
+  else return make_uint2(pack2_bf16(a, b), pack2_bf16(c, d));
 }
 
 // Partials cross workgroups (and XCDs, whose L2s are not coherent with each
@@ -540,7 +551,7 @@ __device__ __forceinline__ void st64(int* a, long long v) {
 }
 
 // One page as a wave holds it: the K rows for S^T and the V^T tiles for O^T
-// (bf16, or fp8 e4m3 codes with the block's two scales).
+// (bf16 or fp16, or fp8 e4m3 codes with the block's two scales).
 template <int D, int KT>
 struct PageRegs;
 template <int D>
@@ -548,6 +559,8 @@ struct PageRegs<D, SPV_BF16> {
   uint4 k[D / 32];  // key i16, dims 32 ks + 8 g .. + 7
   uint2 v[D / 16];  // dim 16 mt + i16, keys 4 g .. 4 g + 3
 };
+template <int D>
+struct PageRegs<D, SPV_F16> : PageRegs<D, SPV_BF16> {};
 template <int D>
 struct PageRegs<D, SPV_FP8E4M3> {
   uint2 k[D / 32];     // key i16, dims 32 ks + 8 g .. + 7 (codes)
@@ -565,6 +578,8 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
 // The MFMA operands of a page: K rows as bf16x8, V^T columns as 4 bf16.
 template <int D>
 __device__ __forceinline__ uint4 k_frag(const PageRegs<D, SPV_BF16>& f, int ks) { return f.k[ks]; }
+template <int D>
+__device__ __forceinline__ uint4 k_frag(const PageRegs<D, SPV_F16>& f, int ks) { return f.k[ks]; }
 template <int D>
 __device__ __forceinline__ uint4 k_frag(const PageRegs<D, SPV_FP8E4M3>& f, int ks) {
   return make_uint4(fp8x2_to_bf16x2<false>(f.k[ks].x), fp8x2_to_bf16x2<true>(f.k[ks].x),
@@ -653,10 +668,10 @@ __device__ void merge_segment(const AttnParams& p, SlotOf slot_of, int ns, int b
     const float inv = 1.f / Ls[it];
     const int j = r / p.ratio, hq = h * p.ratio + (r - j * p.ratio);
     const size_t ob = (((size_t)b * p.C + j) * p.Hq + hq) * D + e0;
-    if constexpr (QT == SPV_BF16) {
-      // four bf16 in one 8-byte store (e0 is a multiple of 4)
+    if constexpr (QT == SPV_BF16 || QT == SPV_F16) {
+      // four 16-bit values in one 8-byte store (e0 is a multiple of 4)
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + ob) =
-          make_uint2(pack2_bf16(acc[it][0] * inv, acc[it][1] * inv), pack2_bf16(acc[it][2] * inv, acc[it][3] * inv));
+          pack4_out<QT>(acc[it][0] * inv, acc[it][1] * inv, acc[it][2] * inv, acc[it][3] * inv);
     } else {
 #pragma unroll
       for (int k = 0; k < 4; ++k) store_out<QT>(p, ob + k, acc[it][k] * inv);
@@ -677,6 +692,10 @@ __device__ __forceinline__ int xswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 template <int NT, int D, int QT, bool BAL, int KT, bool PL>
 __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p) {
   constexpr bool kFp8 = KT == SPV_FP8E4M3;
+  // fp16 pages take fp16 queries (S^T and P V on the fp16 MFMAs); bf16 and
+  // fp8 pages take bf16 queries.
+  constexpr bool kF16 = KT == SPV_F16;
+  static_assert(QT == (kF16 ? SPV_F16 : SPV_BF16), "query type follows the page type");
   // Block ids (and fp8 scales) of a window per lane, or per page from LDS
   // (see the page walk).
   constexpr bool kLaneIds = D == 64 || NT <= 2 || (NT == 3 && PL);
@@ -969,11 +988,13 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       // P vf stays in fp16's normal range; an all-zero block (sv = 0) has
       // P vf = 0. bf16 pages, and fp8 pages in the
       // head_dim-128 kernels with four query tiles (no register to spare),
-      // take P V in bf16 hi + lo.
-      constexpr bool h16 = kFp8 && !(NT == 4 && D == 128);
+      // take P V in bf16 hi + lo. fp16 pages take P V in fp16 with V^T as it
+      // is (vf = 1): P < 2^kSlack, and P in fp16 keeps 11 bits, the precision
+      // of the fp16 output.
+      constexpr bool h16 = (kFp8 && !(NT == 4 && D == 128)) || kF16;
       float vf = 1.f, vsc = 1.f;
       int vc = 0;
-      if constexpr (h16) {
+      if constexpr (h16 && kFp8) {
         const int a = min(max((int)((__builtin_bit_cast(uint32_t, sv) >> 23) & 255u) - 127, -15), 7);
         vsc = __builtin_bit_cast(float, (uint32_t)(a + 127) << 23);
         vf = sv * __builtin_bit_cast(float, (uint32_t)(127 - a) << 23);
@@ -1032,8 +1053,12 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
           uint4 qv;
           if constexpr (kLean) qv = qreg[ks][nt];
           else qv = *reinterpret_cast<const uint4*>(&sQ[(16 * nt + i16) * QSTR + 32 * ks + 8 * g]);
-          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k_frag<D>(f, ks)),
-                                                           __builtin_bit_cast(bf16x8_t, qv), sc[nt], 0, 0, 0);
+          if constexpr (kF16)
+            sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, k_frag<D>(f, ks)),
+                                                            __builtin_bit_cast(f16x8_t, qv), sc[nt], 0, 0, 0);
+          else
+            sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k_frag<D>(f, ks)),
+                                                             __builtin_bit_cast(bf16x8_t, qv), sc[nt], 0, 0, 0);
         }
       const bool need_mask = page * BS + BS - 1 > start;
       float x[NT][4];
@@ -1113,7 +1138,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
       // factor vf rides in the exponent, 2^(s - m + log2 vf), and the row sum
       // takes the tile's sum times 1 / vf (an all-zero block, vf = 0, instead
       // has its V operand zeroed and P unscaled).
-      constexpr bool kFold = kLean && h16;
+      constexpr bool kFold = kLean && h16 && kFp8;
       float lvf = 0.f, rvf = 1.f;
       if constexpr (kFold) {
         if (vscale != 0.f) {
@@ -1358,9 +1383,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void attn_mfma_kernel(AttnParams p
         const int e0 = 16 * (mt0 + ct[ci]) + 4 * cd4[ci];
         if (final_out) {
           const float cinv = sm_l[0][crow[ci]];
-          if constexpr (QT == SPV_BF16) {
+          if constexpr (QT == SPV_BF16 || QT == SPV_F16) {
             *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + cbase[ci] + e0) =
-                make_uint2(pack2_bf16(acc[0] * cinv, acc[1] * cinv), pack2_bf16(acc[2] * cinv, acc[3] * cinv));
+                pack4_out<QT>(acc[0] * cinv, acc[1] * cinv, acc[2] * cinv, acc[3] * cinv);
           } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) store_out<QT>(p, cbase[ci] + e0 + k, acc[k] * cinv);
@@ -1517,7 +1542,8 @@ Plan make_plan(int B, int C, int Hq, int Hkv, int d, int bs, int max_ctx, int kv
                       2LL * kMfmaWGsMax * G * d * (long long)sizeof(float) < (1LL << 31);
   // Any G: below 16 rows (decode, G = Hq / Hkv) the one query tile is padded
   // with zero rows; the pages still cross HBM once, which is what bounds it.
-  pl.mfma = (kv_dtype == SPV_BF16 || kv_dtype == SPV_FP8E4M3) && q_dtype == SPV_BF16 && bs == 16 &&
+  pl.mfma = (((kv_dtype == SPV_BF16 || kv_dtype == SPV_FP8E4M3) && q_dtype == SPV_BF16) ||
+             (kv_dtype == SPV_F16 && q_dtype == SPV_F16)) && bs == 16 &&
             (d == 128 || d == 64) && B <= kMfmaMaxB && fits32;
   const int max_pages = (max_ctx + bs - 1) / bs;
   pl.d128 = d == 128;
@@ -1615,12 +1641,13 @@ int launch_valu_q(const AttnParams& p, int kv_dtype, dim3 grid, hipStream_t s, b
 template <int D, bool BAL, int KT, bool PL>
 void launch_mfma_mode(const AttnParams& p, int nt, hipStream_t s, dim3 grid, size_t smem) {
   const dim3 blk(kMfmaThreads);
+  constexpr int QT = KT == SPV_F16 ? SPV_F16 : SPV_BF16;
   switch (nt) {
-    case 1: launch_attn(attn_mfma_kernel<1, D, SPV_BF16, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
-    case 2: launch_attn(attn_mfma_kernel<2, D, SPV_BF16, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
-    case 3: launch_attn(attn_mfma_kernel<3, D, SPV_BF16, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
+    case 1: launch_attn(attn_mfma_kernel<1, D, QT, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
+    case 2: launch_attn(attn_mfma_kernel<2, D, QT, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
+    case 3: launch_attn(attn_mfma_kernel<3, D, QT, BAL, KT, PL>, grid, blk, smem, s, true, true, p); break;
     default:  // four query tiles: planned only at head_dim 64 (Plan::plannable)
-      launch_attn(attn_mfma_kernel<4, D, SPV_BF16, BAL, KT, PL && D != 128>, grid, blk, smem, s, true, true, p);
+      launch_attn(attn_mfma_kernel<4, D, QT, BAL, KT, PL && D != 128>, grid, blk, smem, s, true, true, p);
       break;
   }
 }
@@ -1735,9 +1762,11 @@ int spv::verify_attn_impl(void* out, const void* q, int q_dtype, const void* k_p
   }
   hipStream_t s = (hipStream_t)stream;
   if (pl.mfma) {
-    const bool fp8 = kv_dtype == SPV_FP8E4M3;
-    if (head_dim == 128) fp8 ? launch_mfma<128, SPV_FP8E4M3>(p, pl.nt, s) : launch_mfma<128, SPV_BF16>(p, pl.nt, s);
-    else fp8 ? launch_mfma<64, SPV_FP8E4M3>(p, pl.nt, s) : launch_mfma<64, SPV_BF16>(p, pl.nt, s);
+    switch (kv_dtype) {
+      case SPV_FP8E4M3: head_dim == 128 ? launch_mfma<128, SPV_FP8E4M3>(p, pl.nt, s) : launch_mfma<64, SPV_FP8E4M3>(p, pl.nt, s); break;
+      case SPV_F16: head_dim == 128 ? launch_mfma<128, SPV_F16>(p, pl.nt, s) : launch_mfma<64, SPV_F16>(p, pl.nt, s); break;
+      default: head_dim == 128 ? launch_mfma<128, SPV_BF16>(p, pl.nt, s) : launch_mfma<64, SPV_BF16>(p, pl.nt, s); break;
+    }
     SPV_CHECK_LAUNCH();
     return SPV_OK;
   }
@@ -1801,8 +1830,10 @@ int spv_verify_attn_plan(const int32_t* block_tables, int32_t max_blocks_per_seq
       max_blocks_per_seq < (max_ctx + block_size - 1) / block_size || dtype_size(kv_dtype) == 0)
     return SPV_ERR_ARG;
   if (B == 0) return SPV_OK;
-  // Planned calls take bf16 queries; a shape off the MFMA path needs no plan.
-  const Plan pl = make_plan(B, C, num_q_heads, num_kv_heads, head_dim, block_size, max_ctx, kv_dtype, SPV_BF16);
+  // Planned calls take queries of the pool's 16-bit type (fp16 for fp16
+  // pools, else bf16); a shape off the MFMA path needs no plan.
+  const int q_dtype = kv_dtype == SPV_F16 ? SPV_F16 : SPV_BF16;
+  const Plan pl = make_plan(B, C, num_q_heads, num_kv_heads, head_dim, block_size, max_ctx, kv_dtype, q_dtype);
   if (!pl.plannable()) return SPV_OK;
   if (plan_bytes < plan_ints(B, persistent_wgs()) * sizeof(int32_t)) return SPV_ERR_WORKSPACE;
   AttnParams p{};

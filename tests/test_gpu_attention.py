@@ -9,6 +9,10 @@
   values. Tolerance (bf16 output): per sequence ||out - ref|| / ||ref|| <= 2e-3,
   plus every element within 1 bf16 ulp (2^-7 relative) + 2e-3 * max |ref| --
   the output itself is rounded to bf16 (up to 2^-9 relative);
+* fp16 pools and queries (the reference's GPU default) on the MFMA path: the
+  same shapes, the cost-balanced split, and fp16 V at the top of its range and
+  in its subnormals. Tolerance: per sequence relative L2 error <= 1e-3 and
+  every element within 2^-10 relative + 1e-3 * max |ref|;
 * size-independent properties: key positions beyond L full of NaN never reach
   the output; one context split and many splits agree.
 """
@@ -83,9 +87,10 @@ def test_decode_matches_oracle(cuda):
                               atol=1e-5, rtol=1e-5)
 
 
-def _dense_pool(cuda, lens, C, Hkv, d, bs, dtype, seed, cap=None, nan_fill=False, perm=True):
+def _dense_pool(cuda, lens, C, Hkv, d, bs, dtype, seed, cap=None, nan_fill=False, perm=True, vmul=None):
     """Pool holding K/V for positions 0..L+C-1 of each sequence, written through
-    write_block, with tables scattered over the pool."""
+    write_block, with tables scattered over the pool. ``vmul(n)``: factors
+    (n, 1, 1) of the n positions' values (before rounding to ``dtype``)."""
     g = torch.Generator().manual_seed(seed)
     need = [-(-(L + C) // bs) for L in lens]
     cap = cap or sum(need) + 8
@@ -100,7 +105,8 @@ def _dense_pool(cuda, lens, C, Hkv, d, bs, dtype, seed, cap=None, nan_fill=False
         pos += n
     gpu.load_state(tables, [0] * len(lens), ids[pos:])
     keys = [torch.randn(L + C, Hkv, d, generator=g).to(dtype) for L in lens]
-    values = [torch.randn(L + C, Hkv, d, generator=g).to(dtype) for L in lens]
+    values = [torch.randn(L + C, Hkv, d, generator=g) for L in lens]
+    values = [(v if vmul is None else v.clamp(-4, 4) * vmul(v.shape[0])).to(dtype) for v in values]
     for s, L in enumerate(lens):
         if L:
             gpu.write_block(0, [s], [0], keys[s][:L].unsqueeze(0).to(cuda),
@@ -169,6 +175,72 @@ def test_bf16_shapes(cuda, shape):
     out = paged_attention_extend(q.to(cuda), gpu, 0, list(range(len(lens))), lens, Hq)
     want = ref_attn.extend_attention_dense(q, keys, values, lens, Hq)
     _bf16_check(out, want)
+
+
+def _f16_check(out, want):
+    """fp16 tolerance: per sequence, relative L2 error <= 1e-3, and every element
+    within 2^-10 relative (two fp16 ulps) plus 1e-3 * max|ref|. The output is
+    rounded to fp16 (up to 2^-12 relative) and P enters P V as fp16."""
+    assert out.dtype == torch.float16
+    out = out.double().cpu()
+    want = want.double()
+    for b in range(out.shape[0]):
+        scale = float(want[b].abs().max())
+        err = (out[b] - want[b]).abs()
+        rel = float(err.norm() / want[b].norm())
+        assert rel <= 1e-3, (b, rel)
+        assert bool((err <= 2.0 ** -10 * want[b].abs() + 1e-3 * scale).all()), (b, float(err.max()), scale)
+
+
+@pytest.mark.parametrize("shape", [
+    # (B, C, Hq, Hkv, d): fp16 pools and queries (the reference's GPU default) on the MFMA path
+    (32, 6, 12, 2, 128),  # Qwen2.5-1.5B verify
+    (8, 7, 16, 2, 128),   # 3B-shaped: four query tiles
+    (8, 9, 14, 2, 64),    # 0.5B-shaped heads: four tiles at d = 64
+    (8, 3, 12, 2, 128),   # G = 18, two tiles with padding
+    (8, 1, 14, 2, 64),    # 0.5B-shaped draft decode: G = 7
+    (160, 6, 12, 2, 128),  # segments outnumber the workgroups: the cost-balanced split
+])
+def test_fp16_mfma_shapes(cuda, shape):
+    B, C, Hq, Hkv, d = shape
+    g = torch.Generator().manual_seed(sum(shape) + 5)
+    lens = ([0, 1, 15, 16, 17, 255, 300, 1000] if B == 8 else
+            torch.randint(16, 4097 if B == 32 else 1500, (B,), generator=g).tolist())
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.float16, seed=B + C, cap=65536)
+    q = torch.randn(B, C, Hq, d, generator=g).to(torch.float16)
+    out = paged_attention_extend(q.to(cuda), gpu, 0, list(range(B)), lens, Hq)
+    rows = list(range(B)) if B <= 32 else list(range(0, B, 9))
+    want = ref_attn.extend_attention_dense(q[rows], [keys[r] for r in rows], [values[r] for r in rows],
+                                           [lens[r] for r in rows], Hq)
+    _f16_check(out[rows], want)
+
+
+@pytest.mark.parametrize("case", ["large", "subnormal", "mixed"])
+def test_fp16_value_magnitudes(cuda, case):
+    """fp16 V near the top of fp16's range (|V| up to 6e4), in its subnormals
+    (|V| below 1e-5), and both within one sequence. Element-wise bound: two fp16
+    ulps relative, 1e-3 of the sequence's largest output, and two subnormal
+    spacings (2^-23) absolute, where the output itself is subnormal."""
+    def vmul(n):
+        pos = torch.arange(n, dtype=torch.float32)[:, None, None]
+        if case == "large":
+            return torch.full_like(pos, 1.5e4)
+        if case == "subnormal":
+            return torch.full_like(pos, 2e-6)
+        return torch.where(pos % 5 == 0, 2e-6, 1.5e4)
+    lens, C, Hq, Hkv, d = [400, 190, 3000], 6, 12, 2, 128
+    gpu, keys, values = _dense_pool(cuda, lens, C, Hkv, d, 16, torch.float16, seed=17, vmul=vmul)
+    q = torch.randn(len(lens), C, Hq, d, generator=torch.Generator().manual_seed(18)).to(torch.float16)
+    out = paged_attention_extend(q.to(cuda), gpu, 0, list(range(len(lens))), lens, Hq)
+    assert bool(torch.isfinite(out).all())
+    want = ref_attn.extend_attention_dense(q, keys, values, lens, Hq).double()
+    out = out.double().cpu()
+    for b in range(len(lens)):
+        err = (out[b] - want[b]).abs()
+        scale = float(want[b].abs().max())
+        # the output's own fp16 rounding, with the subnormals' absolute spacing 2^-24
+        assert bool((err <= 2.0 ** -10 * want[b].abs() + 1e-3 * scale + 2.0 ** -23).all()), \
+            (b, case, float(err.max()), scale)
 
 
 def test_bf16_draft_decode_batch(cuda):

@@ -7,7 +7,8 @@ planned outputs must equal unplanned ones bit for bit. Cases: the
 Qwen2.5-1.5B verify shape (equal pieces), a batch whose segments outnumber the
 workgroups (the cost-balanced split, several pieces per workgroup), head_dim 64
 with four query tiles, one-row draft decode, pieces longer than the 512-entry
-block-id window, fp8 pages, and one plan serving several layers. (The
+block-id window, fp8 pages, fp16 pages with fp16
+queries, and one plan serving several layers. (The
 head_dim-128 kernels with four query tiles do not use a plan; their case checks
 that a planned call of that shape still runs and matches.) The plan's
 once-per-round length check raises the reference's IndexError like the
@@ -100,6 +101,25 @@ def test_planned_fp8_pages(cuda):
     plan = VerifyPlan(gpu, sids, lens, C, Hq, max_ctx)
     assert torch.equal(verify_attention(q, gpu, 0, sids, lens, max_ctx, plan=plan),
                        verify_attention(q, gpu, 0, sids, lens, max_ctx))
+
+
+@pytest.mark.parametrize("d,C,Hq", [(128, 6, 12), (64, 9, 14)])
+def test_planned_fp16_pages(cuda, d, C, Hq):
+    # fp16 pools take fp16 queries on the MFMA path; their plan is made for them
+    from test_gpu_attention import _f16_check
+
+    lens = _lens(24, 1, 3000, seed=d)
+    gpu, keys, values = _dense_pool(cuda, lens, C, 2, d, 16, torch.float16, seed=d + 3)
+    q = torch.randn(len(lens), C, Hq, d, generator=torch.Generator().manual_seed(d)).to(torch.float16)
+    qd = q.to(cuda)
+    sids = list(range(len(lens)))
+    max_ctx = max(lens) + C
+    plan = VerifyPlan(gpu, sids, lens, C, Hq, max_ctx)
+    planned = verify_attention(qd, gpu, 0, sids, lens, max_ctx, plan=plan)
+    assert torch.equal(planned, verify_attention(qd, gpu, 0, sids, lens, max_ctx))
+    rows = list(range(0, len(lens), 4))
+    _f16_check(planned[rows], ref_attn.extend_attention_dense(q[rows], [keys[r] for r in rows],
+                                                              [values[r] for r in rows], [lens[r] for r in rows], Hq))
 
 
 def test_plan_reports_unwritten_keys(cuda):
