@@ -5,7 +5,10 @@ pool admit them, so admission has to wait. After every round the oracle replays 
 CPU in the same order: it admits the new sequences (prompt K/V write), writes
 the verify K/V of every layer, runs the reference's per-sequence attention, the
 rejection rule on the same logits and randomness, and the reference's commit
-rule. Attention must agree within the fp32 tolerance; accepted tokens,
+rule. Attention must agree within the fp32 tolerance (one case runs fp16
+pools and queries at Qwen2.5-1.5B heads, on the MFMA attention, at the fp16
+bar: per sequence relative L2 <= 1e-3, elements within 2^-10 relative +
+1e-3 max|ref|); accepted tokens,
 committed counts, finished flags, block tables, lengths and the free list must
 be identical.
 """
@@ -22,15 +25,21 @@ from oracle import kv_pool as ref
 from oracle import sampler as S
 from oracle.spec_step import SeqState, commit_round
 
+from test_gpu_attention import _f16_check
+
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("eos", [None, 5])
-def test_continuous_batching_matches_oracle(cuda, eos):
-    L, Hq, Hkv, d, bs, V, gamma, max_batch, cap = 2, 4, 2, 16, 4, 24, 3, 5, 32
-    model = SyntheticVerifyModel(L, Hq, Hkv, d, V, gamma, max_batch, cuda, torch.float32, seed=3,
+@pytest.mark.parametrize("eos,dtype", [(None, torch.float32), (5, torch.float32), (5, torch.float16)])
+def test_continuous_batching_matches_oracle(cuda, eos, dtype):
+    # fp16: the reference's GPU dtype, at Qwen2.5-1.5B heads (the MFMA attention)
+    if dtype == torch.float16:
+        L, Hq, Hkv, d, bs, V, gamma, max_batch, cap = 2, 12, 2, 128, 16, 24, 3, 5, 32
+    else:
+        L, Hq, Hkv, d, bs, V, gamma, max_batch, cap = 2, 4, 2, 16, 4, 24, 3, 5, 32
+    model = SyntheticVerifyModel(L, Hq, Hkv, d, V, gamma, max_batch, cuda, dtype, seed=3,
                                  draft_sigma=1.0, prompt_cap=48, n_sets=3)
-    gpu = PagedKVCache(L, Hkv, d, cap, bs, cuda, torch.float32)
+    gpu = PagedKVCache(L, Hkv, d, cap, bs, cuda, dtype)
     cpu = ref.PagedKVCache(L, Hkv, d, cap, bs)
     reqs = poisson_requests(14, 2.5, 3, 40, 2, 16, seed=5)
     by_sid = {r.sid: r for r in reqs}
@@ -45,7 +54,7 @@ def test_continuous_batching_matches_oracle(cuda, eos):
                 cpu.add_sequence(sid)
                 k, v = model.prompt_kv(r.prompt_len)
                 for layer in range(L):
-                    cpu.write_block(layer, [sid], [0], k.cpu(), v.cpu())
+                    cpu.write_block(layer, [sid], [0], k.float().cpu(), v.float().cpu())
                 mirror[sid] = SeqState(sid, r.prompt_len, r.max_new_tokens, [-1])
                 if r.arrive_step < info.step:
                     seen["waits"] += 1
@@ -53,9 +62,14 @@ def test_continuous_batching_matches_oracle(cuda, eos):
         assert info.starts == [cpu.seq_lengths[s] for s in info.sids]
         inp = info.inputs
         for layer in range(L):
-            cpu.write_block(layer, info.sids, info.starts, inp["k"][layer].cpu(), inp["v"][layer].cpu())
-            want = ref_attn.paged_attention_extend(inp["q"][layer].cpu(), cpu, layer, info.sids, info.starts, Hq)
-            torch.testing.assert_close(info.outputs[layer].cpu(), want, atol=1e-5, rtol=1e-5)
+            cpu.write_block(layer, info.sids, info.starts, inp["k"][layer].float().cpu(),
+                            inp["v"][layer].float().cpu())
+            want = ref_attn.paged_attention_extend(inp["q"][layer].float().cpu(), cpu, layer, info.sids,
+                                                   info.starts, Hq)
+            if dtype == torch.float16:
+                _f16_check(info.outputs[layer], want)
+            else:
+                torch.testing.assert_close(info.outputs[layer].cpu(), want, atol=1e-5, rtol=1e-5)
         acc = S.verify_from_logits(inp["target"].cpu(), inp["draft"].cpu(), inp["proposals"].cpu(),
                                    inp["u"].cpu(), inp["noise"].cpu(), 1.0)
         assert info.result.accepted_lists() == acc
