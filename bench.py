@@ -487,6 +487,62 @@ FD_BREAKDOWN_ROUNDS = 3       # rounds with events around every layer's append a
 DD_LAYERS, DD_HQ, DD_HKV, DD_D = 24, 14, 2, 64
 
 
+def fp16_verify(dev, seed=0, dtype=None):
+    """The headline verify attention over an fp16 pool with fp16 queries (the
+    reference's GPU dtype): the same replicas, context lengths and page
+    scatter, each sequence's keys written through position L + chunk, planned
+    calls cycling over the replicas as one captured graph. ``dtype``: the
+    pool's and the queries' type (fp16 unless given)."""
+    import torch
+
+    from engine.attention import VerifyPlan, verify_attention
+    from engine.kv import PagedKVCache
+
+    rlens = replica_lens(seed)
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(CAP, generator=g).tolist()
+    tables, pos = [], 0
+    for lens in rlens:
+        for L in lens:
+            n = -(-(L + C) // BS)
+            tables.append(perm[pos: pos + n])
+            pos += n
+    dtype = dtype or torch.float16
+    kv = PagedKVCache(1, HKV, D, CAP, BS, dev, dtype, max_seqs=B * REPLICAS,
+                      max_blocks_per_seq=-(-(4096 + C) // BS) + 1)
+    kv.load_state(tables, [0] * len(tables), perm[pos:])
+    gd = torch.Generator(device=dev).manual_seed(seed + 1000)
+    for r, lens in enumerate(rlens):
+        for s, L in enumerate(lens):
+            k = torch.randn(1, L + C, HKV, D, generator=gd, device=dev).to(dtype)
+            v = torch.randn(1, L + C, HKV, D, generator=gd, device=dev).to(dtype)
+            kv.write_block(0, [r * B + s], [0], k, v)
+    q = torch.randn(B, C, HQ, D, generator=gd, device=dev).to(dtype)
+    out = torch.empty_like(q)
+    sids = [torch.arange(r * B, (r + 1) * B, dtype=torch.int32, device=dev) for r in range(REPLICAS)]
+    starts = [torch.tensor(lens, dtype=torch.int32, device=dev) for lens in rlens]
+    max_ctx = [max(lens) + C for lens in rlens]
+    plans = [VerifyPlan(kv, sids[r], starts[r], C, HQ, max_ctx[r]) for r in range(REPLICAS)]
+
+    def call(r):
+        verify_attention(q, kv, 0, sids[r], starts[r], max_ctx[r], out=out, plan=plans[r])
+
+    for r in range(REPLICAS):
+        call(r)
+    torch.cuda.synchronize()
+    reps = 3 * REPLICAS
+    ga = graph_of(lambda: [call(i % REPLICAS) for i in range(reps)], 1, torch)
+    us = time_graph(ga, 5, torch) * 1000.0 / reps
+    nbytes = sum(attention_bytes(rlens[i % REPLICAS]) for i in range(reps)) / reps
+    del ga, kv
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"workload": "the verify attention above over an fp16 pool with fp16 queries (planned calls, "
+                        "captured graph)",
+            "attn_us": round(us, 2), "attn_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "attn_bytes_per_call": round(nbytes)}
+
+
 def pool_partition_ok(kv, cap):
     """The pool invariant after a run: the free list and the block tables
     together hold every block of the pool exactly once."""
@@ -855,7 +911,7 @@ def main() -> int:
     ap.add_argument("--full-depth-rounds", type=int, default=24,
                     help="rounds of the 36-layer continuous-batching measurement (0 skips it)")
     ap.add_argument("--no-long-context", action="store_true",
-                    help="skip the 32768-token fp8 / bf16 verify-attention measurement")
+                    help="skip the side measurements: fp16 verify attention, draft decode, prefill and the 32768-token fp8 / bf16 verify attention")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the library has no multi-GPU path "
@@ -988,6 +1044,8 @@ def main() -> int:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(w, dev)
     if not args.no_long_context:
+        print("bench: fp16 verify attention", file=sys.stderr, flush=True)
+        line["fp16_verify"] = fp16_verify(dev, args.seed)
         print("bench: draft decode", file=sys.stderr, flush=True)
         line["draft_decode"] = draft_decode(dev, args.seed)
         print("bench: prefill", file=sys.stderr, flush=True)
