@@ -8,6 +8,9 @@ block boundaries and random lengths mixed), then checks:
   at the bf16 bar of test_gpu_attention (per sequence relative L2 <= 2e-3 and
   every element within one bf16 ulp + 2e-3 max |ref|), and the planned call
   bit for bit against the unplanned one;
+* fp16 pools with fp16 queries: the same two checks at the fp16 bar (per
+  sequence relative L2 <= 1e-3, every element within 2^-10 relative + 1e-3
+  max |ref|), 8 cases of their own draws;
 * fp8 pools: the call against the oracle on the dequantised pool, same bar;
 * fp32 pools (the VALU path): against the oracle at atol = rtol = 1e-5.
 """
@@ -20,7 +23,7 @@ import torch
 
 from engine.attention import VerifyPlan, verify_attention
 from oracle import attention as ref_attn
-from test_gpu_attention import _bf16_check, _dense_pool
+from test_gpu_attention import _bf16_check, _dense_pool, _f16_check
 from test_gpu_fp8 import _fp8_pool_with
 
 pytestmark = pytest.mark.gpu
@@ -44,13 +47,12 @@ def _draw(seed):
     return d, hkv, hkv * ratio, C, [int(x) for x in lens]
 
 
-@pytest.mark.parametrize("seed", range(N_CASES))
-def test_bf16_random_shape(cuda, seed):
+def _planned_and_oracle(cuda, seed, dtype, check):
     d, hkv, hq, C, lens = _draw(seed)
     B = len(lens)
-    gpu, keys, values = _dense_pool(cuda, lens, C, hkv, d, 16, torch.bfloat16, seed=seed)
+    gpu, keys, values = _dense_pool(cuda, lens, C, hkv, d, 16, dtype, seed=seed)
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(B, C, hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    q = torch.randn(B, C, hq, d, generator=g).to(dtype).to(cuda)
     sids = list(range(B))
     max_ctx = max(lens) + C
     plain = verify_attention(q, gpu, 0, sids, lens, max_ctx)
@@ -61,7 +63,18 @@ def test_bf16_random_shape(cuda, seed):
     rows = list(range(0, B, max(1, B // 8)))
     want = ref_attn.extend_attention_dense(q[rows].float().cpu(), [keys[r] for r in rows],
                                            [values[r] for r in rows], [lens[r] for r in rows], hq)
-    _bf16_check(plain[rows], want)
+    check(plain[rows], want)
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_bf16_random_shape(cuda, seed):
+    _planned_and_oracle(cuda, seed, torch.bfloat16, _bf16_check)
+
+
+@pytest.mark.parametrize("seed", range(100, 100 + N_CASES, 2))
+def test_fp16_random_shape(cuda, seed):
+    # fp16 pools with fp16 queries (the MFMA path), other draws than the bf16 cases
+    _planned_and_oracle(cuda, seed, torch.float16, _f16_check)
 
 
 @pytest.mark.parametrize("seed", range(0, N_CASES, 2))
