@@ -200,6 +200,8 @@ def _f16_check(out, want):
     (8, 3, 12, 2, 128),   # G = 18, two tiles with padding
     (8, 1, 14, 2, 64),    # 0.5B-shaped draft decode: G = 7
     (160, 6, 12, 2, 128),  # segments outnumber the workgroups: the cost-balanced split
+    (160, 7, 16, 2, 128),  # the same with four query tiles (the full-depth 3B kernel)
+    (160, 9, 14, 2, 64),   # and at head_dim 64
 ])
 def test_fp16_mfma_shapes(cuda, shape):
     B, C, Hq, Hkv, d = shape
