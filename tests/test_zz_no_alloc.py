@@ -57,6 +57,8 @@ def _static_attention(q, kv, lens, max_ctx):
 @pytest.mark.parametrize("dtype,d,Hq,first,second", [
     # MFMA path: the Qwen2.5-1.5B-shaped verify batch, then a smaller one
     (torch.bfloat16, 128, 12, (32, 256, 4096), (8, 16, 900)),
+    # MFMA path over an fp16 pool with fp16 queries, head_dim 64
+    (torch.float16, 64, 14, (40, 256, 3000), (5, 16, 700)),
     # VALU path (fp32 pool), contexts split across workgroups
     (torch.float32, 64, 4, (6, 100, 1500), (3, 1, 300)),
 ])
