@@ -380,8 +380,10 @@ int spv_time_next_attention(void* start_event, void* stop_event);
  * row (clamped to [0, Lc]). Position j < lengths[b], q head h attends keys
  * 0 .. j of kv head h / (Hq/Hkv) with softmax(scale * q.k); positions >=
  * lengths[b] are written as zeros and none of them enters a result (the
- * padding may hold anything). bf16 with head_dim 64 or 128 takes the MFMA
- * path, other cases an fp32 VALU path. No workspace. */
+ * padding may hold anything). bf16 or f16 with head_dim 64 or 128, a finite
+ * positive scale and Hq/Hkv <= 256 take the MFMA path (within its 32-bit
+ * offsets: Lc*Hkv*d*2 < 2^32, B*Hkv*Lc < 2^31), other cases an fp32 VALU
+ * path. No workspace. */
 int spv_prefill_attn(void* out, const void* q, const void* k, const void* v,
                      int dtype, const int32_t* lengths, int32_t B, int32_t Lc,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
